@@ -1,0 +1,143 @@
+// l3m-mi355x: the C ABI of the MI355X (gfx950) backend for l3m's batch-1 decode hot path.
+//
+// Three layers of entry points, all extern "C" with plain pointers and sizes:
+//  1. the model API, with the reference's names, types and contracts (src/l3m.h:10-58), so a caller of
+//     libl3m.so (the CLI, python/l3m/__init__.py:31-50 via L3M_LIB) runs on the GPU unchanged;
+//  2. the kernel table (src/kernels.h:24-46): l3m_kernels_hip, a drop-in next to the scalar/avx2/avx512
+//     tables, taking the reference's host-side tile layout and prepared vector;
+//  3. device-level entry points on device pointers (the kernels the engine fuses), for tests and benches.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// ============================================================================== 1. model API (l3m.h)
+
+typedef struct l3m_model l3m_model;
+
+// Replaces l3m_opts (src/l3m.h:10-19). cpus/n_cpus are accepted and ignored (one GPU runs the model);
+// reference = 1 runs the same engine with every matrix widened to f32 and f32 activations (ref.c's math).
+typedef struct {
+    const int *cpus;
+    int        n_cpus;
+    int        ctx;        // KV cache length, 0 = min(model context, 512) (engine.c:22, 435)
+    int        reference;
+    int        force;
+    int        verbose;
+    int        cold;       // 1 = evict L2 and the Infinity Cache before each token (engine.c:330-338)
+} l3m_opts;
+
+// Replaces l3m_perf (src/l3m.h:21-29); counters the GPU path cannot read are NAN.
+typedef struct {
+    double tokens, ns_token, ns_compute, ns_wait, bytes_token, l2_bytes;
+    double l3_miss, dram_bytes, energy_j, llc_occupancy;
+} l3m_perf;
+
+l3m_model   *l3m_load(const char *path, const l3m_opts *opts);                         // src/l3m.h:32, engine.c:425
+void         l3m_free(l3m_model *m);                                                    // src/l3m.h:33, engine.c:533
+int          l3m_generate(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, // src/l3m.h:40, engine.c:549
+                          float temperature, uint64_t seed, int (*on_token)(int32_t tok, void *user), void *user);
+const float *l3m_logits(const l3m_model *m);                                            // src/l3m.h:42, engine.c:563
+int          l3m_vocab(const l3m_model *m);                                             // src/l3m.h:43
+int          l3m_ctx(const l3m_model *m);                                               // src/l3m.h:44
+const char  *l3m_describe(const l3m_model *m);                                          // src/l3m.h:45, engine.c:527
+int          l3m_encode(const l3m_model *m, const char *text, int add_bos, int32_t *out, int max);  // src/l3m.h:48
+const char  *l3m_decode(const l3m_model *m, int32_t tok, int *len);                     // src/l3m.h:49
+int          l3m_bos(const l3m_model *m);                                               // src/l3m.h:50
+int          l3m_eos(const l3m_model *m);                                               // src/l3m.h:51
+const char  *l3m_chatml(const l3m_model *m, int32_t *im_start);                         // src/l3m.h:53
+int          l3m_perf_read(l3m_model *m, l3m_perf *out);                                // src/l3m.h:55, engine.c:578
+int          l3m_parse_cpus(const char *list, int *cpus, int max);                      // src/l3m.h:57
+void         l3m_print_hw(FILE *out);                                                   // src/l3m.h:58
+
+// ============================================================================ 2. kernel table (kernels.h)
+
+enum { L3M_HIP_F32, L3M_HIP_BF16, L3M_HIP_Q8_0, L3M_HIP_Q4_0, L3M_HIP_MXFP4, L3M_HIP_NDTYPES };
+
+typedef struct {                 // src/kernels.h:24-30
+    const float    *f32;
+    const uint16_t *bf16;
+    const int8_t   *q8;
+    const float    *scale;
+    const int32_t  *sum;
+} l3m_vec;
+
+typedef void (*l3m_gemv_fn)(float *y, const void *tiles, int ntiles, int k, const l3m_vec *x);   // src/kernels.h:33
+
+typedef struct {                 // src/kernels.h:35-40
+    const char *name;
+    l3m_gemv_fn gemv[L3M_HIP_NDTYPES];
+    void (*attend)(float *out, const float *q, const uint16_t *k, const uint16_t *v, int pos, int head_dim, int stride);
+} l3m_kernels;
+
+extern const l3m_kernels l3m_kernels_hip;          // name "hip"; joins TABLES / best() (kernels.h:42, dispatch.c:15-21)
+int                l3m_kernels_usable(const l3m_kernels *k);   // src/kernels.h:46, dispatch.c:23-26
+const l3m_kernels *l3m_kernels_pick(void);                     // src/kernels.h:45, dispatch.c:28-36: NULL without a GPU
+const char        *l3m_hip_last_error(void);                   // the table's sticky error (its functions return void)
+
+// ============================================================== 3. device-level (pointers are device memory)
+
+typedef struct {
+    const uint8_t *q, *s;        // lane-tile quant and scale planes
+    int rows, tiles, nb, dtype;
+} l3m_dmat;
+
+int         l3m_dev_init(void);
+const char *l3m_dev_error(void);
+void        l3m_dev_clear_error(void);
+const char *l3m_dev_name(void);
+void       *l3m_dev_alloc(size_t bytes);
+void        l3m_dev_free(void *p);
+int         l3m_dev_upload(void *dst, const void *src, size_t bytes);
+int         l3m_dev_download(void *dst, const void *src, size_t bytes);
+int         l3m_dev_sync(void);
+void       *l3m_dev_stream(void);
+
+// Lane-tile layout sizes and host-side packing (the GPU analogue of l3m_tile_bytes / l3m_pack_tile,
+// src/kernels.h:49-50, pack.c:21-99).
+int    l3m_lt_qbytes(int dtype);
+int    l3m_lt_sbytes(int dtype);
+size_t l3m_lt_quant_size(int dtype, int rows, int k);
+size_t l3m_lt_scale_size(int dtype, int rows, int k);
+void   l3m_lt_pack_rows(int dtype, int rows, int k, const void *const *rows_src, uint8_t *quant, uint8_t *scale);
+void   l3m_lt_pack_ltiles(int dtype, int ntiles, int k, const void *tiles, uint8_t *quant, uint8_t *scale);
+
+size_t l3m_act_bytes(int dtype, int k);
+int    l3m_k_prep(int dtype, const float *x, int k, void *act, void *stream);             // l3m_vec_prepare, pack.c:101
+int    l3m_k_gemv(const l3m_dmat *m, const void *act, int k, float *y, void *stream);    // gemv[dtype], kernels_scalar.c
+int    l3m_k_attend(float *out, const float *q, const uint16_t *k, const uint16_t *v,    // l3m_attend, ops.c:58
+                    int pos, int hd, int stride, void *stream);
+int    l3m_k_rmsnorm(float *y, const float *x, const float *w, int n, float eps, void *stream);  // ops.c:13
+int    l3m_k_rope(float *v, int n_heads, int hd, int pos, const float *table, void *stream);      // ops.c:29
+int    l3m_k_silu_mul(float *h, const float *g, int n, void *stream);                            // ops.c:49
+int    l3m_k_argmax(const float *x, int n, int32_t *out, void *stream);                          // engine.c:290-301
+void   l3m_rope_table(float *table, int ctx, int hd, float theta);   // host: [ctx][hd/2] (cos, sin), ops.c:31-32
+
+// The engine's captured decode step, for benches: per-token time of the whole step on the device.
+double l3m_bench_decode(l3m_model *m, const int32_t *prompt, int n_prompt, int n_tokens);   // ns per token, <0 on error
+
+// Synthetic .l3m models (seeded, host-independent bytes).
+typedef struct {
+    const char *arch;
+    int      dim, n_layers, n_heads, n_kv_heads, ffn_dim, vocab, ctx;
+    float    rope_theta, norm_eps;
+    int      dtype, head_dtype, tied;
+    uint64_t seed;
+    float    std;
+    float    norm_jitter;
+    int      bos, eos;
+} l3m_gen_spec;
+int      l3m_gen_write(const l3m_gen_spec *spec, const char *path);
+void     l3m_gen_prompt(uint64_t seed, int vocab, int n, int32_t *out);
+uint64_t l3m_gen_u64(uint64_t stream, uint64_t i);
+float    l3m_gen_normal(uint64_t stream, uint64_t i);
+void     l3m_quantize_row(int dtype, void *dst, const float *x, int k);
+uint16_t l3m_f32_to_f16(float f);
+
+#ifdef __cplusplus
+}
+#endif
