@@ -62,6 +62,11 @@ int    l3m_k_argmax(const float *x, int n, int32_t *out, void *stream);
 // norm, the head, the argmax written to tokens[pos + 1]. Always advances pos.
 int l3m_step_enqueue(const l3m_dmodel *m, const l3m_dlayer *layers, int with_head, void *stream);
 
+// Timing (microseconds per launch, hipEvents on the library stream, after one untimed launch).
+double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);
+// kind: 0 qkv, 1 attention, 2 wo, 3 gate/up, 4 down, 5 head (which then does not advance the position)
+double l3m_time_step_kernel(const l3m_dmodel *m, const l3m_dlayer *layers, int kind, int layer, int iters);
+
 // Captured steps: graph 0 without the head (prompt), graph 1 with it.
 typedef struct l3m_graphs l3m_graphs;
 l3m_graphs *l3m_graphs_build(const l3m_dmodel *m, const l3m_dlayer *layers);

@@ -288,6 +288,7 @@ __device__ Smem carve(uint8_t *base, int dt, int k) {
     return s;
 }
 inline size_t smem_bytes(int dt, int k) { return align16(act_size(dt, k)) + 4 * (size_t)kpad(k) + 4 * (64 + 64 + 16); }
+constexpr size_t LDS_MAX = 65536;   // dynamic LDS per workgroup without opting in to more
 
 int pick_split(int nb) { return nb >= 16 ? 4 : nb >= 8 ? 2 : 1; }
 
@@ -514,7 +515,7 @@ __global__ void __launch_bounds__(NT) k_down(l3m_dmodel M, l3m_dlayer L, int S, 
 // workgroup reduces its rows; the last workgroup to finish reduces the partials in index order,
 // writes tokens[pos + 1], resets the counter and advances pos.
 template <int DT>
-__global__ void __launch_bounds__(NT) k_head(l3m_dmodel M, int S) {
+__global__ void __launch_bounds__(NT) k_head(l3m_dmodel M, int S, int advance) {
     extern __shared__ __align__(16) uint8_t smem[];
     Smem s = carve(smem, DT, M.dim);
     const int kp = kpad(M.dim), pos = *M.pos;
@@ -550,9 +551,11 @@ __global__ void __launch_bounds__(NT) k_head(l3m_dmodel M, int S) {
     }
     wg_argmax(v, idx, s.scr, s.iscr);
     if (threadIdx.x == 0) {
-        M.tokens[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
+        if (advance) {
+            M.tokens[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
+            *M.pos = pos + 1;
+        }
         *M.done = 0;
-        *M.pos = pos + 1;
     }
 }
 
@@ -617,9 +620,16 @@ template <int DT> void launch_down(const l3m_dmodel &M, const l3m_dlayer &L, int
     const int S = pick_split(L.down.nb), grid = (L.down.tiles + 4 / S - 1) / (4 / S);
     hipLaunchKernelGGL(k_down<DT>, dim3(grid), dim3(NT), smem_bytes(DT, M.ffn), st, M, L, S, advance);
 }
-template <int DT> void launch_head(const l3m_dmodel &M, hipStream_t st) {
+template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t st) {
     const int S = pick_split(M.head.nb), grid = (M.head.tiles + 4 / S - 1) / (4 / S);
-    hipLaunchKernelGGL(k_head<DT>, dim3(grid), dim3(NT), smem_bytes(DT, M.dim), st, M, S);
+    hipLaunchKernelGGL(k_head<DT>, dim3(grid), dim3(NT), smem_bytes(DT, M.dim), st, M, S, advance);
+}
+void launch_attend(const l3m_dmodel &M, int l, hipStream_t st) {
+    const size_t sm = 4 * ((size_t)M.hd + ((M.ctx + 4) & ~3) + NT + 8);
+    hipLaunchKernelGGL(k_attend, dim3(M.n_heads), dim3(NT), sm, st, M.attn, (const float *)M.q,
+                       (const uint16_t *)(M.kc + (size_t)l * M.n_kv * M.ctx * M.hd),
+                       (const uint16_t *)(M.vc + (size_t)l * M.n_kv * M.ctx * M.hd), 0, (const int *)M.pos, M.hd, M.hd,
+                       M.n_heads / M.n_kv, (size_t)M.ctx * M.hd);
 }
 
 }  // namespace
@@ -695,7 +705,7 @@ int l3m_dev_sync(void) {
 size_t l3m_act_bytes(int dtype, int k) { return act_size(dtype, k); }
 
 int l3m_k_prep(int dtype, const float *x, int k, void *act, void *stream) {
-    if (k < 1 || k > 16384) return fail_msg("prep: k out of range (1..16384)");
+    if (k < 1 || dtype < 0 || dtype >= L3M_NDTYPES || smem_bytes(dtype, k) > LDS_MAX) return fail_msg("prep: k out of range for this dtype");
     hipStream_t st = as_stream(stream);
     DISPATCH(dtype, launch_prep, x, k, act, st);
     CKL("k_prep");
@@ -703,7 +713,9 @@ int l3m_k_prep(int dtype, const float *x, int k, void *act, void *stream) {
 }
 
 int l3m_k_gemv(const l3m_dmat *m, const void *act, int k, float *y, void *stream) {
-    if (k < 1 || k > 16384 || kpad(k) / 32 != m->nb || m->tiles != (m->rows + 15) / 16) return fail_msg("gemv: shape does not match the matrix");
+    if (k < 1 || m->dtype < 0 || m->dtype >= L3M_NDTYPES || kpad(k) / 32 != m->nb || m->tiles != (m->rows + 15) / 16 || m->rows < 1)
+        return fail_msg("gemv: shape does not match the matrix");
+    if (smem_bytes(m->dtype, k) > LDS_MAX) return fail_msg("gemv: k too large for this dtype");
     hipStream_t st = as_stream(stream);
     const int S = pick_split(m->nb);
     DISPATCH(m->dtype, launch_gemv, *m, act, k, y, S, st);
@@ -714,13 +726,14 @@ int l3m_k_gemv(const l3m_dmat *m, const void *act, int k, float *y, void *stream
 int l3m_k_attend(float *out, const float *q, const uint16_t *k, const uint16_t *v, int pos, int hd, int stride, void *stream) {
     if (pos < 0 || hd < 8 || hd % 8 || hd > NT || stride < hd || stride % 8) return fail_msg("attend: bad shape");
     const size_t sm = 4 * ((size_t)hd + ((pos + 4) & ~3) + NT + 8);
+    if (sm > LDS_MAX) return fail_msg("attend: pos too large");
     hipLaunchKernelGGL(k_attend, dim3(1), dim3(NT), sm, as_stream(stream), out, q, k, v, pos, (const int *)nullptr, hd, stride, 1, (size_t)0);
     CKL("k_attend");
     return 0;
 }
 
 int l3m_k_rmsnorm(float *y, const float *x, const float *w, int n, float eps, void *stream) {
-    if (n < 1 || n > 16384) return fail_msg("rmsnorm: n out of range");
+    if (n < 1 || 4 * ((size_t)kpad(n) + 8) > LDS_MAX) return fail_msg("rmsnorm: n out of range");
     hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(NT), 4 * ((size_t)kpad(n) + 8), as_stream(stream), y, x, w, n, eps);
     CKL("k_rmsnorm");
     return 0;
@@ -752,16 +765,12 @@ int l3m_step_enqueue(const l3m_dmodel *M, const l3m_dlayer *layers, int with_hea
     for (int l = 0; l < M->n_layers; l++) {
         const l3m_dlayer &L = layers[l];
         DISPATCH(dt, launch_qkv, *M, L, l, st);
-        const size_t sm = 4 * ((size_t)M->hd + ((M->ctx + 4) & ~3) + NT + 8);
-        hipLaunchKernelGGL(k_attend, dim3(M->n_heads), dim3(NT), sm, st, M->attn, (const float *)M->q,
-                           (const uint16_t *)(M->kc + (size_t)l * M->n_kv * M->ctx * M->hd),
-                           (const uint16_t *)(M->vc + (size_t)l * M->n_kv * M->ctx * M->hd), 0, (const int *)M->pos, M->hd, M->hd,
-                           M->n_heads / M->n_kv, (size_t)M->ctx * M->hd);
+        launch_attend(*M, l, st);
         DISPATCH(dt, launch_wo, *M, L, st);
         DISPATCH(dt, launch_ffn, *M, L, st);
         DISPATCH(dt, launch_down, *M, L, !with_head && l == M->n_layers - 1, st);
     }
-    if (with_head) DISPATCH(M->head.dtype, launch_head, *M, st);
+    if (with_head) DISPATCH(M->head.dtype, launch_head, *M, 1, st);
     CKL("decode step");
     return 0;
 }
@@ -784,6 +793,62 @@ bad:
 int l3m_graphs_launch(l3m_graphs *g, int with_head, void *stream) {
     CK(hipGraphLaunch(g->e[with_head ? 1 : 0], as_stream(stream)));
     return 0;
+}
+
+// Average microseconds per launch over `iters` launches, timed with events on the library stream.
+static double time_launches(int iters, int (*launch)(void *ctx, int i), void *ctx) {
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { fail_msg("hipEventCreate"); return -1; }
+    double us = -1;
+    int rc = launch(ctx, 0);                                   // untimed first launch
+    if (!rc && hipEventRecord(a, g_stream) == hipSuccess) {
+        for (int i = 0; i < iters && !rc; i++) rc = launch(ctx, i);
+        float ms = 0;
+        if (!rc && hipEventRecord(b, g_stream) == hipSuccess && hipEventSynchronize(b) == hipSuccess &&
+            hipEventElapsedTime(&ms, a, b) == hipSuccess)
+            us = 1e3 * ms / iters;
+    }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return rc ? -1 : us;
+}
+
+struct GemvCtx { const l3m_dmat *mats; int n; const void *act; int k; float *y; };
+static int gemv_one(void *c, int i) {
+    GemvCtx *g = (GemvCtx *)c;
+    return l3m_k_gemv(&g->mats[i % g->n], g->act, g->k, g->y, g_stream);
+}
+
+double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters) {
+    if (l3m_dev_init() || n_mats < 1 || iters < 1) return -1;
+    GemvCtx c{mats, n_mats, act, k, y};
+    return time_launches(iters, gemv_one, &c);
+}
+
+struct StepCtx { const l3m_dmodel *M; const l3m_dlayer *L; int kind, layer; };
+static int step_one(void *c, int) {
+    StepCtx *s = (StepCtx *)c;
+    const l3m_dmodel &M = *s->M;
+    const l3m_dlayer &L = s->L[s->layer];
+    const int dt = L.qkv.dtype;
+    hipStream_t st = g_stream;
+    switch (s->kind) {
+    case 0: DISPATCH(dt, launch_qkv, M, L, s->layer, st); break;
+    case 1: launch_attend(M, s->layer, st); break;
+    case 2: DISPATCH(dt, launch_wo, M, L, st); break;
+    case 3: DISPATCH(dt, launch_ffn, M, L, st); break;
+    case 4: DISPATCH(dt, launch_down, M, L, 0, st); break;
+    case 5: DISPATCH(M.head.dtype, launch_head, M, 0, st); break;
+    default: return fail_msg("bad kernel kind");
+    }
+    CKL("timed kernel");
+    return 0;
+}
+
+double l3m_time_step_kernel(const l3m_dmodel *M, const l3m_dlayer *layers, int kind, int layer, int iters) {
+    if (l3m_dev_init() || layer < 0 || layer >= M->n_layers || iters < 1) return -1;
+    StepCtx c{M, layers, kind, layer};
+    return time_launches(iters, step_one, &c);
 }
 
 void l3m_graphs_free(l3m_graphs *g) {

@@ -1,0 +1,188 @@
+"""Parity of each device kernel, called through the C ABI, against the CPU oracle on the same seeded inputs.
+
+Bars: bit-exact activation quantization and block unpacking; matvec within 1e-3 relative
+(bf16, q8_0, f32) or 5e-3 (q4_0, mxfp4) of the oracle, relative to max|y|; attention within 1e-5 absolute of
+the oracle (the reference's own bar vs double, tests/test_kernels.c:145).
+"""
+import numpy as np
+import pytest
+
+from weights import BF16, F32, MXFP4, Q4_0, Q8_0, SHAPES, extremes, rel_err, rows
+
+pytestmark = pytest.mark.gpu
+TOL = {F32: 1e-3, BF16: 1e-3, Q8_0: 1e-3, Q4_0: 5e-3, MXFP4: 5e-3}
+NAMES = {F32: "f32", BF16: "bf16", Q8_0: "q8_0", Q4_0: "q4_0", MXFP4: "mxfp4"}
+
+
+def split_act(raw, k):
+    kp = (k + 31) // 32 * 32
+    nb = kp // 32
+    return raw[:k].view(np.int8), raw[kp:kp + 4 * nb].view(np.float32), raw[kp + 4 * nb:kp + 8 * nb].view(np.int32)
+
+
+@pytest.mark.parametrize("k", [32, 288, 768, 1376, 2048, 4096])
+def test_prep_quantized_bit_exact(dev, oracle, k):
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal(k).astype(np.float32) * 3
+    x[:32] = 0                                        # an all-zero block: scale 0, inv 0
+    if k > 64:
+        x[40] = 1e-30                                 # tiny values around a large one
+        x[64:96] = np.float32(0.5) * np.arange(32) - 8   # exact .5 products: rint ties to even
+    q8, scale, s = split_act(dev.prep(Q8_0, x), k)
+    want = oracle.prepare(Q8_0, x)
+    assert np.array_equal(q8, want["q8"])
+    assert np.array_equal(scale.view(np.uint32), want["scale"].view(np.uint32))
+    assert np.array_equal(s, want["sum"])
+
+
+@pytest.mark.parametrize("k", [2, 18, 288, 4096])
+def test_prep_bf16_bit_exact(dev, oracle, k):
+    x = np.random.default_rng(k).standard_normal(k).astype(np.float32)
+    raw = dev.prep(BF16, x)
+    assert np.array_equal(raw[: 2 * k].view(np.uint16), oracle.prepare(BF16, x)["bf16"])
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, Q8_0, Q4_0, MXFP4], ids=NAMES.get)
+@pytest.mark.parametrize("shape", SHAPES[:3], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_small_shapes(dev, oracle, dtype, shape):
+    n, k = shape
+    w = rows(dtype, n, k, seed=n + k + dtype)
+    x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
+    y = dev.gemv(dev.matrix(dtype, w, k), x)
+    want = oracle.gemv(dtype, w, n, k, x)
+    assert rel_err(y, want) < TOL[dtype], rel_err(y, want)
+    dev.free_all()
+
+
+@pytest.mark.parametrize("dtype", [BF16, Q8_0, Q4_0, MXFP4], ids=NAMES.get)
+@pytest.mark.parametrize("shape", SHAPES[3:], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_large_shapes(dev, oracle, dtype, shape):
+    n, k = shape
+    w = rows(dtype, n, k, seed=7)
+    x = np.random.default_rng(2).standard_normal(k).astype(np.float32)
+    y = dev.gemv(dev.matrix(dtype, w, k), x)
+    want = oracle.gemv(dtype, w, n, k, x)
+    assert rel_err(y, want) < TOL[dtype], rel_err(y, want)
+    dev.free_all()
+
+
+@pytest.mark.parametrize("dtype", [Q8_0, Q4_0, MXFP4], ids=NAMES.get)
+@pytest.mark.parametrize("k", [288, 1376, 3072])
+def test_gemv_edges(dev, oracle, dtype, k):
+    """q8 weight -128, subnormal mxfp4 scales, a zero activation block, zero (missing) rows."""
+    n = 48
+    w = extremes(dtype, rows(dtype, n, k, seed=k), k)
+    w_list = [w[i] if i < n - 5 else None for i in range(n)]
+    x = np.random.default_rng(3).standard_normal(k).astype(np.float32) * 4
+    x[:32] = 0
+    y = dev.gemv(dev.matrix(dtype, w_list, k), x)
+    w0 = w.copy()
+    w0[n - 5:] = 0
+    want = oracle.gemv(dtype, w0, n, k, x)
+    want[n - 5:] = 0
+    assert np.all(y[n - 5:] == 0)
+    assert rel_err(y, want) < TOL[dtype], rel_err(y, want)
+    dev.free_all()
+
+
+@pytest.mark.parametrize("dtype,k", [(F32, 2), (F32, 18), (F32, 34), (BF16, 2), (BF16, 18), (BF16, 34)])
+def test_gemv_ragged_k(dev, oracle, dtype, k):
+    n = 33
+    w = rows(dtype, n, k, seed=k)
+    x = np.random.default_rng(4).standard_normal(k).astype(np.float32)
+    y = dev.gemv(dev.matrix(dtype, w, k), x)
+    assert rel_err(y, oracle.gemv(dtype, w, n, k, x)) < TOL[dtype]
+    dev.free_all()
+
+
+@pytest.mark.parametrize("hd", [16, 32, 40, 48, 64])
+@pytest.mark.parametrize("pos", [0, 1, 37, 255])
+def test_attend(dev, oracle, hd, pos):
+    rng = np.random.default_rng(hd * 1000 + pos)
+    stride = 3 * hd
+    q = (rng.standard_normal(hd) * 2).astype(np.float32)
+    k = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBFFF   # bf16 with |v| < 2
+    v = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBFFF
+    got = dev.attend(q, k, v, pos, hd, stride)
+    want = oracle.attend(q, k, v, pos, hd, stride)
+    assert np.abs(got - want).max() <= 1e-5
+    dev.free_all()
+
+
+def test_attend_large_scores(dev, oracle):
+    """qscale 40 pushes scores far past exp's range (tests/test_kernels.c:197)."""
+    rng = np.random.default_rng(40)
+    hd, pos, stride = 64, 255, 192
+    q = (rng.uniform(-1, 1, hd) * 40).astype(np.float32)
+    k = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBF7F
+    v = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBF7F
+    assert np.abs(dev.attend(q, k, v, pos, hd, stride) - oracle.attend(q, k, v, pos, hd, stride)).max() <= 1e-5
+    dev.free_all()
+
+
+@pytest.mark.parametrize("n", [64, 288, 576, 768])
+def test_rmsnorm(dev, oracle, n):
+    rng = np.random.default_rng(n)
+    x, w = rng.standard_normal(n).astype(np.float32), (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    assert rel_err(dev.rmsnorm(x, w, 1e-5), oracle.rmsnorm(x, w, 1e-5)) < 1e-6
+
+
+@pytest.mark.parametrize("hd,pos", [(48, 0), (48, 7), (64, 127), (64, 1023)])
+def test_rope(dev, oracle, hd, pos):
+    n_heads = 6
+    v = np.random.default_rng(pos).standard_normal(n_heads * hd).astype(np.float32)
+    got = dev.rope(v, n_heads, hd, pos, 10000.0)
+    want = oracle.rope(v, n_heads, hd, pos, 10000.0)
+    assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
+
+
+def test_silu_mul(dev, oracle):
+    rng = np.random.default_rng(5)
+    h, g = rng.standard_normal(2048).astype(np.float32), (rng.standard_normal(2048) * 4).astype(np.float32)
+    assert rel_err(dev.silu_mul(h, g), oracle.silu_mul(h, g)) < 1e-6
+
+
+def test_argmax_lowest_index_wins(dev):
+    x = np.random.default_rng(6).standard_normal(49152).astype(np.float32)
+    assert dev.argmax(x) == int(np.argmax(x))
+    x[[100, 7000, 40000]] = x.max() + 1
+    assert dev.argmax(x) == 100
+    assert dev.argmax(np.zeros(32000, np.float32)) == 0
+    dev.free_all()
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, Q8_0, Q4_0, MXFP4], ids=NAMES.get)
+def test_table_matches_reference_tables(reference, dtype):
+    """l3m_kernels_hip on the reference's own packed tiles and prepared vector, against its scalar table."""
+    import ctypes as C
+    import l3m_amd as A
+    from oracle.oracle import _Table
+    lib = A.lib()
+    table = _Table.in_dll(lib, "l3m_kernels_hip")
+    assert table.name == b"hip"
+    for k, ntiles in [(288, 3), (1376, 2), (3072, 5)]:
+        n = ntiles * 16
+        w = rows(dtype, n, k, seed=k + dtype)
+        tiles = reference.pack_tiles(dtype, [w[i] if i < n - 3 else None for i in range(n)], k)
+        x = np.random.default_rng(k).standard_normal(k).astype(np.float32)
+        v, keep = reference.prepare(dtype, x)
+        y = np.zeros(n, np.float32)
+        table.gemv[dtype](y.ctypes.data_as(C.POINTER(C.c_float)), tiles.ctypes.data, ntiles, k, C.byref(v))
+        want = reference.gemv("scalar", dtype, tiles, ntiles, k, x)
+        assert rel_err(y, want) < TOL[dtype], (k, rel_err(y, want))
+
+
+def test_table_attend_matches_reference(reference):
+    import ctypes as C
+    import l3m_amd as A
+    from oracle.oracle import _Table
+    table = _Table.in_dll(A.lib(), "l3m_kernels_hip")
+    rng = np.random.default_rng(9)
+    hd, pos, stride = 64, 100, 128
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBFFF
+    v = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBFFF
+    out = np.zeros(hd, np.float32)
+    f, u16 = C.POINTER(C.c_float), C.POINTER(C.c_uint16)
+    table.attend(out.ctypes.data_as(f), q.ctypes.data_as(f), k.ctypes.data_as(u16), v.ctypes.data_as(u16), pos, hd, stride)
+    assert np.abs(out - reference.attend("scalar", q, k, v, pos, hd, stride)).max() <= 1e-5
