@@ -121,9 +121,9 @@ void   l3m_rope_table(float *table, int ctx, int hd, float theta);   // host: [c
 // generated token. Timers use hipEvents on the library stream; microseconds per launch, <0 on error.
 double l3m_bench_decode(l3m_model *m, const int32_t *prompt, int n_prompt, int n_tokens);
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);
-// One kernel of the decode step at position pos: kind 0 qkv, 1 attention, 2 wo, 3 gate/up, 4 down, 5 head.
+// One kernel of the decode step at position pos: kind 0 attention block, 1 FFN block, 2 head.
 double l3m_bench_kernel(l3m_model *m, int kind, int layer, int pos, int iters);
-double l3m_kernel_bytes(const l3m_model *m, int kind, int pos);   // bytes of weights (or KV) one launch reads
+double l3m_kernel_bytes(const l3m_model *m, int kind, int pos);   // weight bytes one launch of that kernel reads
 double l3m_weight_bytes(const l3m_model *m);                       // weight bytes streamed per token
 
 // Synthetic .l3m models (seeded, host-independent bytes).

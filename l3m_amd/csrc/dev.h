@@ -11,24 +11,43 @@ extern "C" {
 
 // l3m_dmat (lane-tile device matrix, layout in host.h) is declared in l3m_hip.h.
 
+// One head group of a layer's attention block: nq consecutive query heads (nq * hd a multiple of 32 for
+// quantized weights, so the Wo slice is whole blocks) and the kv heads they read.
 typedef struct {
-    l3m_dmat     qkv;            // [q rows (dim) | k rows (kv_dim) | v rows (kv_dim)] x dim
-    l3m_dmat     wo;             // dim x dim
-    l3m_dmat     gate_up;        // tiles interleaved: gate tile j, up tile j, ... (ffn padded to 16) x dim
-    l3m_dmat     down;           // dim x ffn
-    const float *attn_norm, *ffn_norm;
+    l3m_dmat qkv;                // rows [q of the nq heads | k of the nkv kv heads | v of them] x dim
+    l3m_dmat wo;                 // dim rows x the group's nq * hd Wo columns
+    int      q0, nq, kv0, nkv;   // first query head, count; first kv head, count
+    unsigned write_kv;           // bit i: this group writes kv head kv0 + i into the cache
+    int      pad_;
+} l3m_dgroup;
+
+// One chunk of a layer's FFN block: ffn rows [f0, f0 + nf), nf a multiple of 32.
+typedef struct {
+    l3m_dmat gate_up;            // 2 * ceil16(nf) rows: gate tile t, up tile t, ... x dim
+    l3m_dmat down;               // dim rows x the chunk's nf Wdown columns
+    int      f0, nf;
+} l3m_dchunk;
+
+typedef struct {
+    const l3m_dgroup *groups;    // device arrays [n_groups], [n_chunks]
+    const l3m_dchunk *chunks;
+    const float      *attn_norm, *ffn_norm;
 } l3m_dlayer;
 
 typedef struct {
-    int          dim, hd, n_heads, n_kv, kv_dim, ffn, ffn_pad, vocab, ctx, n_layers, nslots;
+    int          dim, hd, n_heads, n_kv, kv_dim, ffn, vocab, ctx, n_layers, nslots;
+    int          n_groups, n_chunks, head_grid, head_tiles_per_wg, body_dtype;
     float        eps;
+    unsigned     lds_a, lds_b, lds_h;   // dynamic LDS bytes of the three step kernels
     int         *pos;            // [1] position of the step being run
     int32_t     *tokens;         // [ctx + 1]: prompt ids, then each step's argmax at pos + 1
-    float       *x, *q, *attn, *h;
+    float       *xa, *xb;        // residual stream entering the attention block / the FFN block
+    float       *po;             // [n_groups][dim] attention-block partials (Wo column slices)
+    float       *pd;             // [n_chunks][dim] FFN partials (Wdown column slices)
     float       *logits;         // [nslots][vocab], slot = pos % nslots
-    float       *part_val;       // per-workgroup argmax partials of the head
+    float       *part_val;       // [head_grid] argmax partials
     int         *part_idx;
-    unsigned    *done;           // workgroups finished in the head kernel
+    unsigned    *done;           // head workgroups finished this step
     const float *rope;           // [ctx][hd/2][2] cos, sin (host libm, the reference's angles)
     uint16_t    *kc, *vc;        // [layer][n_kv][ctx][hd] bf16
     l3m_dmat     embed, head;    // head may alias embed (tied)
@@ -58,13 +77,17 @@ int    l3m_k_silu_mul(float *h, const float *g, int n, void *stream);
 int    l3m_k_argmax(const float *x, int n, int32_t *out, void *stream);
 
 // ------------------------------------------------------------------ decode step
-// Enqueue one decode step at the device position: embedding, every layer, and when with_head, the final
-// norm, the head, the argmax written to tokens[pos + 1]. Always advances pos.
+// Enqueue one decode step at the device position: per layer the attention block (one workgroup per head
+// group) and the FFN block (one per chunk); with_head adds the final norm, the head and the argmax written
+// to tokens[pos + 1]. Always advances pos. LDS sizes in m must come from l3m_step_lds.
+unsigned l3m_lds_attn(int dtype, int dim, int ctx, int hd, const l3m_dgroup *g);
+unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c);
+unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg);
 int l3m_step_enqueue(const l3m_dmodel *m, const l3m_dlayer *layers, int with_head, void *stream);
 
 // Timing (microseconds per launch, hipEvents on the library stream, after one untimed launch).
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);
-// kind: 0 qkv, 1 attention, 2 wo, 3 gate/up, 4 down, 5 head (which then does not advance the position)
+// kind: 0 attention block, 1 FFN block, 2 head (which then does not advance the position)
 double l3m_time_step_kernel(const l3m_dmodel *m, const l3m_dlayer *layers, int kind, int layer, int iters);
 
 // Captured steps: graph 0 without the head (prompt), graph 1 with it.

@@ -414,126 +414,406 @@ __global__ void __launch_bounds__(NT) k_argmax(const float *x, int n, int32_t *o
     if (threadIdx.x == 0) *out = idx == 0x7FFFFFFF ? 0 : idx;
 }
 
-// ------------------------------------------------------------------------------ fused decode kernels
+// ------------------------------------------------------------------------------ decode step kernels
+//
+// Per layer: kernel A (one workgroup per head group) = norm + prep + qkv rows + RoPE + KV write +
+// attention + the group's Wo column slice; kernel B (one workgroup per FFN chunk) = norm + prep + gate/up
+// rows + SiLU + prep + the chunk's Wdown column slice. Each writes a partial residual (po, pd); the next
+// kernel adds the partials in index order, so results are run-to-run identical. Workgroups are 1024
+// threads: waves 0-3 build the activation (prologue) while waves 4-15 already hold their weights in
+// flight, loaded into registers at entry because they depend on nothing.
 
-// Layer input x: the residual stream, or for layer 0 the embedding row of tokens[pos] (engine.c:236).
-struct XIn {
-    const float *x;
-    l3m_dmat embed;
-    int tok;
-    __device__ float operator()(int i) const { return x ? x[i] : lt_elem(embed, tok, i); }
+constexpr int NTE = 1024, NWE = NTE / 64, WPRO = 4, WCOMP = NWE - WPRO, NPRO = WPRO * 64;
+
+template <int DT> constexpr int nslot_a() { return DT == L3M_F32 ? 2 : DT == L3M_BF16 ? 3 : DT == L3M_Q8_0 ? 5 : 8; }
+template <int DT> constexpr int nslot_b() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 3 : 4; }
+
+// One lane's weights: slot s holds pair p = (cw + s * WCOMP) * 4 + sub of the matrix, where a pair is
+// (tile, block) = (p / nb, p % nb) and the lane reads row (lane & 15) of it: 4 consecutive pairs per
+// wavefront = one contiguous 64 * QBYTES run.
+template <int DT, int NS>
+struct Pref {
+    uint4 w[NS][qbytes(DT) / 16];
+    uint32_t sc[NS];
 };
 
-// RMSNorm + prep + qkv rows + RoPE on q and k + bf16 K, V into the cache at pos (engine.c:241-248).
-template <int DT>
-__global__ void __launch_bounds__(NT) k_qkv(l3m_dmodel M, l3m_dlayer L, int layer, int from_embed, int S) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    Smem s = carve(smem, DT, M.dim);
-    const int kp = kpad(M.dim), pos = *M.pos;
-    XIn src{from_embed ? nullptr : M.x, M.embed, from_embed ? M.tokens[pos] : 0};
-    if (from_embed && blockIdx.x == 0)
-        for (int i = threadIdx.x; i < M.dim; i += NT) M.x[i] = src(i);
-    stage_x(s.xs, src, M.dim, kp, L.attn_norm, M.eps, s.scr);
-    prep_act<DT>(s.act, s.xs, kp);
-    const int tpw = 4 / S, tile0 = blockIdx.x * tpw;
-    wg_matvec<DT>(L.qkv, tile0, S, s.act, kp, s.red, s.yv);
-    if (threadIdx.x < 64) {
-        const int tid = threadIdx.x, r = (tile0 + (tid >> 4)) * RT + (tid & 15);
-        const float val = tid < tpw * 16 ? s.yv[tid] : 0.f, partner = __shfl_xor(val, 1);
-        if (tid < tpw * 16 && r < L.qkv.rows) {
-            const int kvd = M.kv_dim;
-            if (r < M.dim + kvd) {
-                const int local = r < M.dim ? r : r - M.dim, i = (local % M.hd) >> 1;
-                const float *cs = M.rope + ((size_t)pos * (M.hd >> 1) + i) * 2;
-                const float o = rope_one(val, partner, cs[0], cs[1], local & 1);
-                if (r < M.dim) M.q[r] = o;
-                else M.kc[(((size_t)layer * M.n_kv + local / M.hd) * M.ctx + pos) * M.hd + local % M.hd] = f32_bf16(o);
-            } else {
-                const int local = r - M.dim - kvd;
-                M.vc[(((size_t)layer * M.n_kv + local / M.hd) * M.ctx + pos) * M.hd + local % M.hd] = f32_bf16(val);
-            }
+template <int DT, int NS>
+__device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, int cw, int s0, int lane) {
+    constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
+    const int sub = lane >> 4, row = lane & 15, P = m.tiles * m.nb;
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int p = (cw + (s0 + s) * WCOMP) * 4 + sub;
+        pf.sc[s] = 0;
+        if (p < P) {
+            const uint4 *src = (const uint4 *)(m.q + ((size_t)p * 16 + row) * QBY);
+#pragma unroll
+            for (int v = 0; v < NV; v++) pf.w[s][v] = src[v];
+            if constexpr (SBY == 2) pf.sc[s] = ((const uint16_t *)m.s)[(size_t)p * 16 + row];
+            if constexpr (SBY == 1) pf.sc[s] = m.s[(size_t)p * 16 + row];
         }
     }
 }
 
-// Prep of attn + wo rows + residual add (engine.c:256-259).
-template <int DT>
-__global__ void __launch_bounds__(NT) k_wo(l3m_dmodel M, l3m_dlayer L, int S) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    Smem s = carve(smem, DT, M.dim);
-    const int kp = kpad(M.dim);
-    const float *a = M.attn;
-    stage_x(s.xs, [&](int i) { return a[i]; }, M.dim, kp, nullptr, 0.f, s.scr);
-    prep_act<DT>(s.act, s.xs, kp);
-    const int tpw = 4 / S, tile0 = blockIdx.x * tpw;
-    wg_matvec<DT>(L.wo, tile0, S, s.act, kp, s.red, s.yv);
-    if (threadIdx.x < tpw * 16) {
-        const int r = (tile0 + (threadIdx.x >> 4)) * RT + (threadIdx.x & 15);
-        if (r < M.dim) M.x[r] += s.yv[threadIdx.x];
+template <int DT, int NS>
+__device__ __forceinline__ void pref_compute(const Pref<DT, NS> &pf, const l3m_dmat &m, int cw, int s0, int lane,
+                                             const uint8_t *act, int kp, float *res) {
+    const int sub = lane >> 4, row = lane & 15, P = m.tiles * m.nb;
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int p = (cw + (s0 + s) * WCOMP) * 4 + sub;
+        if (p < P) res[p * 16 + row] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, p % m.nb);
     }
 }
 
-// RMSNorm + prep + gate and up rows of the same outputs + h = up * silu(gate) (engine.c:261-268).
-template <int DT>
-__global__ void __launch_bounds__(NT) k_ffn(l3m_dmodel M, l3m_dlayer L, int S) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    Smem s = carve(smem, DT, M.dim);
-    const int kp = kpad(M.dim);
-    const float *x = M.x;
-    stage_x(s.xs, [&](int i) { return x[i]; }, M.dim, kp, L.ffn_norm, M.eps, s.scr);
-    prep_act<DT>(s.act, s.xs, kp);
-    const int tpw = 4 / S, tile0 = blockIdx.x * tpw;
-    wg_matvec<DT>(L.gate_up, tile0, S, s.act, kp, s.red, s.yv);
-    if (threadIdx.x < tpw * 8) {
-        const int p = threadIdx.x >> 4, r16 = threadIdx.x & 15;
-        const float g = s.yv[(2 * p) * 16 + r16], u = s.yv[(2 * p + 1) * 16 + r16];
-        const int r = (tile0 / 2 + p) * RT + r16;
-        if (r < M.ffn) M.h[r] = silu_mul(u, g);
+// Compute waves: the prefetched first batch, then any further batches of m. res[pair * 16 + row].
+template <int DT, int NS>
+__device__ void mv_pairs(Pref<DT, NS> &pf, const l3m_dmat &m, int cw, int lane, const uint8_t *act, int kp, float *res) {
+    const int P = m.tiles * m.nb;
+    pref_compute<DT, NS>(pf, m, cw, 0, lane, act, kp, res);
+    for (int s0 = NS; s0 * WCOMP * 4 < P; s0 += NS) {
+        pref_load<DT, NS>(pf, m, cw, s0, lane);
+        pref_compute<DT, NS>(pf, m, cw, s0, lane, act, kp, res);
     }
 }
 
-// Prep of h + down rows + residual add (engine.c:272-275). The last layer of a step without the head
-// advances the position (nothing in this kernel reads it).
-template <int DT>
-__global__ void __launch_bounds__(NT) k_down(l3m_dmodel M, l3m_dlayer L, int S, int advance) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    Smem s = carve(smem, DT, M.ffn);
-    const int kp = kpad(M.ffn);
-    const float *h = M.h;
-    stage_x(s.xs, [&](int i) { return h[i]; }, M.ffn, kp, nullptr, 0.f, s.scr);
-    prep_act<DT>(s.act, s.xs, kp);
-    const int tpw = 4 / S, tile0 = blockIdx.x * tpw;
-    wg_matvec<DT>(L.down, tile0, S, s.act, kp, s.red, s.yv);
-    if (threadIdx.x < tpw * 16) {
-        const int r = (tile0 + (threadIdx.x >> 4)) * RT + (threadIdx.x & 15);
-        if (r < M.dim) M.x[r] += s.yv[threadIdx.x];
+// out[r] = sum over the row's blocks, in block order (all threads), for r < rows.
+__device__ void rows_sum(const l3m_dmat &m, const float *res, float *out, int rows) {
+    for (int i = threadIdx.x; i < rows; i += NTE) {
+        const float *p = res + (size_t)(i >> 4) * m.nb * 16 + (i & 15);
+        float y = p[0];
+        for (int b = 1; b < m.nb; b++) y += p[b * 16];
+        out[i] = y;
     }
-    if (advance && blockIdx.x == 0 && threadIdx.x == 0) *M.pos += 1;
 }
 
-// Final RMSNorm + prep + head rows -> logits slot, then the greedy argmax (engine.c:277-301): each
-// workgroup reduces its rows; the last workgroup to finish reduces the partials in index order,
-// writes tokens[pos + 1], resets the counter and advances pos.
+// Workgroup-wide (all 16 wavefronts) reductions in a fixed order; scr: 16 floats / ints of LDS.
+__device__ float wge_sum(float v, float *scr) {
+    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scr[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = scr[0];
+    for (int w = 1; w < NWE; w++) t += scr[w];
+    return t;
+}
+__device__ float wge_max(float v, float *scr) {
+    for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scr[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = scr[0];
+    for (int w = 1; w < NWE; w++) t = fmaxf(t, scr[w]);
+    return t;
+}
+__device__ void wge_argmax(float &v, int &i, float *sv, int *si) {
+    for (int o = 32; o; o >>= 1) {
+        const float v2 = __shfl_xor(v, o);
+        const int i2 = __shfl_xor(i, o);
+        better(v, i, v2, i2);
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = i; }
+    __syncthreads();
+    v = sv[0]; i = si[0];
+    for (int w = 1; w < NWE; w++) better(v, i, sv[w], si[w]);
+}
+
+// xs[0, dim) = base + parts[0] + parts[1] + ... in index order (waves 0-3, float4 slots; the loads of
+// a batch of 8 parts are issued before its adds). Optionally also stored to `keep`.
+__device__ void fill_sum(float *xs, const float *base, const float *parts, int nparts, int dim, float *keep) {
+    if (threadIdx.x >= NPRO) return;
+    for (int f = threadIdx.x; f < dim / 4; f += NPRO) {
+        float4 v = ((const float4 *)base)[f];
+        for (int j0 = 0; j0 < nparts; j0 += 8) {
+            float4 p[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (j0 + j < nparts) p[j] = ((const float4 *)(parts + (size_t)(j0 + j) * dim))[f];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (j0 + j < nparts) { v.x += p[j].x; v.y += p[j].y; v.z += p[j].z; v.w += p[j].w; }
+        }
+        ((float4 *)xs)[f] = v;
+        if (keep) ((float4 *)keep)[f] = v;
+    }
+}
+
+// Norm + prep of xs (filled for [0, k) by waves 0-3, padded here): RMSNorm with nw when given
+// (ops.c:13-18), then the activation prep (pack.c:101-123) into act. All threads call it.
 template <int DT>
-__global__ void __launch_bounds__(NT) k_head(l3m_dmodel M, int S, int advance) {
+__device__ void norm_prep(float *xs, uint8_t *act, int k, int kp, const float *nw, float eps, float *scr) {
+    const int tid = threadIdx.x;
+    for (int i = k + tid; i < kp; i += NTE) xs[i] = 0.f;
+    __syncthreads();
+    if (nw) {
+        float ss = 0.f;
+        if (tid < NPRO)
+            for (int i = tid; i < k; i += NPRO) ss = fmaf(xs[i], xs[i], ss);
+        const float tot = wge_sum(ss, scr);
+        const float s = 1.0f / sqrtf(tot / (float)k + eps);
+        if (tid < NPRO)
+            for (int i = tid; i < k; i += NPRO) xs[i] = xs[i] * s * nw[i];
+        __syncthreads();
+    }
+    if constexpr (quantized(DT)) {
+        const int nb = kp / 32, g = tid >> 3, l = tid & 7;
+        float *scale = (float *)(act + kp);
+        int *sum = (int *)(act + kp + 4 * nb);
+        for (int b = g; b < nb; b += NTE / 8) {
+            const float4 v = *(const float4 *)(xs + b * 32 + 4 * l);
+            float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+            am = fmaxf(am, __shfl_xor(am, 1));
+            am = fmaxf(am, __shfl_xor(am, 2));
+            am = fmaxf(am, __shfl_xor(am, 4));
+            const float inv = am > 0.f ? 127.0f / am : 0.f;
+            const int q0 = (int)rintf(v.x * inv), q1 = (int)rintf(v.y * inv), q2 = (int)rintf(v.z * inv), q3 = (int)rintf(v.w * inv);
+            *(uint32_t *)(act + b * 32 + 4 * l) = (uint32_t)(q0 & 255) | (uint32_t)(q1 & 255) << 8 | (uint32_t)(q2 & 255) << 16 | (uint32_t)(q3 & 255) << 24;
+            int s = q0 + q1 + q2 + q3;
+            s += __shfl_xor(s, 1);
+            s += __shfl_xor(s, 2);
+            s += __shfl_xor(s, 4);
+            if (l == 0) { scale[b] = am / 127.0f; sum[b] = s; }
+        }
+    } else if constexpr (DT == L3M_BF16) {
+        for (int i = tid; i < kp; i += NTE) ((uint16_t *)act)[i] = f32_bf16(xs[i]);
+    } else {
+        for (int i = tid; i < kp; i += NTE) ((float *)act)[i] = xs[i];
+    }
+    __syncthreads();
+}
+
+// LDS regions of the step kernels (byte offsets, 16-aligned) from the layer geometry.
+struct LdsA { size_t xs, act, res, qkv, kv, sc, att, act2, scr, total; };
+__host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g) {
+    LdsA L;
+    size_t o = 0;
+    const size_t pq = (size_t)g.qkv.tiles * g.qkv.nb, pw = (size_t)g.wo.tiles * g.wo.nb;
+    L.xs = o;   o += align16(4 * (size_t)kpad(dim));
+    L.act = o;  o += align16(act_size(dt, dim));
+    L.res = o;  o += align16(64 * (pq > pw ? pq : pw));
+    L.qkv = o;  o += align16(64 * (size_t)g.qkv.tiles);
+    L.kv = o;   o += align16(8 * (size_t)g.nkv * hd);
+    L.sc = o;   o += align16(4 * (size_t)(ctx + 4));
+    L.att = o;  o += align16(4 * (size_t)kpad(g.nq * hd));
+    L.act2 = o; o += align16(act_size(dt, g.nq * hd));
+    L.scr = o;  o += 4 * (NTE + 64);
+    L.total = o;
+    return L;
+}
+struct LdsB { size_t xs, act, res, gu, h, act2, scr, total; };
+__host__ __device__ inline LdsB lds_b(int dt, int dim, const l3m_dchunk &c) {
+    LdsB L;
+    size_t o = 0;
+    const size_t pg = (size_t)c.gate_up.tiles * c.gate_up.nb, pw = (size_t)c.down.tiles * c.down.nb;
+    L.xs = o;   o += align16(4 * (size_t)kpad(dim));
+    L.act = o;  o += align16(act_size(dt, dim));
+    L.res = o;  o += align16(64 * (pg > pw ? pg : pw));
+    L.gu = o;   o += align16(64 * (size_t)c.gate_up.tiles);
+    L.h = o;    o += align16(4 * (size_t)kpad(c.nf));
+    L.act2 = o; o += align16(act_size(dt, c.nf));
+    L.scr = o;  o += 4 * 64;
+    L.total = o;
+    return L;
+}
+struct LdsH { size_t xs, act, res, y, scr, total; };
+__host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg) {
+    LdsH L;
+    size_t o = 0;
+    L.xs = o;  o += align16(4 * (size_t)kpad(dim));
+    L.act = o; o += align16(act_size(dt, dim));
+    L.res = o; o += align16(64 * (size_t)tiles_per_wg * nb);
+    L.y = o;   o += align16(64 * (size_t)tiles_per_wg);
+    L.scr = o; o += 4 * 64;
+    L.total = o;
+    return L;
+}
+
+// Kernel A: the attention block of one head group (engine.c:241-258).
+template <int DT>
+__global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw, int layer) {
     extern __shared__ __align__(16) uint8_t smem[];
-    Smem s = carve(smem, DT, M.dim);
-    const int kp = kpad(M.dim), pos = *M.pos;
-    const float *x = M.x;
-    stage_x(s.xs, [&](int i) { return x[i]; }, M.dim, kp, M.norm, M.eps, s.scr);
-    prep_act<DT>(s.act, s.xs, kp);
-    const int tpw = 4 / S, tile0 = blockIdx.x * tpw;
-    wg_matvec<DT>(M.head, tile0, S, s.act, kp, s.red, s.yv);
-    float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab;
+    const l3m_dgroup G = Lw.groups[blockIdx.x];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, cw = wave - WPRO;
+    Pref<DT, nslot_a<DT>()> pa;
+    Pref<DT, nslot_b<DT>()> pb;
+    if (wave >= WPRO) {
+        pref_load<DT, nslot_a<DT>()>(pa, G.qkv, cw, 0, lane);
+        pref_load<DT, nslot_b<DT>()>(pb, G.wo, cw, 0, lane);
+    }
+    const int pos = *M.pos, dim = M.dim, hd = M.hd, kp = kpad(dim);
+    const LdsA L = lds_a(DT, dim, M.ctx, hd, G);
+    float *xs = (float *)(smem + L.xs), *res = (float *)(smem + L.res), *qkv = (float *)(smem + L.qkv);
+    float *kvc = (float *)(smem + L.kv), *sc = (float *)(smem + L.sc), *att = (float *)(smem + L.att), *scr = (float *)(smem + L.scr);
+    uint8_t *act = smem + L.act, *act2 = smem + L.act2;
+
+    // layer input: the embedding row (engine.c:236) or xb + the previous FFN partials; group 0 keeps it in xa
+    if (layer == 0) {
+        const int tok = M.tokens[pos];
+        if (tid < NPRO)
+            for (int i = tid; i < dim; i += NPRO) {
+                xs[i] = lt_elem(M.embed, tok, i);
+                if (blockIdx.x == 0) M.xa[i] = xs[i];
+            }
+    } else {
+        fill_sum(xs, M.xb, M.pd, M.n_chunks, dim, blockIdx.x == 0 ? M.xa : nullptr);
+    }
+    norm_prep<DT>(xs, act, dim, kp, Lw.attn_norm, M.eps, scr);
+
+    if (wave >= WPRO) mv_pairs<DT, nslot_a<DT>()>(pa, G.qkv, cw, lane, act, kp, res);
+    __syncthreads();
+    const int nqd = G.nq * hd, nkd = G.nkv * hd;
+    rows_sum(G.qkv, res, qkv, nqd + 2 * nkd);
+    __syncthreads();
+
+    // RoPE on q and k: pairs (2i, 2i+1) of each head by the table angle i (ops.c:29-40)
+    float rot = 0.f;
+    if (tid < nqd + nkd) {
+        const int local = tid < nqd ? tid : tid - nqd, i = (local % hd) >> 1;
+        const float *cs = M.rope + ((size_t)pos * (hd >> 1) + i) * 2;
+        const float a = qkv[tid], b = qkv[tid ^ 1];
+        rot = (tid & 1) ? b * cs[1] + a * cs[0] : a * cs[0] - b * cs[1];
+    }
+    __syncthreads();
+    if (tid < nqd + nkd) qkv[tid] = rot;
+    __syncthreads();
+    // k and v of this position, as the bf16 cache holds them (engine.c:247-248)
+    for (int i = tid; i < 2 * nkd; i += NTE) {
+        const uint16_t h = f32_bf16(qkv[nqd + i]);
+        kvc[i] = bf16_f32(h);
+        const int j = i < nkd ? i : i - nkd, kvl = j / hd;
+        if (G.write_kv >> kvl & 1u) {
+            uint16_t *c = i < nkd ? M.kc : M.vc;
+            c[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + j % hd] = h;
+        }
+    }
+    __syncthreads();
+
+    // attention of each query head over positions 0..pos (ops.c:58-73); position pos from LDS
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int hpk = M.n_heads / M.n_kv, groups = NTE / hd, gi = tid / hd, ii = tid % hd;
+    for (int h = 0; h < G.nq; h++) {
+        const int kvl = (G.q0 + h) / hpk - G.kv0;
+        const float *q = qkv + h * hd;
+        const uint16_t *kh = M.kc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx * hd;
+        const uint16_t *vh = M.vc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx * hd;
+        float mx = -INFINITY;
+        for (int t = tid; t <= pos; t += NTE) {
+            float dot = 0.f;
+            if (t < pos) {
+                const uint4 *kr = (const uint4 *)(kh + (size_t)t * hd);
+                for (int v = 0; v < hd / 8; v++) {
+                    const uint4 kk = kr[v];
+                    const float *qq = q + v * 8;
+                    dot = fmaf(qq[0], bf16_f32(kk.x & 0xFFFF), dot); dot = fmaf(qq[1], bf16_f32(kk.x >> 16), dot);
+                    dot = fmaf(qq[2], bf16_f32(kk.y & 0xFFFF), dot); dot = fmaf(qq[3], bf16_f32(kk.y >> 16), dot);
+                    dot = fmaf(qq[4], bf16_f32(kk.z & 0xFFFF), dot); dot = fmaf(qq[5], bf16_f32(kk.z >> 16), dot);
+                    dot = fmaf(qq[6], bf16_f32(kk.w & 0xFFFF), dot); dot = fmaf(qq[7], bf16_f32(kk.w >> 16), dot);
+                }
+            } else {
+                const float *kr = kvc + kvl * hd;
+                for (int i = 0; i < hd; i++) dot = fmaf(q[i], kr[i], dot);
+            }
+            sc[t] = dot * scale;
+            mx = fmaxf(mx, dot * scale);
+        }
+        mx = wge_max(mx, scr);
+        float sum = 0.f;
+        for (int t = tid; t <= pos; t += NTE) {
+            const float e = expf(sc[t] - mx);
+            sc[t] = e;
+            sum += e;
+        }
+        sum = wge_sum(sum, scr);
+        for (int t = tid; t <= pos; t += NTE) sc[t] = sc[t] / sum;
+        __syncthreads();
+        float acc = 0.f;
+        if (gi < groups)
+            for (int t = gi; t <= pos; t += groups)
+                acc = fmaf(sc[t], t < pos ? bf16_f32(vh[(size_t)t * hd + ii]) : kvc[nkd + kvl * hd + ii], acc);
+        scr[64 + tid] = acc;
+        __syncthreads();
+        if (tid < hd) {
+            float o = scr[64 + tid];
+            for (int g = 1; g < groups; g++) o += scr[64 + g * hd + tid];
+            att[h * hd + tid] = o;
+        }
+        __syncthreads();
+    }
+    // prep of the group's attention output, then its Wo columns -> the partial residual po[group]
+    norm_prep<DT>(att, act2, nqd, kpad(nqd), nullptr, 0.f, scr);
+    if (wave >= WPRO) mv_pairs<DT, nslot_b<DT>()>(pb, G.wo, cw, lane, act2, kpad(nqd), res);
+    __syncthreads();
+    rows_sum(G.wo, res, M.po + (size_t)blockIdx.x * dim, dim);
+}
+
+// Kernel B: the FFN block of one chunk of ffn rows (engine.c:259-275). The last layer of a step without
+// the head advances the position (nothing in this kernel reads it).
+template <int DT>
+__global__ void __launch_bounds__(NTE) k_ffn_block(l3m_dmodel M, l3m_dlayer Lw, int advance) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const l3m_dchunk C = Lw.chunks[blockIdx.x];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, cw = wave - WPRO;
+    Pref<DT, nslot_a<DT>()> pa;
+    Pref<DT, nslot_b<DT>()> pb;
+    if (wave >= WPRO) {
+        pref_load<DT, nslot_a<DT>()>(pa, C.gate_up, cw, 0, lane);
+        pref_load<DT, nslot_b<DT>()>(pb, C.down, cw, 0, lane);
+    }
+    const int dim = M.dim, kp = kpad(dim);
+    const LdsB L = lds_b(DT, dim, C);
+    float *xs = (float *)(smem + L.xs), *res = (float *)(smem + L.res), *gu = (float *)(smem + L.gu);
+    float *h = (float *)(smem + L.h), *scr = (float *)(smem + L.scr);
+    uint8_t *act = smem + L.act, *act2 = smem + L.act2;
+
+    fill_sum(xs, M.xa, M.po, M.n_groups, dim, blockIdx.x == 0 ? M.xb : nullptr);   // x += proj (engine.c:259)
+    norm_prep<DT>(xs, act, dim, kp, Lw.ffn_norm, M.eps, scr);
+    if (wave >= WPRO) mv_pairs<DT, nslot_a<DT>()>(pa, C.gate_up, cw, lane, act, kp, res);
+    __syncthreads();
+    rows_sum(C.gate_up, res, gu, C.gate_up.rows);
+    __syncthreads();
+    if (tid < NPRO)                                         // h = up * silu(gate) (ops.c:49-51)
+        for (int i = tid; i < C.nf; i += NPRO) h[i] = silu_mul(gu[(2 * (i >> 4) + 1) * 16 + (i & 15)], gu[(2 * (i >> 4)) * 16 + (i & 15)]);
+    norm_prep<DT>(h, act2, C.nf, kpad(C.nf), nullptr, 0.f, scr);
+    if (wave >= WPRO) mv_pairs<DT, nslot_b<DT>()>(pb, C.down, cw, lane, act2, kpad(C.nf), res);
+    __syncthreads();
+    rows_sum(C.down, res, M.pd + (size_t)blockIdx.x * dim, dim);
+    if (advance && blockIdx.x == 0 && tid == 0) *M.pos += 1;
+}
+
+// Final norm + head rows -> logits slot, then the greedy argmax (engine.c:277-301): each workgroup
+// reduces its rows; the last workgroup to finish reduces the partials in index order, writes
+// tokens[pos + 1], resets the counter and (advance) moves pos on.
+template <int DT>
+__global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, cw = wave - WPRO;
+    const int tpw = M.head_tiles_per_wg, t0 = blockIdx.x * tpw;
+    l3m_dmat V = M.head;                                    // this workgroup's tiles of the head
+    const int nt = t0 + tpw <= V.tiles ? tpw : V.tiles - t0;
+    V.q += (size_t)t0 * V.nb * 16 * qbytes(DT);
+    if (sbytes(DT)) V.s += (size_t)t0 * V.nb * 16 * sbytes(DT);
+    V.tiles = nt > 0 ? nt : 0;
+    V.rows = V.tiles * 16 < M.vocab - t0 * 16 ? V.tiles * 16 : M.vocab - t0 * 16;
+    Pref<DT, nslot_a<DT>()> pa;
+    if (wave >= WPRO && nt > 0) pref_load<DT, nslot_a<DT>()>(pa, V, cw, 0, lane);
+    const int pos = *M.pos, dim = M.dim, kp = kpad(dim);
+    const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
+    float *xs = (float *)(smem + L.xs), *res = (float *)(smem + L.res), *y = (float *)(smem + L.y), *scr = (float *)(smem + L.scr);
+    uint8_t *act = smem + L.act;
+    fill_sum(xs, M.xb, M.pd, M.n_chunks, dim, nullptr);     // x += down (engine.c:275), last layer
+    norm_prep<DT>(xs, act, dim, kp, M.norm, M.eps, scr);
+    if (wave >= WPRO && nt > 0) mv_pairs<DT, nslot_a<DT>()>(pa, V, cw, lane, act, kp, res);
+    __syncthreads();
+    if (nt > 0) rows_sum(V, res, y, V.rows);
+    __syncthreads();
+    float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab + (size_t)t0 * 16;
     float v = -INFINITY;
     int idx = 0x7FFFFFFF;
-    if (threadIdx.x < tpw * 16) {
-        const int r = (tile0 + (threadIdx.x >> 4)) * RT + (threadIdx.x & 15);
-        if (r < M.vocab) { lg[r] = s.yv[threadIdx.x]; v = s.yv[threadIdx.x]; idx = r; }
-    }
-    wg_argmax(v, idx, s.scr, s.iscr);
+    if (nt > 0 && tid < V.rows) { lg[tid] = y[tid]; v = y[tid]; idx = t0 * 16 + tid; }
+    wge_argmax(v, idx, scr, (int *)(scr + 16));
     __shared__ int last;
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         M.part_val[blockIdx.x] = v;
         M.part_idx[blockIdx.x] = idx;
         __threadfence();
@@ -544,13 +824,13 @@ __global__ void __launch_bounds__(NT) k_head(l3m_dmodel M, int S, int advance) {
     __threadfence();
     v = -INFINITY;
     idx = 0x7FFFFFFF;
-    for (int w = threadIdx.x; w < (int)gridDim.x; w += NT) {
+    for (int w = tid; w < (int)gridDim.x; w += NTE) {
         const float pv = __hip_atomic_load(M.part_val + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int pi = __hip_atomic_load(M.part_idx + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         better(v, idx, pv, pi);
     }
-    wg_argmax(v, idx, s.scr, s.iscr);
-    if (threadIdx.x == 0) {
+    wge_argmax(v, idx, scr, (int *)(scr + 16));
+    if (tid == 0) {
         if (advance) {
             M.tokens[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
             *M.pos = pos + 1;
@@ -604,32 +884,14 @@ template <int DT> void launch_gemv(const l3m_dmat &m, const void *act, int k, fl
     const int grid = (m.tiles + 4 / S - 1) / (4 / S);
     hipLaunchKernelGGL(k_gemv<DT>, dim3(grid), dim3(NT), smem_bytes(DT, k), st, m, (const uint8_t *)act, k, y, S);
 }
-template <int DT> void launch_qkv(const l3m_dmodel &M, const l3m_dlayer &L, int layer, hipStream_t st) {
-    const int S = pick_split(L.qkv.nb), grid = (L.qkv.tiles + 4 / S - 1) / (4 / S);
-    hipLaunchKernelGGL(k_qkv<DT>, dim3(grid), dim3(NT), smem_bytes(DT, M.dim), st, M, L, layer, layer == 0, S);
+template <int DT> void launch_attn(const l3m_dmodel &M, const l3m_dlayer &L, int layer, hipStream_t st) {
+    hipLaunchKernelGGL(k_attn_block<DT>, dim3(M.n_groups), dim3(NTE), M.lds_a, st, M, L, layer);
 }
-template <int DT> void launch_wo(const l3m_dmodel &M, const l3m_dlayer &L, hipStream_t st) {
-    const int S = pick_split(L.wo.nb), grid = (L.wo.tiles + 4 / S - 1) / (4 / S);
-    hipLaunchKernelGGL(k_wo<DT>, dim3(grid), dim3(NT), smem_bytes(DT, M.dim), st, M, L, S);
-}
-template <int DT> void launch_ffn(const l3m_dmodel &M, const l3m_dlayer &L, hipStream_t st) {
-    const int S = L.gate_up.nb >= 8 ? 2 : 1, grid = L.gate_up.tiles / (4 / S) + (L.gate_up.tiles % (4 / S) ? 1 : 0);
-    hipLaunchKernelGGL(k_ffn<DT>, dim3(grid), dim3(NT), smem_bytes(DT, M.dim), st, M, L, S);
-}
-template <int DT> void launch_down(const l3m_dmodel &M, const l3m_dlayer &L, int advance, hipStream_t st) {
-    const int S = pick_split(L.down.nb), grid = (L.down.tiles + 4 / S - 1) / (4 / S);
-    hipLaunchKernelGGL(k_down<DT>, dim3(grid), dim3(NT), smem_bytes(DT, M.ffn), st, M, L, S, advance);
+template <int DT> void launch_ffn(const l3m_dmodel &M, const l3m_dlayer &L, int advance, hipStream_t st) {
+    hipLaunchKernelGGL(k_ffn_block<DT>, dim3(M.n_chunks), dim3(NTE), M.lds_b, st, M, L, advance);
 }
 template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t st) {
-    const int S = pick_split(M.head.nb), grid = (M.head.tiles + 4 / S - 1) / (4 / S);
-    hipLaunchKernelGGL(k_head<DT>, dim3(grid), dim3(NT), smem_bytes(DT, M.dim), st, M, S, advance);
-}
-void launch_attend(const l3m_dmodel &M, int l, hipStream_t st) {
-    const size_t sm = 4 * ((size_t)M.hd + ((M.ctx + 4) & ~3) + NT + 8);
-    hipLaunchKernelGGL(k_attend, dim3(M.n_heads), dim3(NT), sm, st, M.attn, (const float *)M.q,
-                       (const uint16_t *)(M.kc + (size_t)l * M.n_kv * M.ctx * M.hd),
-                       (const uint16_t *)(M.vc + (size_t)l * M.n_kv * M.ctx * M.hd), 0, (const int *)M.pos, M.hd, M.hd,
-                       M.n_heads / M.n_kv, (size_t)M.ctx * M.hd);
+    hipLaunchKernelGGL(k_head_block<DT>, dim3(M.head_grid), dim3(NTE), M.lds_h, st, M, advance);
 }
 
 }  // namespace
@@ -759,16 +1021,15 @@ int l3m_k_argmax(const float *x, int n, int32_t *out, void *stream) {
     return 0;
 }
 
+unsigned l3m_lds_attn(int dtype, int dim, int ctx, int hd, const l3m_dgroup *g) { return (unsigned)lds_a(dtype, dim, ctx, hd, *g).total; }
+unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c) { return (unsigned)lds_b(dtype, dim, *c).total; }
+unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg) { return (unsigned)lds_h(dtype, dim, nb, tiles_per_wg).total; }
+
 int l3m_step_enqueue(const l3m_dmodel *M, const l3m_dlayer *layers, int with_head, void *stream) {
     hipStream_t st = as_stream(stream);
-    const int dt = layers[0].qkv.dtype;
     for (int l = 0; l < M->n_layers; l++) {
-        const l3m_dlayer &L = layers[l];
-        DISPATCH(dt, launch_qkv, *M, L, l, st);
-        launch_attend(*M, l, st);
-        DISPATCH(dt, launch_wo, *M, L, st);
-        DISPATCH(dt, launch_ffn, *M, L, st);
-        DISPATCH(dt, launch_down, *M, L, !with_head && l == M->n_layers - 1, st);
+        DISPATCH(M->body_dtype, launch_attn, *M, layers[l], l, st);
+        DISPATCH(M->body_dtype, launch_ffn, *M, layers[l], !with_head && l == M->n_layers - 1, st);
     }
     if (with_head) DISPATCH(M->head.dtype, launch_head, *M, 1, st);
     CKL("decode step");
@@ -829,16 +1090,11 @@ struct StepCtx { const l3m_dmodel *M; const l3m_dlayer *L; int kind, layer; };
 static int step_one(void *c, int) {
     StepCtx *s = (StepCtx *)c;
     const l3m_dmodel &M = *s->M;
-    const l3m_dlayer &L = s->L[s->layer];
-    const int dt = L.qkv.dtype;
     hipStream_t st = g_stream;
     switch (s->kind) {
-    case 0: DISPATCH(dt, launch_qkv, M, L, s->layer, st); break;
-    case 1: launch_attend(M, s->layer, st); break;
-    case 2: DISPATCH(dt, launch_wo, M, L, st); break;
-    case 3: DISPATCH(dt, launch_ffn, M, L, st); break;
-    case 4: DISPATCH(dt, launch_down, M, L, 0, st); break;
-    case 5: DISPATCH(M.head.dtype, launch_head, M, 0, st); break;
+    case 0: DISPATCH(M.body_dtype, launch_attn, M, s->L[s->layer], s->layer, st); break;
+    case 1: DISPATCH(M.body_dtype, launch_ffn, M, s->L[s->layer], 0, st); break;
+    case 2: DISPATCH(M.head.dtype, launch_head, M, 0, st); break;
     default: return fail_msg("bad kernel kind");
     }
     CKL("timed kernel");
