@@ -37,6 +37,7 @@ typedef struct {
 typedef struct {
     int          dim, hd, n_heads, n_kv, kv_dim, ffn, vocab, ctx, n_layers, nslots;
     int          n_groups, n_chunks, head_grid, head_tiles_per_wg, body_dtype;
+    int          kv_lds;         // attention copies the K, V rows of its kv heads into LDS (they fit)
     float        eps;
     unsigned     lds_a, lds_b, lds_h;   // dynamic LDS bytes of the three step kernels
     int         *pos;            // [1] position of the step being run
@@ -80,9 +81,11 @@ int    l3m_k_argmax(const float *x, int n, int32_t *out, void *stream);
 // Enqueue one decode step at the device position: per layer the attention block (one workgroup per head
 // group) and the FFN block (one per chunk); with_head adds the final norm, the head and the argmax written
 // to tokens[pos + 1]. Always advances pos. LDS sizes in m must come from l3m_step_lds.
-unsigned l3m_lds_attn(int dtype, int dim, int ctx, int hd, const l3m_dgroup *g);
+unsigned l3m_lds_attn(int dtype, int dim, int ctx, int hd, const l3m_dgroup *g, int kv_lds);
+unsigned l3m_dev_lds_max(void);       // dynamic LDS one workgroup may use on this device
 unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c);
 unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg);
+int      l3m_step_slots(int dtype, int which);   // weight slots per lane (matrix A / B of a step kernel), 64 pairs each
 int l3m_step_enqueue(const l3m_dmodel *m, const l3m_dlayer *layers, int with_head, void *stream);
 
 // Timing (microseconds per launch, hipEvents on the library stream, after one untimed launch).

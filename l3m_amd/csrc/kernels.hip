@@ -30,6 +30,22 @@ __host__ __device__ inline size_t act_size(int dt, int k) {
 }
 __host__ __device__ inline size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
 
+// Reads through explicit global (address space 1) pointers: pointers taken from descriptors in device
+// memory would otherwise be flat, and flat loads also count against the LDS wait counter, so every LDS
+// barrier would wait for the weight stream in flight.
+#define GLOBAL __attribute__((address_space(1)))
+template <class T> __device__ __forceinline__ const GLOBAL T *gp(const void *p) { return (const GLOBAL T *)p; }
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg16(const void *p, size_t i) {
+    const u32x4 v = gp<u32x4>(p)[i];
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 ldg16f(const void *p, size_t i) {
+    const f32x4 v = gp<f32x4>(p)[i];
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // ------------------------------------------------------------------------------------------ scalars
 
 __device__ __forceinline__ float f16_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
@@ -63,15 +79,15 @@ __device__ float lt_elem(const l3m_dmat &m, int r, int i) {
     const size_t slot = ((size_t)(r >> 4) * m.nb + (i >> 5)) * RT + (r & 15);
     const int j = i & 31;
     switch (m.dtype) {
-    case L3M_F32:  return ((const float *)m.q)[slot * 32 + j];
-    case L3M_BF16: return bf16_f32(((const uint16_t *)m.q)[slot * 32 + j]);
-    case L3M_Q8_0: return f16_f32(((const uint16_t *)m.s)[slot]) * (float)((const int8_t *)m.q)[slot * 32 + j];
+    case L3M_F32:  return gp<float>(m.q)[slot * 32 + j];
+    case L3M_BF16: return bf16_f32(gp<uint16_t>(m.q)[slot * 32 + j]);
+    case L3M_Q8_0: return f16_f32(gp<uint16_t>(m.s)[slot]) * (float)gp<int8_t>(m.q)[slot * 32 + j];
     default: {
-        const uint8_t byte = m.q[slot * 16 + (j & 15)];
+        const uint8_t byte = gp<uint8_t>(m.q)[slot * 16 + (j & 15)];
         const int n = j < 16 ? byte & 15 : byte >> 4;
-        if (m.dtype == L3M_Q4_0) return f16_f32(((const uint16_t *)m.s)[slot]) * (float)(n - 8);
+        if (m.dtype == L3M_Q4_0) return f16_f32(gp<uint16_t>(m.s)[slot]) * (float)(n - 8);
         const int8_t e2m1x2[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
-        return e8m0_half(m.s[slot]) * (float)e2m1x2[n];
+        return e8m0_half(gp<uint8_t>(m.s)[slot]) * (float)e2m1x2[n];
     }
     }
 }
@@ -419,61 +435,71 @@ __global__ void __launch_bounds__(NT) k_argmax(const float *x, int n, int32_t *o
 // Per layer: kernel A (one workgroup per head group) = norm + prep + qkv rows + RoPE + KV write +
 // attention + the group's Wo column slice; kernel B (one workgroup per FFN chunk) = norm + prep + gate/up
 // rows + SiLU + prep + the chunk's Wdown column slice. Each writes a partial residual (po, pd); the next
-// kernel adds the partials in index order, so results are run-to-run identical. Workgroups are 1024
-// threads: waves 0-3 build the activation (prologue) while waves 4-15 already hold their weights in
-// flight, loaded into registers at entry because they depend on nothing.
+// kernel adds the partials in a fixed order, so results are run-to-run identical.
+//
+// Every one of the 16 wavefronts of a workgroup runs the same sequence: issue its share of the loads of
+// the incoming partial residuals, then issue its share of the weights (nothing depends on them), then
+// wait for the partials only (loads complete in order), build the normalized activation in LDS, and
+// only then consume the weights. So the weight stream overlaps the prologue instead of following it.
 
-constexpr int NTE = 1024, NWE = NTE / 64, WPRO = 4, WCOMP = NWE - WPRO, NPRO = WPRO * 64;
+constexpr int NTE = 1024, NWE = NTE / 64;
 
-template <int DT> constexpr int nslot_a() { return DT == L3M_F32 ? 2 : DT == L3M_BF16 ? 3 : DT == L3M_Q8_0 ? 5 : 8; }
-template <int DT> constexpr int nslot_b() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 3 : 4; }
+// Weight slots per lane: a step kernel streams matrix A (qkv, gate/up, head rows) and matrix B (Wo,
+// Wdown columns), each through its own register array; 64 (tile, block) pairs per slot and workgroup.
+template <int DT> constexpr int nslot_a() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 5 : 6; }
+template <int DT> constexpr int nslot_b() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 1 : 3; }
 
-// One lane's weights: slot s holds pair p = (cw + s * WCOMP) * 4 + sub of the matrix, where a pair is
-// (tile, block) = (p / nb, p % nb) and the lane reads row (lane & 15) of it: 4 consecutive pairs per
-// wavefront = one contiguous 64 * QBYTES run.
 template <int DT, int NS>
 struct Pref {
     uint4 w[NS][qbytes(DT) / 16];
     uint32_t sc[NS];
 };
 
+// Slot s of this lane holds pair p = (wave + (s0 + s) * NWE) * 4 + sub of m, a pair being (tile, block)
+// = (p / nb, p % nb) and the lane reading row (lane & 15) of it: 4 consecutive pairs = one contiguous
+// 64 * QBYTES run per wavefront. Loads are unconditional (past the end they repeat the last pair) so that
+// no branch ties a load to its use.
 template <int DT, int NS>
-__device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, int cw, int s0, int lane) {
+__device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, int s0) {
     constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
-    const int sub = lane >> 4, row = lane & 15, P = m.tiles * m.nb;
+    const int wave = threadIdx.x >> 6, sub = (threadIdx.x >> 4) & 3, row = threadIdx.x & 15, n = m.tiles * m.nb;
+    if (n <= 0) return;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
-        const int p = (cw + (s0 + s) * WCOMP) * 4 + sub;
-        pf.sc[s] = 0;
-        if (p < P) {
-            const uint4 *src = (const uint4 *)(m.q + ((size_t)p * 16 + row) * QBY);
+        int p = (wave + (s0 + s) * NWE) * 4 + sub;
+        p = p < n ? p : n - 1;
+        const size_t slot = (size_t)p * 16 + row;
 #pragma unroll
-            for (int v = 0; v < NV; v++) pf.w[s][v] = src[v];
-            if constexpr (SBY == 2) pf.sc[s] = ((const uint16_t *)m.s)[(size_t)p * 16 + row];
-            if constexpr (SBY == 1) pf.sc[s] = m.s[(size_t)p * 16 + row];
-        }
+        for (int v = 0; v < NV; v++) pf.w[s][v] = ldg16(m.q, slot * NV + v);
+        if constexpr (SBY == 2) pf.sc[s] = gp<uint16_t>(m.s)[slot];
+        if constexpr (SBY == 1) pf.sc[s] = gp<uint8_t>(m.s)[slot];
+        if constexpr (SBY == 0) pf.sc[s] = 0;
     }
 }
 
+// res[pair * 16 + row] for this lane's slots.
 template <int DT, int NS>
-__device__ __forceinline__ void pref_compute(const Pref<DT, NS> &pf, const l3m_dmat &m, int cw, int s0, int lane,
-                                             const uint8_t *act, int kp, float *res) {
-    const int sub = lane >> 4, row = lane & 15, P = m.tiles * m.nb;
+__device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m, int s0, const uint8_t *act, int kp, float *res) {
+    const int wave = threadIdx.x >> 6, sub = (threadIdx.x >> 4) & 3, row = threadIdx.x & 15, n = m.tiles * m.nb;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
-        const int p = (cw + (s0 + s) * WCOMP) * 4 + sub;
-        if (p < P) res[p * 16 + row] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, p % m.nb);
+        // Pin the loaded registers here: otherwise the compiler hoists their first use (the f16 scale
+        // conversion) up to the loads, and every wavefront stalls on its first load at entry.
+        asm volatile("" : "+v"(pf.sc[s]));
+#pragma unroll
+        for (int v = 0; v < qbytes(DT) / 16; v++) asm volatile("" : "+v"(pf.w[s][v].x), "+v"(pf.w[s][v].y), "+v"(pf.w[s][v].z), "+v"(pf.w[s][v].w));
+        const int p = (wave + (s0 + s) * NWE) * 4 + sub;
+        if (p < n) res[p * 16 + row] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, p % m.nb);
     }
 }
 
-// Compute waves: the prefetched first batch, then any further batches of m. res[pair * 16 + row].
+// All pairs of m: the prefetched batch, then any further batches (loaded here).
 template <int DT, int NS>
-__device__ void mv_pairs(Pref<DT, NS> &pf, const l3m_dmat &m, int cw, int lane, const uint8_t *act, int kp, float *res) {
-    const int P = m.tiles * m.nb;
-    pref_compute<DT, NS>(pf, m, cw, 0, lane, act, kp, res);
-    for (int s0 = NS; s0 * WCOMP * 4 < P; s0 += NS) {
-        pref_load<DT, NS>(pf, m, cw, s0, lane);
-        pref_compute<DT, NS>(pf, m, cw, s0, lane, act, kp, res);
+__device__ void mv(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int kp, float *res) {
+    pref_compute<DT, NS>(pf, m, 0, act, kp, res);
+    for (int s0 = NS; s0 * NWE * 4 < m.tiles * m.nb; s0 += NS) {
+        pref_load<DT, NS>(pf, m, s0);
+        pref_compute<DT, NS>(pf, m, s0, act, kp, res);
     }
 }
 
@@ -487,7 +513,7 @@ __device__ void rows_sum(const l3m_dmat &m, const float *res, float *out, int ro
     }
 }
 
-// Workgroup-wide (all 16 wavefronts) reductions in a fixed order; scr: 16 floats / ints of LDS.
+// Workgroup-wide reductions in a fixed order; scr: 32 words of LDS.
 __device__ float wge_sum(float v, float *scr) {
     for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
     __syncthreads();
@@ -506,56 +532,102 @@ __device__ float wge_max(float v, float *scr) {
     for (int w = 1; w < NWE; w++) t = fmaxf(t, scr[w]);
     return t;
 }
-__device__ void wge_argmax(float &v, int &i, float *sv, int *si) {
+__device__ void wge_argmax(float &v, int &i, float *scr) {
+    int *si = (int *)(scr + 16);
     for (int o = 32; o; o >>= 1) {
         const float v2 = __shfl_xor(v, o);
         const int i2 = __shfl_xor(i, o);
         better(v, i, v2, i2);
     }
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = i; }
+    if ((threadIdx.x & 63) == 0) { scr[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = i; }
     __syncthreads();
-    v = sv[0]; i = si[0];
-    for (int w = 1; w < NWE; w++) better(v, i, sv[w], si[w]);
+    v = scr[0]; i = si[0];
+    for (int w = 1; w < NWE; w++) better(v, i, scr[w], si[w]);
 }
 
-// xs[0, dim) = base + parts[0] + parts[1] + ... in index order (waves 0-3, float4 slots; the loads of
-// a batch of 8 parts are issued before its adds). Optionally also stored to `keep`.
-__device__ void fill_sum(float *xs, const float *base, const float *parts, int nparts, int dim, float *keep) {
-    if (threadIdx.x >= NPRO) return;
-    for (int f = threadIdx.x; f < dim / 4; f += NPRO) {
-        float4 v = ((const float4 *)base)[f];
-        for (int j0 = 0; j0 < nparts; j0 += 8) {
-            float4 p[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (j0 + j < nparts) p[j] = ((const float4 *)(parts + (size_t)(j0 + j) * dim))[f];
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (j0 + j < nparts) { v.x += p[j].x; v.y += p[j].y; v.z += p[j].z; v.w += p[j].w; }
-        }
-        ((float4 *)xs)[f] = v;
-        if (keep) ((float4 *)keep)[f] = v;
+// The incoming residual x = base + parts[0] + ... + parts[n-1] (or, for layer 0, the embedding row of
+// tok). Thread t takes float4 column f = t % (dim/4) and the parts of group t / (dim/4); fill_load only
+// issues its loads, fill_finish (after the weights are issued) adds them: group sums go through LDS and
+// are added in group order.
+constexpr int FILL_PER = 8;
+struct Fill {
+    float4 p[FILL_PER];
+    float4 base;
+    float e;
+};
+struct FillGeom {
+    int n4, groups, per;
+};
+__device__ __forceinline__ FillGeom fill_geom(int dim, int nparts) {
+    FillGeom g;
+    g.n4 = dim / 4;
+    g.groups = NTE / g.n4 < 1 ? 1 : NTE / g.n4;
+    g.per = (nparts + g.groups - 1) / g.groups;
+    if (g.per < 1) g.per = 1;
+    return g;
+}
+// embed (by value: a pointer into the kernel's argument struct would move the whole struct to scratch)
+// is read when use_embed is set.
+__device__ __forceinline__ void fill_load(Fill &F, const float *base, const float *parts, int nparts, int dim, l3m_dmat embed, bool use_embed, int tok) {
+    if (use_embed) {                                         // layer 0: x = dequant(embed[tok]) (engine.c:236)
+        F.e = threadIdx.x < dim ? lt_elem(embed, tok, threadIdx.x) : 0.f;
+        return;
     }
+    const FillGeom G = fill_geom(dim, nparts);
+    const int f = threadIdx.x % G.n4, grp = threadIdx.x / G.n4, j0 = grp * G.per;
+    if (grp < G.groups && grp == 0) F.base = ldg16f(base, f);
+#pragma unroll
+    for (int j = 0; j < FILL_PER; j++)
+        if (grp < G.groups && j < G.per && j0 + j < nparts) F.p[j] = ldg16f(parts + (size_t)(j0 + j) * dim, f);
+}
+// xs[0, dim) = x; also stored to keep when given. pbuf: LDS for the group sums (NTE float4). All threads call.
+__device__ void fill_finish(Fill &F, float *xs, const float *parts, int nparts, int dim, float4 *pbuf, float *keep, bool embed) {
+    if (embed) {
+        if (threadIdx.x < dim) { xs[threadIdx.x] = F.e; if (keep) keep[threadIdx.x] = F.e; }
+        __syncthreads();
+        return;
+    }
+    const FillGeom G = fill_geom(dim, nparts);
+    const int f = threadIdx.x % G.n4, grp = threadIdx.x / G.n4, j0 = grp * G.per;
+    if (grp < G.groups) {
+        float4 v = grp == 0 ? F.base : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < FILL_PER; j++)
+            if (j < G.per && j0 + j < nparts) { v.x += F.p[j].x; v.y += F.p[j].y; v.z += F.p[j].z; v.w += F.p[j].w; }
+        for (int j = FILL_PER; j < G.per && j0 + j < nparts; j++) {   // more parts than one batch: in order
+            const float4 p = ldg16f(parts + (size_t)(j0 + j) * dim, f);
+            v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+        }
+        pbuf[grp * G.n4 + f] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < G.n4) {
+        float4 v = pbuf[threadIdx.x];
+        for (int g = 1; g < G.groups; g++) {
+            const float4 p = pbuf[g * G.n4 + threadIdx.x];
+            v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+        }
+        ((float4 *)xs)[threadIdx.x] = v;
+        if (keep) ((float4 *)keep)[threadIdx.x] = v;
+    }
+    __syncthreads();
 }
 
-// Norm + prep of xs (filled for [0, k) by waves 0-3, padded here): RMSNorm with nw when given
-// (ops.c:13-18), then the activation prep (pack.c:101-123) into act. All threads call it.
+// Norm + prep of xs (x in [0, k)): RMSNorm with nw when given (ops.c:13-18), then the activation prep
+// (pack.c:101-123) into act, padded to kp. All threads call it.
 template <int DT>
 __device__ void norm_prep(float *xs, uint8_t *act, int k, int kp, const float *nw, float eps, float *scr) {
     const int tid = threadIdx.x;
     for (int i = k + tid; i < kp; i += NTE) xs[i] = 0.f;
-    __syncthreads();
     if (nw) {
         float ss = 0.f;
-        if (tid < NPRO)
-            for (int i = tid; i < k; i += NPRO) ss = fmaf(xs[i], xs[i], ss);
+        for (int i = tid; i < k; i += NTE) ss = fmaf(xs[i], xs[i], ss);
         const float tot = wge_sum(ss, scr);
         const float s = 1.0f / sqrtf(tot / (float)k + eps);
-        if (tid < NPRO)
-            for (int i = tid; i < k; i += NPRO) xs[i] = xs[i] * s * nw[i];
-        __syncthreads();
+        for (int i = tid; i < k; i += NTE) xs[i] = xs[i] * s * nw[i];
     }
+    __syncthreads();
     if constexpr (quantized(DT)) {
         const int nb = kp / 32, g = tid >> 3, l = tid & 7;
         float *scale = (float *)(act + kp);
@@ -583,32 +655,38 @@ __device__ void norm_prep(float *xs, uint8_t *act, int k, int kp, const float *n
     __syncthreads();
 }
 
-// LDS regions of the step kernels (byte offsets, 16-aligned) from the layer geometry.
-struct LdsA { size_t xs, act, res, qkv, kv, sc, att, act2, scr, total; };
-__host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g) {
+// LDS regions of the step kernels (byte offsets, 16-aligned) from the layer geometry. `work` holds the
+// prologue's group sums, then the per-pair matvec results, then the attention partials.
+struct LdsA { size_t xs, act, work, qkv, kv, sc, att, act2, scr, kvb, total; };
+__host__ __device__ inline size_t work_bytes(size_t pairs) {
+    const size_t w = 64 * pairs;
+    return align16(w > 16 * (size_t)NTE ? w : 16 * (size_t)NTE);
+}
+__host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g, int kv_lds) {
     LdsA L;
     size_t o = 0;
     const size_t pq = (size_t)g.qkv.tiles * g.qkv.nb, pw = (size_t)g.wo.tiles * g.wo.nb;
     L.xs = o;   o += align16(4 * (size_t)kpad(dim));
     L.act = o;  o += align16(act_size(dt, dim));
-    L.res = o;  o += align16(64 * (pq > pw ? pq : pw));
+    L.work = o; o += work_bytes(pq > pw ? pq : pw);
     L.qkv = o;  o += align16(64 * (size_t)g.qkv.tiles);
     L.kv = o;   o += align16(8 * (size_t)g.nkv * hd);
     L.sc = o;   o += align16(4 * (size_t)(ctx + 4));
     L.att = o;  o += align16(4 * (size_t)kpad(g.nq * hd));
     L.act2 = o; o += align16(act_size(dt, g.nq * hd));
-    L.scr = o;  o += 4 * (NTE + 64);
+    L.scr = o;  o += 4 * 64;
+    L.kvb = o;  o += kv_lds ? align16(4 * (size_t)g.nkv * ctx * hd) : 0;   // [K | V][nkv][ctx][hd] bf16
     L.total = o;
     return L;
 }
-struct LdsB { size_t xs, act, res, gu, h, act2, scr, total; };
+struct LdsB { size_t xs, act, work, gu, h, act2, scr, total; };
 __host__ __device__ inline LdsB lds_b(int dt, int dim, const l3m_dchunk &c) {
     LdsB L;
     size_t o = 0;
     const size_t pg = (size_t)c.gate_up.tiles * c.gate_up.nb, pw = (size_t)c.down.tiles * c.down.nb;
     L.xs = o;   o += align16(4 * (size_t)kpad(dim));
     L.act = o;  o += align16(act_size(dt, dim));
-    L.res = o;  o += align16(64 * (pg > pw ? pg : pw));
+    L.work = o; o += work_bytes(pg > pw ? pg : pw);
     L.gu = o;   o += align16(64 * (size_t)c.gate_up.tiles);
     L.h = o;    o += align16(4 * (size_t)kpad(c.nf));
     L.act2 = o; o += align16(act_size(dt, c.nf));
@@ -616,54 +694,63 @@ __host__ __device__ inline LdsB lds_b(int dt, int dim, const l3m_dchunk &c) {
     L.total = o;
     return L;
 }
-struct LdsH { size_t xs, act, res, y, scr, total; };
+struct LdsH { size_t xs, act, work, y, scr, total; };
 __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg) {
     LdsH L;
     size_t o = 0;
-    L.xs = o;  o += align16(4 * (size_t)kpad(dim));
-    L.act = o; o += align16(act_size(dt, dim));
-    L.res = o; o += align16(64 * (size_t)tiles_per_wg * nb);
-    L.y = o;   o += align16(64 * (size_t)tiles_per_wg);
-    L.scr = o; o += 4 * 64;
+    L.xs = o;   o += align16(4 * (size_t)kpad(dim));
+    L.act = o;  o += align16(act_size(dt, dim));
+    L.work = o; o += work_bytes((size_t)tiles_per_wg * nb);
+    L.y = o;    o += align16(64 * (size_t)tiles_per_wg);
+    L.scr = o;  o += 4 * 64;
     L.total = o;
     return L;
 }
 
-// Kernel A: the attention block of one head group (engine.c:241-258).
+// K and V rows 0..pos-1 of the group's kv heads, copied from the cache into LDS [K | V][nkv][ctx][hd] by
+// the memory unit (global_load_lds_dwordx4: 64 lanes x 16 bytes into 1 KiB of LDS, no registers).
+// Rows up to pos - 1 were written by earlier steps, so the copy can start at the top of the kernel.
+__device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int kv0, int nkv, int pos) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const size_t win = (size_t)M.ctx * M.hd, total = (size_t)pos * M.hd * 2;     // bytes per head, K or V
+    const int nch = (int)((total + 1023) / 1024), items = 2 * nkv * nch;
+    for (int it = wave; it < items; it += NWE) {
+        const int which = it / (nkv * nch), rem = it % (nkv * nch), j = rem / nch, c = rem % nch;
+        const size_t byte = (size_t)c * 1024 + (size_t)lane * 16;
+        const uint16_t *src = (which ? M.vc : M.kc) + ((size_t)layer * M.n_kv + kv0 + j) * win;
+        uint8_t *dst = (uint8_t *)(kvb + ((size_t)which * nkv + j) * win) + (size_t)c * 1024;
+        if (byte < total)
+            __builtin_amdgcn_global_load_lds((const GLOBAL void *)((const uint8_t *)src + byte),
+                                             (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+    }
+}
+
+// Kernel A: the attention block of one head group (engine.c:236-258).
 template <int DT>
 __global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw, int layer) {
     extern __shared__ __align__(16) uint8_t smem[];
     const l3m_dgroup G = Lw.groups[blockIdx.x];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, cw = wave - WPRO;
-    Pref<DT, nslot_a<DT>()> pa;
-    Pref<DT, nslot_b<DT>()> pb;
-    if (wave >= WPRO) {
-        pref_load<DT, nslot_a<DT>()>(pa, G.qkv, cw, 0, lane);
-        pref_load<DT, nslot_b<DT>()>(pb, G.wo, cw, 0, lane);
-    }
-    const int pos = *M.pos, dim = M.dim, hd = M.hd, kp = kpad(dim);
-    const LdsA L = lds_a(DT, dim, M.ctx, hd, G);
-    float *xs = (float *)(smem + L.xs), *res = (float *)(smem + L.res), *qkv = (float *)(smem + L.qkv);
+    const int tid = threadIdx.x, pos = *M.pos, dim = M.dim, hd = M.hd, kp = kpad(dim);
+    const LdsA L = lds_a(DT, dim, M.ctx, hd, G, M.kv_lds);
+    float *xs = (float *)(smem + L.xs), *work = (float *)(smem + L.work), *qkv = (float *)(smem + L.qkv);
     float *kvc = (float *)(smem + L.kv), *sc = (float *)(smem + L.sc), *att = (float *)(smem + L.att), *scr = (float *)(smem + L.scr);
     uint8_t *act = smem + L.act, *act2 = smem + L.act2;
 
-    // layer input: the embedding row (engine.c:236) or xb + the previous FFN partials; group 0 keeps it in xa
-    if (layer == 0) {
-        const int tok = M.tokens[pos];
-        if (tid < NPRO)
-            for (int i = tid; i < dim; i += NPRO) {
-                xs[i] = lt_elem(M.embed, tok, i);
-                if (blockIdx.x == 0) M.xa[i] = xs[i];
-            }
-    } else {
-        fill_sum(xs, M.xb, M.pd, M.n_chunks, dim, blockIdx.x == 0 ? M.xa : nullptr);
-    }
+    Fill F;
+    fill_load(F, M.xb, M.pd, M.n_chunks, dim, M.embed, layer == 0, layer ? 0 : M.tokens[pos]);
+    Pref<DT, nslot_a<DT>()> pa;
+    Pref<DT, nslot_b<DT>()> pb;
+    pref_load<DT, nslot_a<DT>()>(pa, G.qkv, 0);
+    pref_load<DT, nslot_b<DT>()>(pb, G.wo, 0);
+    fill_finish(F, xs, M.pd, M.n_chunks, dim, (float4 *)work, blockIdx.x == 0 ? M.xa : nullptr, layer == 0);
+    uint16_t *kvb = (uint16_t *)(smem + L.kvb);
+    if (M.kv_lds) kv_window_dma(kvb, M, layer, G.kv0, G.nkv, pos);   // K, V rows 0..pos-1: no dependence on this step
     norm_prep<DT>(xs, act, dim, kp, Lw.attn_norm, M.eps, scr);
 
-    if (wave >= WPRO) mv_pairs<DT, nslot_a<DT>()>(pa, G.qkv, cw, lane, act, kp, res);
+    mv<DT, nslot_a<DT>()>(pa, G.qkv, act, kp, work);
     __syncthreads();
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
-    rows_sum(G.qkv, res, qkv, nqd + 2 * nkd);
+    rows_sum(G.qkv, work, qkv, nqd + 2 * nkd);
     __syncthreads();
 
     // RoPE on q and k: pairs (2i, 2i+1) of each head by the table angle i (ops.c:29-40)
@@ -689,21 +776,25 @@ __global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw,
     }
     __syncthreads();
 
-    // attention of each query head over positions 0..pos (ops.c:58-73); position pos from LDS
+    // attention of each query head over positions 0..pos (ops.c:58-73): rows before pos from the LDS
+    // window (kv_lds) or from the cache, row pos from kvc
+    if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     const float scale = 1.0f / sqrtf((float)hd);
-    const int hpk = M.n_heads / M.n_kv, groups = NTE / hd, gi = tid / hd, ii = tid % hd;
+    const int hpk = M.n_heads / M.n_kv, groups = NTE / hd, gi = tid / hd, ii = tid % hd, nv = hd / 8;
+    const size_t win = (size_t)M.ctx * hd;
     for (int h = 0; h < G.nq; h++) {
         const int kvl = (G.q0 + h) / hpk - G.kv0;
         const float *q = qkv + h * hd;
-        const uint16_t *kh = M.kc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx * hd;
-        const uint16_t *vh = M.vc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx * hd;
+        const uint16_t *kh = M.kv_lds ? kvb + kvl * win : M.kc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
+        const uint16_t *vh = M.kv_lds ? kvb + (G.nkv + kvl) * win : M.vc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
         float mx = -INFINITY;
         for (int t = tid; t <= pos; t += NTE) {
             float dot = 0.f;
             if (t < pos) {
-                const uint4 *kr = (const uint4 *)(kh + (size_t)t * hd);
-                for (int v = 0; v < hd / 8; v++) {
-                    const uint4 kk = kr[v];
+                const uint16_t *kr = kh + (size_t)t * hd;
+                for (int v = 0; v < nv; v++) {
+                    const uint4 kk = M.kv_lds ? ((const uint4 *)kr)[v] : ldg16(kr, v);
                     const float *qq = q + v * 8;
                     dot = fmaf(qq[0], bf16_f32(kk.x & 0xFFFF), dot); dot = fmaf(qq[1], bf16_f32(kk.x >> 16), dot);
                     dot = fmaf(qq[2], bf16_f32(kk.y & 0xFFFF), dot); dot = fmaf(qq[3], bf16_f32(kk.y >> 16), dot);
@@ -729,22 +820,25 @@ __global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw,
         __syncthreads();
         float acc = 0.f;
         if (gi < groups)
-            for (int t = gi; t <= pos; t += groups)
-                acc = fmaf(sc[t], t < pos ? bf16_f32(vh[(size_t)t * hd + ii]) : kvc[nkd + kvl * hd + ii], acc);
-        scr[64 + tid] = acc;
+            for (int t = gi; t <= pos; t += groups) {
+                const float v = t == pos ? kvc[nkd + kvl * hd + ii]
+                              : bf16_f32(M.kv_lds ? vh[(size_t)t * hd + ii] : gp<uint16_t>(vh)[(size_t)t * hd + ii]);
+                acc = fmaf(sc[t], v, acc);
+            }
+        work[tid] = acc;
         __syncthreads();
         if (tid < hd) {
-            float o = scr[64 + tid];
-            for (int g = 1; g < groups; g++) o += scr[64 + g * hd + tid];
+            float o = work[tid];
+            for (int g = 1; g < groups; g++) o += work[g * hd + tid];
             att[h * hd + tid] = o;
         }
         __syncthreads();
     }
     // prep of the group's attention output, then its Wo columns -> the partial residual po[group]
     norm_prep<DT>(att, act2, nqd, kpad(nqd), nullptr, 0.f, scr);
-    if (wave >= WPRO) mv_pairs<DT, nslot_b<DT>()>(pb, G.wo, cw, lane, act2, kpad(nqd), res);
+    mv<DT, nslot_b<DT>()>(pb, G.wo, act2, kpad(nqd), work);
     __syncthreads();
-    rows_sum(G.wo, res, M.po + (size_t)blockIdx.x * dim, dim);
+    rows_sum(G.wo, work, M.po + (size_t)blockIdx.x * dim, dim);
 }
 
 // Kernel B: the FFN block of one chunk of ffn rows (engine.c:259-275). The last layer of a step without
@@ -753,31 +847,31 @@ template <int DT>
 __global__ void __launch_bounds__(NTE) k_ffn_block(l3m_dmodel M, l3m_dlayer Lw, int advance) {
     extern __shared__ __align__(16) uint8_t smem[];
     const l3m_dchunk C = Lw.chunks[blockIdx.x];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, cw = wave - WPRO;
-    Pref<DT, nslot_a<DT>()> pa;
-    Pref<DT, nslot_b<DT>()> pb;
-    if (wave >= WPRO) {
-        pref_load<DT, nslot_a<DT>()>(pa, C.gate_up, cw, 0, lane);
-        pref_load<DT, nslot_b<DT>()>(pb, C.down, cw, 0, lane);
-    }
-    const int dim = M.dim, kp = kpad(dim);
+    const int tid = threadIdx.x, dim = M.dim, kp = kpad(dim);
     const LdsB L = lds_b(DT, dim, C);
-    float *xs = (float *)(smem + L.xs), *res = (float *)(smem + L.res), *gu = (float *)(smem + L.gu);
+    float *xs = (float *)(smem + L.xs), *work = (float *)(smem + L.work), *gu = (float *)(smem + L.gu);
     float *h = (float *)(smem + L.h), *scr = (float *)(smem + L.scr);
     uint8_t *act = smem + L.act, *act2 = smem + L.act2;
 
-    fill_sum(xs, M.xa, M.po, M.n_groups, dim, blockIdx.x == 0 ? M.xb : nullptr);   // x += proj (engine.c:259)
+    Fill F;
+    fill_load(F, M.xa, M.po, M.n_groups, dim, M.embed, false, 0);     // x += proj (engine.c:259)
+    Pref<DT, nslot_a<DT>()> pa;
+    Pref<DT, nslot_b<DT>()> pb;
+    pref_load<DT, nslot_a<DT>()>(pa, C.gate_up, 0);
+    pref_load<DT, nslot_b<DT>()>(pb, C.down, 0);
+    fill_finish(F, xs, M.po, M.n_groups, dim, (float4 *)work, blockIdx.x == 0 ? M.xb : nullptr, false);
     norm_prep<DT>(xs, act, dim, kp, Lw.ffn_norm, M.eps, scr);
-    if (wave >= WPRO) mv_pairs<DT, nslot_a<DT>()>(pa, C.gate_up, cw, lane, act, kp, res);
+    mv<DT, nslot_a<DT>()>(pa, C.gate_up, act, kp, work);
     __syncthreads();
-    rows_sum(C.gate_up, res, gu, C.gate_up.rows);
+    rows_sum(C.gate_up, work, gu, C.gate_up.rows);
     __syncthreads();
-    if (tid < NPRO)                                         // h = up * silu(gate) (ops.c:49-51)
-        for (int i = tid; i < C.nf; i += NPRO) h[i] = silu_mul(gu[(2 * (i >> 4) + 1) * 16 + (i & 15)], gu[(2 * (i >> 4)) * 16 + (i & 15)]);
+    for (int i = tid; i < C.nf; i += NTE)                           // h = up * silu(gate) (ops.c:49-51)
+        h[i] = silu_mul(gu[(2 * (i >> 4) + 1) * 16 + (i & 15)], gu[(2 * (i >> 4)) * 16 + (i & 15)]);
+    __syncthreads();
     norm_prep<DT>(h, act2, C.nf, kpad(C.nf), nullptr, 0.f, scr);
-    if (wave >= WPRO) mv_pairs<DT, nslot_b<DT>()>(pb, C.down, cw, lane, act2, kpad(C.nf), res);
+    mv<DT, nslot_b<DT>()>(pb, C.down, act2, kpad(C.nf), work);
     __syncthreads();
-    rows_sum(C.down, res, M.pd + (size_t)blockIdx.x * dim, dim);
+    rows_sum(C.down, work, M.pd + (size_t)blockIdx.x * dim, dim);
     if (advance && blockIdx.x == 0 && tid == 0) *M.pos += 1;
 }
 
@@ -787,31 +881,33 @@ __global__ void __launch_bounds__(NTE) k_ffn_block(l3m_dmodel M, l3m_dlayer Lw, 
 template <int DT>
 __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, cw = wave - WPRO;
-    const int tpw = M.head_tiles_per_wg, t0 = blockIdx.x * tpw;
+    const int tid = threadIdx.x, tpw = M.head_tiles_per_wg, t0 = blockIdx.x * tpw;
     l3m_dmat V = M.head;                                    // this workgroup's tiles of the head
     const int nt = t0 + tpw <= V.tiles ? tpw : V.tiles - t0;
     V.q += (size_t)t0 * V.nb * 16 * qbytes(DT);
     if (sbytes(DT)) V.s += (size_t)t0 * V.nb * 16 * sbytes(DT);
-    V.tiles = nt > 0 ? nt : 0;
-    V.rows = V.tiles * 16 < M.vocab - t0 * 16 ? V.tiles * 16 : M.vocab - t0 * 16;
-    Pref<DT, nslot_a<DT>()> pa;
-    if (wave >= WPRO && nt > 0) pref_load<DT, nslot_a<DT>()>(pa, V, cw, 0, lane);
+    V.tiles = nt;
+    V.rows = nt * 16 < M.vocab - t0 * 16 ? nt * 16 : M.vocab - t0 * 16;
     const int pos = *M.pos, dim = M.dim, kp = kpad(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
-    float *xs = (float *)(smem + L.xs), *res = (float *)(smem + L.res), *y = (float *)(smem + L.y), *scr = (float *)(smem + L.scr);
+    float *xs = (float *)(smem + L.xs), *work = (float *)(smem + L.work), *y = (float *)(smem + L.y), *scr = (float *)(smem + L.scr);
     uint8_t *act = smem + L.act;
-    fill_sum(xs, M.xb, M.pd, M.n_chunks, dim, nullptr);     // x += down (engine.c:275), last layer
+
+    Fill F;
+    fill_load(F, M.xb, M.pd, M.n_chunks, dim, M.embed, false, 0);     // x += down (engine.c:275), last layer
+    Pref<DT, nslot_a<DT>() + nslot_b<DT>()> pa;
+    pref_load<DT, nslot_a<DT>() + nslot_b<DT>()>(pa, V, 0);
+    fill_finish(F, xs, M.pd, M.n_chunks, dim, (float4 *)work, nullptr, false);
     norm_prep<DT>(xs, act, dim, kp, M.norm, M.eps, scr);
-    if (wave >= WPRO && nt > 0) mv_pairs<DT, nslot_a<DT>()>(pa, V, cw, lane, act, kp, res);
+    mv<DT, nslot_a<DT>() + nslot_b<DT>()>(pa, V, act, kp, work);
     __syncthreads();
-    if (nt > 0) rows_sum(V, res, y, V.rows);
+    rows_sum(V, work, y, V.rows);
     __syncthreads();
     float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab + (size_t)t0 * 16;
     float v = -INFINITY;
     int idx = 0x7FFFFFFF;
-    if (nt > 0 && tid < V.rows) { lg[tid] = y[tid]; v = y[tid]; idx = t0 * 16 + tid; }
-    wge_argmax(v, idx, scr, (int *)(scr + 16));
+    if (tid < V.rows) { lg[tid] = y[tid]; v = y[tid]; idx = t0 * 16 + tid; }
+    wge_argmax(v, idx, scr);
     __shared__ int last;
     if (tid == 0) {
         M.part_val[blockIdx.x] = v;
@@ -829,7 +925,7 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
         const int pi = __hip_atomic_load(M.part_idx + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         better(v, idx, pv, pi);
     }
-    wge_argmax(v, idx, scr, (int *)(scr + 16));
+    wge_argmax(v, idx, scr);
     if (tid == 0) {
         if (advance) {
             M.tokens[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
@@ -846,6 +942,7 @@ int g_has_err;
 hipStream_t g_stream;
 int g_ready = -1;
 char g_name[128];
+unsigned g_lds_max = 65536;
 
 int fail(const char *what, hipError_t e) {
     if (!g_has_err) {
@@ -884,13 +981,20 @@ template <int DT> void launch_gemv(const l3m_dmat &m, const void *act, int k, fl
     const int grid = (m.tiles + 4 / S - 1) / (4 / S);
     hipLaunchKernelGGL(k_gemv<DT>, dim3(grid), dim3(NT), smem_bytes(DT, k), st, m, (const uint8_t *)act, k, y, S);
 }
+// Kernels that take more than 64 KiB of dynamic LDS declare it once.
+template <class K> void lds_opt_in(K kernel, unsigned bytes) {
+    if (bytes > 65536) (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
 template <int DT> void launch_attn(const l3m_dmodel &M, const l3m_dlayer &L, int layer, hipStream_t st) {
+    lds_opt_in(k_attn_block<DT>, M.lds_a);
     hipLaunchKernelGGL(k_attn_block<DT>, dim3(M.n_groups), dim3(NTE), M.lds_a, st, M, L, layer);
 }
 template <int DT> void launch_ffn(const l3m_dmodel &M, const l3m_dlayer &L, int advance, hipStream_t st) {
+    lds_opt_in(k_ffn_block<DT>, M.lds_b);
     hipLaunchKernelGGL(k_ffn_block<DT>, dim3(M.n_chunks), dim3(NTE), M.lds_b, st, M, L, advance);
 }
 template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t st) {
+    lds_opt_in(k_head_block<DT>, M.lds_h);
     hipLaunchKernelGGL(k_head_block<DT>, dim3(M.head_grid), dim3(NTE), M.lds_h, st, M, advance);
 }
 
@@ -920,6 +1024,8 @@ int l3m_dev_init(void) {
         return fail_msg(msg);
     }
     CK(hipSetDevice(0));
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, 0) == hipSuccess && lds > 0) g_lds_max = (unsigned)lds;
     CK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     hipLaunchKernelGGL(k_dummy, dim3(1), dim3(NT), 0, g_stream);
     CKL("first launch");
@@ -931,6 +1037,7 @@ int l3m_dev_init(void) {
 const char *l3m_dev_error(void) { return g_has_err ? g_err : NULL; }
 void l3m_dev_clear_error(void) { g_has_err = 0; g_err[0] = 0; }
 const char *l3m_dev_name(void) { return g_name; }
+unsigned l3m_dev_lds_max(void) { return l3m_dev_init() ? 65536u : g_lds_max; }
 void *l3m_dev_stream(void) { return (void *)g_stream; }
 
 void *l3m_dev_alloc(size_t bytes) {
@@ -1021,9 +1128,13 @@ int l3m_k_argmax(const float *x, int n, int32_t *out, void *stream) {
     return 0;
 }
 
-unsigned l3m_lds_attn(int dtype, int dim, int ctx, int hd, const l3m_dgroup *g) { return (unsigned)lds_a(dtype, dim, ctx, hd, *g).total; }
+unsigned l3m_lds_attn(int dtype, int dim, int ctx, int hd, const l3m_dgroup *g, int kv_lds) { return (unsigned)lds_a(dtype, dim, ctx, hd, *g, kv_lds).total; }
 unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c) { return (unsigned)lds_b(dtype, dim, *c).total; }
 unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg) { return (unsigned)lds_h(dtype, dim, nb, tiles_per_wg).total; }
+int l3m_step_slots(int dtype, int which) {
+    if (which) return dtype == L3M_F32 ? nslot_b<L3M_F32>() : dtype == L3M_BF16 ? nslot_b<L3M_BF16>() : dtype == L3M_Q8_0 ? nslot_b<L3M_Q8_0>() : nslot_b<L3M_Q4_0>();
+    return dtype == L3M_F32 ? nslot_a<L3M_F32>() : dtype == L3M_BF16 ? nslot_a<L3M_BF16>() : dtype == L3M_Q8_0 ? nslot_a<L3M_Q8_0>() : nslot_a<L3M_Q4_0>();
+}
 
 int l3m_step_enqueue(const l3m_dmodel *M, const l3m_dlayer *layers, int with_head, void *stream) {
     hipStream_t st = as_stream(stream);
