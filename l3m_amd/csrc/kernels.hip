@@ -37,6 +37,7 @@ __host__ __device__ inline size_t align16(size_t n) { return (n + 15) & ~(size_t
 template <class T> __device__ __forceinline__ const GLOBAL T *gp(const void *p) { return (const GLOBAL T *)p; }
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 ldg16(const void *p, size_t i) {
     const u32x4 v = gp<u32x4>(p)[i];
     return make_uint4(v.x, v.y, v.z, v.w);
@@ -74,20 +75,32 @@ __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
-// Element i of row r of a lane-tile matrix, exactly dequantized (the reference's dequant_row, pack.c:55-62).
-__device__ float lt_elem(const l3m_dmat &m, int r, int i) {
+// Elements i..i+3 (i a multiple of 4) of row r of a lane-tile matrix, exactly dequantized (the
+// reference's dequant_row, pack.c:55-62): one block, loaded together.
+__device__ float4 lt_elem4(const l3m_dmat &m, int r, int i) {
     const size_t slot = ((size_t)(r >> 4) * m.nb + (i >> 5)) * RT + (r & 15);
     const int j = i & 31;
     switch (m.dtype) {
-    case L3M_F32:  return gp<float>(m.q)[slot * 32 + j];
-    case L3M_BF16: return bf16_f32(gp<uint16_t>(m.q)[slot * 32 + j]);
-    case L3M_Q8_0: return f16_f32(gp<uint16_t>(m.s)[slot]) * (float)gp<int8_t>(m.q)[slot * 32 + j];
+    case L3M_F32: return ldg16f(m.q, slot * 8 + (j >> 2));
+    case L3M_BF16: {
+        const u32x2 v = gp<u32x2>(m.q)[slot * 8 + (j >> 2)];      // 32 bf16 = 8 x 8 bytes per slot
+        return make_float4(bf16_f32(v.x & 0xFFFF), bf16_f32(v.x >> 16), bf16_f32(v.y & 0xFFFF), bf16_f32(v.y >> 16));
+    }
+    case L3M_Q8_0: {
+        const float d = f16_f32(gp<uint16_t>(m.s)[slot]);
+        const uint32_t v = gp<uint32_t>(m.q)[slot * 8 + (j >> 2)];
+        return make_float4(d * (float)(int8_t)v, d * (float)(int8_t)(v >> 8), d * (float)(int8_t)(v >> 16), d * (float)(int8_t)(v >> 24));
+    }
     default: {
-        const uint8_t byte = gp<uint8_t>(m.q)[slot * 16 + (j & 15)];
-        const int n = j < 16 ? byte & 15 : byte >> 4;
-        if (m.dtype == L3M_Q4_0) return f16_f32(gp<uint16_t>(m.s)[slot]) * (float)(n - 8);
+        const uint32_t b = gp<uint32_t>(m.q)[slot * 4 + ((j & 15) >> 2)], n = j < 16 ? b & 0x0F0F0F0Fu : (b >> 4) & 0x0F0F0F0Fu;
+        if (m.dtype == L3M_Q4_0) {
+            const float d = f16_f32(gp<uint16_t>(m.s)[slot]);
+            return make_float4(d * (float)((int)(n & 15) - 8), d * (float)((int)(n >> 8 & 15) - 8), d * (float)((int)(n >> 16 & 15) - 8),
+                               d * (float)((int)(n >> 24) - 8));
+        }
+        const float d = e8m0_half(gp<uint8_t>(m.s)[slot]);
         const int8_t e2m1x2[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
-        return e8m0_half(gp<uint8_t>(m.s)[slot]) * (float)e2m1x2[n];
+        return make_float4(d * (float)e2m1x2[n & 15], d * (float)e2m1x2[n >> 8 & 15], d * (float)e2m1x2[n >> 16 & 15], d * (float)e2m1x2[n >> 24]);
     }
     }
 }
@@ -448,6 +461,8 @@ constexpr int NTE = 1024, NWE = NTE / 64;
 // Wdown columns), each through its own register array; 64 (tile, block) pairs per slot and workgroup.
 template <int DT> constexpr int nslot_a() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 5 : 6; }
 template <int DT> constexpr int nslot_b() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 1 : 3; }
+// The attention block keeps its Wo slots live through the attention; q8_0 gives one up to stay in registers.
+template <int DT> constexpr int nslot_wo() { return DT == L3M_Q8_0 ? 2 : nslot_b<DT>(); }
 
 template <int DT, int NS>
 struct Pref {
@@ -458,12 +473,12 @@ struct Pref {
 // Slot s of this lane holds pair p = (wave + (s0 + s) * NWE) * 4 + sub of m, a pair being (tile, block)
 // = (p / nb, p % nb) and the lane reading row (lane & 15) of it: 4 consecutive pairs = one contiguous
 // 64 * QBYTES run per wavefront. Loads are unconditional (past the end they repeat the last pair) so that
-// no branch ties a load to its use.
+// no branch ties a load to its use (a branch around them would make the compiler copy the loaded
+// registers at the join, which waits for the loads). m has at least one pair.
 template <int DT, int NS>
 __device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, int s0) {
     constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
     const int wave = threadIdx.x >> 6, sub = (threadIdx.x >> 4) & 3, row = threadIdx.x & 15, n = m.tiles * m.nb;
-    if (n <= 0) return;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         int p = (wave + (s0 + s) * NWE) * 4 + sub;
@@ -503,175 +518,270 @@ __device__ void mv(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int 
     }
 }
 
-// out[r] = sum over the row's blocks, in block order (all threads), for r < rows.
-__device__ void rows_sum(const l3m_dmat &m, const float *res, float *out, int rows) {
-    for (int i = threadIdx.x; i < rows; i += NTE) {
-        const float *p = res + (size_t)(i >> 4) * m.nb * 16 + (i & 15);
-        float y = p[0];
-        for (int b = 1; b < m.nb; b++) y += p[b * 16];
-        out[i] = y;
-    }
+// ------------------------------------------------------------------------------ cross-lane sums
+// DPP and gfx950 permlane swaps: every lane of an aligned group of N lanes gets the group's sum (max),
+// added in one fixed order, so the value is identical in every lane and every run. All 64 lanes of the
+// wavefront must be active.
+template <int C> __device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), C, 0xF, 0xF, false));
+}
+template <int C> __device__ __forceinline__ int dppi(int v) { return __builtin_amdgcn_update_dpp(0, v, C, 0xF, 0xF, false); }
+// (lanes with bit 4 clear, lanes with bit 4 set) of each 32, and (lanes 0-31, lanes 32-63)
+__device__ __forceinline__ void swap16(float v, float &lo, float &hi) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(r[0]); hi = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap32(float v, float &lo, float &hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(r[0]); hi = __uint_as_float(r[1]);
+}
+constexpr int QP_X1 = 0xB1, QP_X2 = 0x4E, ROW_HALF_MIRROR = 0x141, ROW_MIRROR = 0x140, ROW_ROR4 = 0x124, ROW_ROR8 = 0x128;
+
+template <int N> __device__ __forceinline__ float lanes_sum(float v) {
+    if constexpr (N >= 2) v += dppf<QP_X1>(v);
+    if constexpr (N >= 4) v += dppf<QP_X2>(v);
+    if constexpr (N >= 8) v += dppf<ROW_HALF_MIRROR>(v);
+    if constexpr (N >= 16) v += dppf<ROW_MIRROR>(v);
+    if constexpr (N >= 32) { float lo, hi; swap16(v, lo, hi); v = lo + hi; }
+    if constexpr (N >= 64) { float lo, hi; swap32(v, lo, hi); v = lo + hi; }
+    return v;
+}
+template <int N> __device__ __forceinline__ float lanes_max(float v) {
+    if constexpr (N >= 2) v = fmaxf(v, dppf<QP_X1>(v));
+    if constexpr (N >= 4) v = fmaxf(v, dppf<QP_X2>(v));
+    if constexpr (N >= 8) v = fmaxf(v, dppf<ROW_HALF_MIRROR>(v));
+    if constexpr (N >= 16) v = fmaxf(v, dppf<ROW_MIRROR>(v));
+    if constexpr (N >= 32) { float lo, hi; swap16(v, lo, hi); v = fmaxf(lo, hi); }
+    if constexpr (N >= 64) { float lo, hi; swap32(v, lo, hi); v = fmaxf(lo, hi); }
+    return v;
+}
+template <int N> __device__ __forceinline__ int lanes_sumi(int v) {
+    if constexpr (N >= 2) v += dppi<QP_X1>(v);
+    if constexpr (N >= 4) v += dppi<QP_X2>(v);
+    if constexpr (N >= 8) v += dppi<ROW_HALF_MIRROR>(v);
+    return v;
+}
+// Sum over groups of n (4, 8, 16 or 32; uniform) aligned lanes.
+__device__ __forceinline__ float lanes_sum_n(float v, int n) {
+    v = lanes_sum<4>(v);
+    if (n >= 8) v += dppf<ROW_HALF_MIRROR>(v);
+    if (n >= 16) v += dppf<ROW_MIRROR>(v);
+    if (n >= 32) { float lo, hi; swap16(v, lo, hi); v = lo + hi; }
+    return v;
+}
+// Sum over the lanes of a wavefront that share (lane % n), n = 4, 8, 16 or 32 (uniform); lanes
+// with lane < n hold the results.
+__device__ __forceinline__ float strided_sum(float v, int n) {
+    float lo, hi;
+    if (n <= 4) v += dppf<ROW_ROR4>(v);
+    if (n <= 8) v += dppf<ROW_ROR8>(v);
+    if (n <= 16) { swap16(v, lo, hi); v = lo + hi; }
+    swap32(v, lo, hi);
+    return lo + hi;
 }
 
-// Workgroup-wide reductions in a fixed order; scr: 32 words of LDS.
-__device__ float wge_sum(float v, float *scr) {
-    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+// Workgroup (16 wavefronts) reductions, one barrier each: the wavefront results go to one of two
+// 16-float slots of scr, used alternately, so a slot is only rewritten after every thread has passed
+// the barrier of the reduction in between. All threads call them, in the same order.
+struct Red {
+    float *scr;    // 32 floats of LDS
+    int k;
+};
+__device__ __forceinline__ const float *red_publish(Red &r, float v) {
+    float *s = r.scr + 16 * (r.k++ & 1);
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = v;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) scr[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = scr[0];
-    for (int w = 1; w < NWE; w++) t += scr[w];
-    return t;
+    return s;
 }
-__device__ float wge_max(float v, float *scr) {
-    for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) scr[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = scr[0];
-    for (int w = 1; w < NWE; w++) t = fmaxf(t, scr[w]);
-    return t;
+__device__ float red_sum(Red &r, float v) {
+    const float4 *s = (const float4 *)red_publish(r, lanes_sum<64>(v));
+    const float4 a = s[0], b = s[1], c = s[2], d = s[3];
+    return (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) + (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
 }
-__device__ void wge_argmax(float &v, int &i, float *scr) {
-    int *si = (int *)(scr + 16);
+__device__ float red_max(Red &r, float v) {
+    const float4 *s = (const float4 *)red_publish(r, lanes_max<64>(v));
+    const float4 a = s[0], b = s[1], c = s[2], d = s[3];
+    return fmaxf(fmaxf(fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)), fmaxf(fmaxf(b.x, b.y), fmaxf(b.z, b.w))),
+                 fmaxf(fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w)), fmaxf(fmaxf(d.x, d.y), fmaxf(d.z, d.w))));
+}
+// (value, index) maximum with the reference's tie rule (better()); sv, si: 16 words each.
+__device__ void wge_argmax(float &v, int &i, float *sv, int *si) {
     for (int o = 32; o; o >>= 1) {
         const float v2 = __shfl_xor(v, o);
         const int i2 = __shfl_xor(i, o);
         better(v, i, v2, i2);
     }
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) { scr[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = i; }
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = i; }
     __syncthreads();
-    v = scr[0]; i = si[0];
-    for (int w = 1; w < NWE; w++) better(v, i, scr[w], si[w]);
+    v = sv[0]; i = si[0];
+    for (int w = 1; w < NWE; w++) better(v, i, sv[w], si[w]);
 }
 
+// Matvec results res[pair * 16 + row] summed per row in block order by 4 adjacent lanes (each a
+// quarter of the blocks, quarters added pairwise); every lane of the quad gets the row's value y.
+// f(i, y, partner) runs in every lane for rows i < rows, partner being row i ^ 1's value.
+template <class F>
+__device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, int rows, F f) {
+    const int nb = m.nb, q = threadIdx.x & 3, b0 = q * nb >> 2, b1 = (q + 1) * nb >> 2;
+    for (int base = 0; base < rows; base += NTE / 4) {
+        const int i = base + (threadIdx.x >> 2);
+        float y = 0.f;
+        if (i < rows) {
+            const float *p = res + (size_t)(i >> 4) * nb * 16 + (i & 15);
+#pragma unroll 4
+            for (int b = b0; b < b1; b++) y += p[b * 16];
+        }
+        y = lanes_sum<4>(y);
+        const float partner = dppf<ROW_HALF_MIRROR>(y);
+        if (i < rows) f(i, y, partner);
+    }
+}
+
+// ----------------------------------------------------------------------------------- prologue
 // The incoming residual x = base + parts[0] + ... + parts[n-1] (or, for layer 0, the embedding row of
-// tok). Thread t takes float4 column f = t % (dim/4) and the parts of group t / (dim/4); fill_load only
-// issues its loads, fill_finish (after the weights are issued) adds them: group sums go through LDS and
-// are added in group order.
-constexpr int FILL_PER = 8;
-struct Fill {
+// tok), with thread f < dim/4 owning x[4f, 4f+4). The parts are split over G = NTE / (dim/4) thread
+// groups; pro_load only issues the loads (with the norm weights and RoPE angles the kernel needs),
+// pro_finish adds them: each group's sum goes through LDS and the owners add the groups in order.
+constexpr int FILL_PER = 4;
+struct Pro {
     float4 p[FILL_PER];
     float4 base;
-    float e;
+    float4 emb;       // layer 0: the embedding row's owned elements
+    float4 nw;        // norm weights of the owned elements
+    float2 cs;        // RoPE (cos, sin) of angle index tid (tid < hd / 2)
 };
-struct FillGeom {
+struct ProGeom {
     int n4, groups, per;
 };
-__device__ __forceinline__ FillGeom fill_geom(int dim, int nparts) {
-    FillGeom g;
-    g.n4 = dim / 4;
+__device__ __forceinline__ ProGeom pro_geom(int dim, int nparts) {
+    ProGeom g;
+    g.n4 = dim >> 2;
     g.groups = NTE / g.n4 < 1 ? 1 : NTE / g.n4;
     g.per = (nparts + g.groups - 1) / g.groups;
     if (g.per < 1) g.per = 1;
     return g;
 }
-// embed (by value: a pointer into the kernel's argument struct would move the whole struct to scratch)
-// is read when use_embed is set.
-__device__ __forceinline__ void fill_load(Fill &F, const float *base, const float *parts, int nparts, int dim, l3m_dmat embed, bool use_embed, int tok) {
-    if (use_embed) {                                         // layer 0: x = dequant(embed[tok]) (engine.c:236)
-        F.e = threadIdx.x < dim ? lt_elem(embed, tok, threadIdx.x) : 0.f;
-        return;
-    }
-    const FillGeom G = fill_geom(dim, nparts);
-    const int f = threadIdx.x % G.n4, grp = threadIdx.x / G.n4, j0 = grp * G.per;
-    if (grp < G.groups && grp == 0) F.base = ldg16f(base, f);
+// Loads are unconditional (indices clamped into range) wherever possible: a load under a branch that
+// later merges makes the compiler wait for it there, before the weight stream is issued.
+// embed is passed by value: a pointer into the kernel's argument struct would move that struct to scratch.
+__device__ __forceinline__ void pro_load(Pro &P, const float *base, const float *parts, int nparts, int dim, const float *nw,
+                                         l3m_dmat embed, bool use_embed, int tok, const float *rope_row, int hd) {
+    const int tid = threadIdx.x;
+    const ProGeom G = pro_geom(dim, nparts);
+    const int f = tid % G.n4, grp = tid / G.n4, j0 = grp * G.per, own = tid < G.n4 ? tid : G.n4 - 1;
+    P.nw = ldg16f(nw, own);
+    P.base = ldg16f(base, f);
 #pragma unroll
-    for (int j = 0; j < FILL_PER; j++)
-        if (grp < G.groups && j < G.per && j0 + j < nparts) F.p[j] = ldg16f(parts + (size_t)(j0 + j) * dim, f);
+    for (int j = 0; j < FILL_PER; j++) {
+        const int pj = j0 + j < nparts ? j0 + j : nparts - 1;
+        P.p[j] = ldg16f(parts + (size_t)pj * dim, f);
+    }
+    if (rope_row) {
+        const int i = tid < (hd >> 1) ? tid : (hd >> 1) - 1;
+        P.cs = make_float2(gp<float>(rope_row)[2 * i], gp<float>(rope_row)[2 * i + 1]);
+    }
+    if (use_embed) P.emb = lt_elem4(embed, tok, 4 * own);   // layer 0: x = dequant(embed[tok]) (engine.c:236)
+    asm volatile("" ::: "memory");                            // these loads are issued before the weights
 }
-// xs[0, dim) = x; also stored to keep when given. pbuf: LDS for the group sums (NTE float4). All threads call.
-__device__ void fill_finish(Fill &F, float *xs, const float *parts, int nparts, int dim, float4 *pbuf, float *keep, bool embed) {
-    if (embed) {
-        if (threadIdx.x < dim) { xs[threadIdx.x] = F.e; if (keep) keep[threadIdx.x] = F.e; }
-        __syncthreads();
-        return;
-    }
-    const FillGeom G = fill_geom(dim, nparts);
-    const int f = threadIdx.x % G.n4, grp = threadIdx.x / G.n4, j0 = grp * G.per;
-    if (grp < G.groups) {
-        float4 v = grp == 0 ? F.base : make_float4(0.f, 0.f, 0.f, 0.f);
+// Returns x[4f, 4f+4) to owner f (zeros to the other threads); stores it to keep when given; writes the
+// RoPE angles to cs_lds when given. pbuf: NTE float4 of LDS. All threads call it.
+__device__ float4 pro_finish(Pro &P, const float *parts, int nparts, int dim, bool use_embed, float4 *pbuf, float *keep,
+                             float *cs_lds, int hd) {
+    const int tid = threadIdx.x;
+    const ProGeom G = pro_geom(dim, nparts);
+    const int f = tid % G.n4, grp = tid / G.n4, j0 = grp * G.per;
+    if (cs_lds && tid < (hd >> 1)) ((float2 *)cs_lds)[tid] = P.cs;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (use_embed) {
+        if (tid < G.n4) x = P.emb;
+    } else {
+        if (grp < G.groups) {
+            float4 v = grp == 0 ? P.base : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int j = 0; j < FILL_PER; j++)
-            if (j < G.per && j0 + j < nparts) { v.x += F.p[j].x; v.y += F.p[j].y; v.z += F.p[j].z; v.w += F.p[j].w; }
-        for (int j = FILL_PER; j < G.per && j0 + j < nparts; j++) {   // more parts than one batch: in order
-            const float4 p = ldg16f(parts + (size_t)(j0 + j) * dim, f);
-            v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+            for (int j = 0; j < FILL_PER; j++) {
+                const bool use = j < G.per && j0 + j < nparts;
+                v.x += use ? P.p[j].x : 0.f; v.y += use ? P.p[j].y : 0.f; v.z += use ? P.p[j].z : 0.f; v.w += use ? P.p[j].w : 0.f;
+            }
+            for (int j = FILL_PER; j < G.per && j0 + j < nparts; j++) {   // beyond one batch: in order
+                const float4 p = ldg16f(parts + (size_t)(j0 + j) * dim, f);
+                v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+            }
+            if (G.groups > 1) pbuf[grp * G.n4 + f] = v;
+            else x = v;
         }
-        pbuf[grp * G.n4 + f] = v;
+        if (G.groups > 1) {
+            __syncthreads();
+            if (tid < G.n4) {
+                x = pbuf[tid];
+                for (int g = 1; g < G.groups; g++) {
+                    const float4 p = pbuf[g * G.n4 + tid];
+                    x.x += p.x; x.y += p.y; x.z += p.z; x.w += p.w;
+                }
+            }
+        }
     }
-    __syncthreads();
-    if (threadIdx.x < G.n4) {
-        float4 v = pbuf[threadIdx.x];
-        for (int g = 1; g < G.groups; g++) {
-            const float4 p = pbuf[g * G.n4 + threadIdx.x];
-            v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    if (keep && tid < G.n4) ((float4 *)keep)[tid] = x;
+    return x;
+}
+
+// act = the prepared activation (pack.c:101-123) of the values v[4f, 4f+4) held by thread f, f < kp/4
+// (zero beyond k): the reference's per-32-block int8 quantization (8 lanes per block), bf16 or f32.
+// Ends with a barrier.
+template <int DT>
+__device__ void prep_owned(float4 y, uint8_t *act, int kp) {
+    const int f = threadIdx.x;
+    if constexpr (quantized(DT)) {
+        float am = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
+        am = lanes_max<8>(am);
+        const float inv = am > 0.f ? 127.0f / am : 0.f;
+        const int q0 = (int)rintf(y.x * inv), q1 = (int)rintf(y.y * inv), q2 = (int)rintf(y.z * inv), q3 = (int)rintf(y.w * inv);
+        const int s = lanes_sumi<8>(q0 + q1 + q2 + q3);
+        if (4 * f < kp) {
+            *(uint32_t *)(act + 4 * f) = (uint32_t)(q0 & 255) | (uint32_t)(q1 & 255) << 8 | (uint32_t)(q2 & 255) << 16 | (uint32_t)(q3 & 255) << 24;
+            if ((f & 7) == 0) {
+                ((float *)(act + kp))[f >> 3] = am / 127.0f;
+                ((int *)(act + kp + 4 * (kp / 32)))[f >> 3] = s;
+            }
         }
-        ((float4 *)xs)[threadIdx.x] = v;
-        if (keep) ((float4 *)keep)[threadIdx.x] = v;
+    } else if constexpr (DT == L3M_BF16) {
+        if (4 * f < kp)
+            *(uint2 *)(act + 8 * f) = make_uint2((uint32_t)f32_bf16(y.x) | (uint32_t)f32_bf16(y.y) << 16,
+                                                 (uint32_t)f32_bf16(y.z) | (uint32_t)f32_bf16(y.w) << 16);
+    } else {
+        if (4 * f < kp) *(float4 *)(act + 16 * f) = y;
     }
     __syncthreads();
 }
 
-// Norm + prep of xs (x in [0, k)): RMSNorm with nw when given (ops.c:13-18), then the activation prep
-// (pack.c:101-123) into act, padded to kp. All threads call it.
+// RMSNorm (ops.c:13-18: s = 1/sqrt(sum x^2 / n + eps), y = x * s * w) of the owned x, then its prep.
 template <int DT>
-__device__ void norm_prep(float *xs, uint8_t *act, int k, int kp, const float *nw, float eps, float *scr) {
-    const int tid = threadIdx.x;
-    for (int i = k + tid; i < kp; i += NTE) xs[i] = 0.f;
-    if (nw) {
-        float ss = 0.f;
-        for (int i = tid; i < k; i += NTE) ss = fmaf(xs[i], xs[i], ss);
-        const float tot = wge_sum(ss, scr);
-        const float s = 1.0f / sqrtf(tot / (float)k + eps);
-        for (int i = tid; i < k; i += NTE) xs[i] = xs[i] * s * nw[i];
-    }
-    __syncthreads();
-    if constexpr (quantized(DT)) {
-        const int nb = kp / 32, g = tid >> 3, l = tid & 7;
-        float *scale = (float *)(act + kp);
-        int *sum = (int *)(act + kp + 4 * nb);
-        for (int b = g; b < nb; b += NTE / 8) {
-            const float4 v = *(const float4 *)(xs + b * 32 + 4 * l);
-            float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-            am = fmaxf(am, __shfl_xor(am, 1));
-            am = fmaxf(am, __shfl_xor(am, 2));
-            am = fmaxf(am, __shfl_xor(am, 4));
-            const float inv = am > 0.f ? 127.0f / am : 0.f;
-            const int q0 = (int)rintf(v.x * inv), q1 = (int)rintf(v.y * inv), q2 = (int)rintf(v.z * inv), q3 = (int)rintf(v.w * inv);
-            *(uint32_t *)(act + b * 32 + 4 * l) = (uint32_t)(q0 & 255) | (uint32_t)(q1 & 255) << 8 | (uint32_t)(q2 & 255) << 16 | (uint32_t)(q3 & 255) << 24;
-            int s = q0 + q1 + q2 + q3;
-            s += __shfl_xor(s, 1);
-            s += __shfl_xor(s, 2);
-            s += __shfl_xor(s, 4);
-            if (l == 0) { scale[b] = am / 127.0f; sum[b] = s; }
-        }
-    } else if constexpr (DT == L3M_BF16) {
-        for (int i = tid; i < kp; i += NTE) ((uint16_t *)act)[i] = f32_bf16(xs[i]);
-    } else {
-        for (int i = tid; i < kp; i += NTE) ((float *)act)[i] = xs[i];
-    }
-    __syncthreads();
+__device__ void norm_prep(float4 x, float4 nw, int k, int kp, float eps, uint8_t *act, Red &red) {
+    const float tot = red_sum(red, x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
+    const float s = 1.0f / sqrtf(tot / (float)k + eps);
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * (int)threadIdx.x < k) y = make_float4(x.x * s * nw.x, x.y * s * nw.y, x.z * s * nw.z, x.w * s * nw.w);
+    prep_owned<DT>(y, act, kp);
 }
 
 // LDS regions of the step kernels (byte offsets, 16-aligned) from the layer geometry. `work` holds the
-// prologue's group sums, then the per-pair matvec results, then the attention partials.
-struct LdsA { size_t xs, act, work, qkv, kv, sc, att, act2, scr, kvb, total; };
+// prologue's group sums, then the per-pair matvec results.
 __host__ __device__ inline size_t work_bytes(size_t pairs) {
     const size_t w = 64 * pairs;
     return align16(w > 16 * (size_t)NTE ? w : 16 * (size_t)NTE);
 }
+struct LdsA { size_t act, work, q, cur, cs, sc, vred, att, act2, scr, kvb, total; };
 __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g, int kv_lds) {
     LdsA L;
     size_t o = 0;
     const size_t pq = (size_t)g.qkv.tiles * g.qkv.nb, pw = (size_t)g.wo.tiles * g.wo.nb;
-    L.xs = o;   o += align16(4 * (size_t)kpad(dim));
     L.act = o;  o += align16(act_size(dt, dim));
     L.work = o; o += work_bytes(pq > pw ? pq : pw);
-    L.qkv = o;  o += align16(64 * (size_t)g.qkv.tiles);
-    L.kv = o;   o += align16(8 * (size_t)g.nkv * hd);
+    L.q = o;    o += align16(4 * (size_t)g.nq * hd);
+    L.cur = o;  o += align16(4 * (size_t)g.nkv * hd);              // this step's k, v rows: bf16 [2][nkv][hd]
+    L.cs = o;   o += align16(4 * (size_t)hd);
     L.sc = o;   o += align16(4 * (size_t)(ctx + 4));
+    L.vred = o; o += align16(4 * (size_t)NWE * hd);
     L.att = o;  o += align16(4 * (size_t)kpad(g.nq * hd));
     L.act2 = o; o += align16(act_size(dt, g.nq * hd));
     L.scr = o;  o += 4 * 64;
@@ -679,26 +789,23 @@ __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3
     L.total = o;
     return L;
 }
-struct LdsB { size_t xs, act, work, gu, h, act2, scr, total; };
+struct LdsB { size_t act, work, gu, act2, scr, total; };
 __host__ __device__ inline LdsB lds_b(int dt, int dim, const l3m_dchunk &c) {
     LdsB L;
     size_t o = 0;
     const size_t pg = (size_t)c.gate_up.tiles * c.gate_up.nb, pw = (size_t)c.down.tiles * c.down.nb;
-    L.xs = o;   o += align16(4 * (size_t)kpad(dim));
     L.act = o;  o += align16(act_size(dt, dim));
     L.work = o; o += work_bytes(pg > pw ? pg : pw);
     L.gu = o;   o += align16(64 * (size_t)c.gate_up.tiles);
-    L.h = o;    o += align16(4 * (size_t)kpad(c.nf));
     L.act2 = o; o += align16(act_size(dt, c.nf));
     L.scr = o;  o += 4 * 64;
     L.total = o;
     return L;
 }
-struct LdsH { size_t xs, act, work, y, scr, total; };
+struct LdsH { size_t act, work, y, scr, total; };
 __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg) {
     LdsH L;
     size_t o = 0;
-    L.xs = o;   o += align16(4 * (size_t)kpad(dim));
     L.act = o;  o += align16(act_size(dt, dim));
     L.work = o; o += work_bytes((size_t)tiles_per_wg * nb);
     L.y = o;    o += align16(64 * (size_t)tiles_per_wg);
@@ -725,6 +832,94 @@ __device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int
     }
 }
 
+__device__ __forceinline__ float dot8_bf16(const float *q, uint4 k, float acc) {
+    acc = fmaf(q[0], bf16_f32(k.x & 0xFFFF), acc); acc = fmaf(q[1], bf16_f32(k.x >> 16), acc);
+    acc = fmaf(q[2], bf16_f32(k.y & 0xFFFF), acc); acc = fmaf(q[3], bf16_f32(k.y >> 16), acc);
+    acc = fmaf(q[4], bf16_f32(k.z & 0xFFFF), acc); acc = fmaf(q[5], bf16_f32(k.z >> 16), acc);
+    acc = fmaf(q[6], bf16_f32(k.w & 0xFFFF), acc); acc = fmaf(q[7], bf16_f32(k.w >> 16), acc);
+    return acc;
+}
+
+// Attention of the group's query heads over positions 0..pos (ops.c:58-73). Lane j of each aligned
+// group of LP lanes takes dims [8j, 8j+8) of one position (LP = hd/8 rounded up to a power of two):
+// scores are lane-group sums, the softmax is a workgroup max and sum, and the weighted V sum runs over
+// positions g, g + NTE/LP, ... per lane group, then across lane groups (in a wavefront, then over the
+// wavefronts through LDS). K, V rows before pos come from the LDS window (WIN) or the cache, row pos
+// from cur (this step's rows, bf16 as the cache holds them).
+template <bool WIN>
+__device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer, int pos, const float *qh, const uint16_t *cur,
+                             const uint16_t *kvb, float *sc, float *vred, float *att, Red &red) {
+    const int hd = M.hd, nv = hd >> 3, LP = nv <= 4 ? 4 : nv <= 8 ? 8 : nv <= 16 ? 16 : 32;
+    const int tid = threadIdx.x, lane = tid & 63, j = tid & (LP - 1), g = tid / LP, NG = NTE / LP, n = pos + 1;
+    const int hpk = M.n_heads / M.n_kv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const size_t win = (size_t)M.ctx * hd;
+    for (int h = 0; h < G.nq; h++) {
+        const int kvl = (G.q0 + h) / hpk - G.kv0;
+        const uint16_t *kw = WIN ? kvb + kvl * win : M.kc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
+        const uint16_t *vw = WIN ? kvb + (G.nkv + kvl) * win : M.vc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
+        const uint4 *kcur = (const uint4 *)(cur + kvl * hd), *vcur = (const uint4 *)(cur + (G.nkv + kvl) * hd);
+        float q[8];
+        {
+            const float4 a = j < nv ? ((const float4 *)(qh + h * hd))[2 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 b = j < nv ? ((const float4 *)(qh + h * hd))[2 * j + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+            q[0] = a.x; q[1] = a.y; q[2] = a.z; q[3] = a.w; q[4] = b.x; q[5] = b.y; q[6] = b.z; q[7] = b.w;
+        }
+        float mx = -INFINITY;
+        for (int t0 = 0; t0 < n; t0 += NG) {
+            const int t = t0 + g;
+            float part = 0.f;
+            if (t < n && j < nv) {
+                uint4 kk;
+                if (t == pos) kk = kcur[j];
+                else if (WIN) kk = ((const uint4 *)(kw + (size_t)t * hd))[j];
+                else kk = ldg16(kw + (size_t)t * hd, j);
+                part = dot8_bf16(q, kk, 0.f);
+            }
+            const float s = lanes_sum_n(part, LP) * scale;
+            if (t < n) {
+                if (j == 0) sc[t] = s;
+                mx = fmaxf(mx, s);
+            }
+        }
+        mx = red_max(red, mx);
+        float sum = 0.f;
+        for (int t = tid; t < n; t += NTE) {
+            const float e = expf(sc[t] - mx);
+            sc[t] = e;
+            sum += e;
+        }
+        sum = red_sum(red, sum);
+        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (j < nv)
+            for (int t = g; t < n; t += NG) {
+                const float p = sc[t] / sum;
+                uint4 vv;
+                if (t == pos) vv = vcur[j];
+                else if (WIN) vv = ((const uint4 *)(vw + (size_t)t * hd))[j];
+                else vv = ldg16(vw + (size_t)t * hd, j);
+                o[0] = fmaf(p, bf16_f32(vv.x & 0xFFFF), o[0]); o[1] = fmaf(p, bf16_f32(vv.x >> 16), o[1]);
+                o[2] = fmaf(p, bf16_f32(vv.y & 0xFFFF), o[2]); o[3] = fmaf(p, bf16_f32(vv.y >> 16), o[3]);
+                o[4] = fmaf(p, bf16_f32(vv.z & 0xFFFF), o[4]); o[5] = fmaf(p, bf16_f32(vv.z >> 16), o[5]);
+                o[6] = fmaf(p, bf16_f32(vv.w & 0xFFFF), o[6]); o[7] = fmaf(p, bf16_f32(vv.w >> 16), o[7]);
+            }
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = strided_sum(o[e], LP);
+        if (lane < LP && j < nv) {
+            float4 *d = (float4 *)(vred + (tid >> 6) * hd + 8 * j);
+            d[0] = make_float4(o[0], o[1], o[2], o[3]);
+            d[1] = make_float4(o[4], o[5], o[6], o[7]);
+        }
+        __syncthreads();
+        if (tid < hd) {
+            float a = vred[tid];
+            for (int w = 1; w < NWE; w++) a += vred[w * hd + tid];
+            att[h * hd + tid] = a;
+        }
+        __syncthreads();
+    }
+}
+
 // Kernel A: the attention block of one head group (engine.c:236-258).
 template <int DT>
 __global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw, int layer) {
@@ -732,113 +927,60 @@ __global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw,
     const l3m_dgroup G = Lw.groups[blockIdx.x];
     const int tid = threadIdx.x, pos = *M.pos, dim = M.dim, hd = M.hd, kp = kpad(dim);
     const LdsA L = lds_a(DT, dim, M.ctx, hd, G, M.kv_lds);
-    float *xs = (float *)(smem + L.xs), *work = (float *)(smem + L.work), *qkv = (float *)(smem + L.qkv);
-    float *kvc = (float *)(smem + L.kv), *sc = (float *)(smem + L.sc), *att = (float *)(smem + L.att), *scr = (float *)(smem + L.scr);
+    float *work = (float *)(smem + L.work), *qh = (float *)(smem + L.q), *cs = (float *)(smem + L.cs);
+    float *sc = (float *)(smem + L.sc), *vred = (float *)(smem + L.vred), *att = (float *)(smem + L.att);
+    uint16_t *cur = (uint16_t *)(smem + L.cur), *kvb = (uint16_t *)(smem + L.kvb);
     uint8_t *act = smem + L.act, *act2 = smem + L.act2;
+    Red red{(float *)(smem + L.scr), 0};
 
-    Fill F;
-    fill_load(F, M.xb, M.pd, M.n_chunks, dim, M.embed, layer == 0, layer ? 0 : M.tokens[pos]);
+    Pro P;
+    pro_load(P, M.xb, M.pd, M.n_chunks, dim, Lw.attn_norm, M.embed, layer == 0, layer ? 0 : M.tokens[pos],
+             M.rope + (size_t)pos * hd, hd);
     Pref<DT, nslot_a<DT>()> pa;
-    Pref<DT, nslot_b<DT>()> pb;
+    Pref<DT, nslot_wo<DT>()> pb;
     pref_load<DT, nslot_a<DT>()>(pa, G.qkv, 0);
-    pref_load<DT, nslot_b<DT>()>(pb, G.wo, 0);
-    fill_finish(F, xs, M.pd, M.n_chunks, dim, (float4 *)work, blockIdx.x == 0 ? M.xa : nullptr, layer == 0);
-    uint16_t *kvb = (uint16_t *)(smem + L.kvb);
-    if (M.kv_lds) kv_window_dma(kvb, M, layer, G.kv0, G.nkv, pos);   // K, V rows 0..pos-1: no dependence on this step
-    norm_prep<DT>(xs, act, dim, kp, Lw.attn_norm, M.eps, scr);
+    pref_load<DT, nslot_wo<DT>()>(pb, G.wo, 0);
+    const float4 x = pro_finish(P, M.pd, M.n_chunks, dim, layer == 0, (float4 *)work, blockIdx.x == 0 ? M.xa : nullptr, cs, hd);
+    // K, V rows 0..pos-1 (no dependence on this step). Issued after the prologue is consumed: a copy of
+    // data-dependent length ahead of it would make the compiler wait for every load in flight there.
+    if (M.kv_lds) kv_window_dma(kvb, M, layer, G.kv0, G.nkv, pos);
+    norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
 
     mv<DT, nslot_a<DT>()>(pa, G.qkv, act, kp, work);
     __syncthreads();
+    // q, k rows: RoPE on pairs (2i, 2i+1) of each head by the angle i (ops.c:29-40); k, v rows rounded
+    // to bf16 as the cache holds them (engine.c:247-248), into cur and (for the heads this group writes)
+    // the cache
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
-    rows_sum(G.qkv, work, qkv, nqd + 2 * nkd);
-    __syncthreads();
-
-    // RoPE on q and k: pairs (2i, 2i+1) of each head by the table angle i (ops.c:29-40)
-    float rot = 0.f;
-    if (tid < nqd + nkd) {
-        const int local = tid < nqd ? tid : tid - nqd, i = (local % hd) >> 1;
-        const float *cs = M.rope + ((size_t)pos * (hd >> 1) + i) * 2;
-        const float a = qkv[tid], b = qkv[tid ^ 1];
-        rot = (tid & 1) ? b * cs[1] + a * cs[0] : a * cs[0] - b * cs[1];
-    }
-    __syncthreads();
-    if (tid < nqd + nkd) qkv[tid] = rot;
-    __syncthreads();
-    // k and v of this position, as the bf16 cache holds them (engine.c:247-248)
-    for (int i = tid; i < 2 * nkd; i += NTE) {
-        const uint16_t h = f32_bf16(qkv[nqd + i]);
-        kvc[i] = bf16_f32(h);
-        const int j = i < nkd ? i : i - nkd, kvl = j / hd;
-        if (G.write_kv >> kvl & 1u) {
-            uint16_t *c = i < nkd ? M.kc : M.vc;
-            c[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + j % hd] = h;
+    rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner) {
+        if (i < nqd + nkd) {
+            const int local = i < nqd ? i : i - nqd;
+            const float2 c = ((const float2 *)cs)[(local % hd) >> 1];
+            y = (i & 1) ? partner * c.y + y * c.x : y * c.x - partner * c.y;
         }
-    }
-    __syncthreads();
-
-    // attention of each query head over positions 0..pos (ops.c:58-73): rows before pos from the LDS
-    // window (kv_lds) or from the cache, row pos from kvc
+        if ((threadIdx.x & 3) == 0) {
+            if (i < nqd) qh[i] = y;
+            else {
+                const int r = i - nqd, kv = r < nkd ? 0 : 1, jj = r - kv * nkd, kvl = jj / hd;
+                const uint16_t hb = f32_bf16(y);
+                cur[kv * nkd + jj] = hb;
+                if (G.write_kv >> kvl & 1u)
+                    (kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + jj % hd] = hb;
+            }
+        }
+    });
     if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    const float scale = 1.0f / sqrtf((float)hd);
-    const int hpk = M.n_heads / M.n_kv, groups = NTE / hd, gi = tid / hd, ii = tid % hd, nv = hd / 8;
-    const size_t win = (size_t)M.ctx * hd;
-    for (int h = 0; h < G.nq; h++) {
-        const int kvl = (G.q0 + h) / hpk - G.kv0;
-        const float *q = qkv + h * hd;
-        const uint16_t *kh = M.kv_lds ? kvb + kvl * win : M.kc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
-        const uint16_t *vh = M.kv_lds ? kvb + (G.nkv + kvl) * win : M.vc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
-        float mx = -INFINITY;
-        for (int t = tid; t <= pos; t += NTE) {
-            float dot = 0.f;
-            if (t < pos) {
-                const uint16_t *kr = kh + (size_t)t * hd;
-                for (int v = 0; v < nv; v++) {
-                    const uint4 kk = M.kv_lds ? ((const uint4 *)kr)[v] : ldg16(kr, v);
-                    const float *qq = q + v * 8;
-                    dot = fmaf(qq[0], bf16_f32(kk.x & 0xFFFF), dot); dot = fmaf(qq[1], bf16_f32(kk.x >> 16), dot);
-                    dot = fmaf(qq[2], bf16_f32(kk.y & 0xFFFF), dot); dot = fmaf(qq[3], bf16_f32(kk.y >> 16), dot);
-                    dot = fmaf(qq[4], bf16_f32(kk.z & 0xFFFF), dot); dot = fmaf(qq[5], bf16_f32(kk.z >> 16), dot);
-                    dot = fmaf(qq[6], bf16_f32(kk.w & 0xFFFF), dot); dot = fmaf(qq[7], bf16_f32(kk.w >> 16), dot);
-                }
-            } else {
-                const float *kr = kvc + kvl * hd;
-                for (int i = 0; i < hd; i++) dot = fmaf(q[i], kr[i], dot);
-            }
-            sc[t] = dot * scale;
-            mx = fmaxf(mx, dot * scale);
-        }
-        mx = wge_max(mx, scr);
-        float sum = 0.f;
-        for (int t = tid; t <= pos; t += NTE) {
-            const float e = expf(sc[t] - mx);
-            sc[t] = e;
-            sum += e;
-        }
-        sum = wge_sum(sum, scr);
-        for (int t = tid; t <= pos; t += NTE) sc[t] = sc[t] / sum;
-        __syncthreads();
-        float acc = 0.f;
-        if (gi < groups)
-            for (int t = gi; t <= pos; t += groups) {
-                const float v = t == pos ? kvc[nkd + kvl * hd + ii]
-                              : bf16_f32(M.kv_lds ? vh[(size_t)t * hd + ii] : gp<uint16_t>(vh)[(size_t)t * hd + ii]);
-                acc = fmaf(sc[t], v, acc);
-            }
-        work[tid] = acc;
-        __syncthreads();
-        if (tid < hd) {
-            float o = work[tid];
-            for (int g = 1; g < groups; g++) o += work[g * hd + tid];
-            att[h * hd + tid] = o;
-        }
-        __syncthreads();
-    }
-    // prep of the group's attention output, then its Wo columns -> the partial residual po[group]
-    norm_prep<DT>(att, act2, nqd, kpad(nqd), nullptr, 0.f, scr);
-    mv<DT, nslot_b<DT>()>(pb, G.wo, act2, kpad(nqd), work);
+    if (M.kv_lds) attend_group<true>(M, G, layer, pos, qh, cur, kvb, sc, vred, att, red);
+    else attend_group<false>(M, G, layer, pos, qh, cur, kvb, sc, vred, att, red);
+
+    // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
+    const int kq = kpad(nqd);
+    prep_owned<DT>(4 * tid < nqd ? ((const float4 *)att)[tid] : make_float4(0.f, 0.f, 0.f, 0.f), act2, kq);
+    mv<DT, nslot_wo<DT>()>(pb, G.wo, act2, kq, work);
     __syncthreads();
-    rows_sum(G.wo, work, M.po + (size_t)blockIdx.x * dim, dim);
+    float *po = M.po + (size_t)blockIdx.x * dim;
+    rows_sum4(G.wo, work, dim, [&](int i, float y, float) { if ((threadIdx.x & 3) == 0) po[i] = y; });
 }
 
 // Kernel B: the FFN block of one chunk of ffn rows (engine.c:259-275). The last layer of a step without
@@ -849,29 +991,39 @@ __global__ void __launch_bounds__(NTE) k_ffn_block(l3m_dmodel M, l3m_dlayer Lw, 
     const l3m_dchunk C = Lw.chunks[blockIdx.x];
     const int tid = threadIdx.x, dim = M.dim, kp = kpad(dim);
     const LdsB L = lds_b(DT, dim, C);
-    float *xs = (float *)(smem + L.xs), *work = (float *)(smem + L.work), *gu = (float *)(smem + L.gu);
-    float *h = (float *)(smem + L.h), *scr = (float *)(smem + L.scr);
+    float *work = (float *)(smem + L.work), *gu = (float *)(smem + L.gu);
     uint8_t *act = smem + L.act, *act2 = smem + L.act2;
+    Red red{(float *)(smem + L.scr), 0};
 
-    Fill F;
-    fill_load(F, M.xa, M.po, M.n_groups, dim, M.embed, false, 0);     // x += proj (engine.c:259)
+    Pro P;
+    pro_load(P, M.xa, M.po, M.n_groups, dim, Lw.ffn_norm, M.embed, false, 0, nullptr, 0);     // x += proj (engine.c:259)
     Pref<DT, nslot_a<DT>()> pa;
     Pref<DT, nslot_b<DT>()> pb;
     pref_load<DT, nslot_a<DT>()>(pa, C.gate_up, 0);
     pref_load<DT, nslot_b<DT>()>(pb, C.down, 0);
-    fill_finish(F, xs, M.po, M.n_groups, dim, (float4 *)work, blockIdx.x == 0 ? M.xb : nullptr, false);
-    norm_prep<DT>(xs, act, dim, kp, Lw.ffn_norm, M.eps, scr);
+    const float4 x = pro_finish(P, M.po, M.n_groups, dim, false, (float4 *)work, blockIdx.x == 0 ? M.xb : nullptr, nullptr, 0);
+    norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>()>(pa, C.gate_up, act, kp, work);
     __syncthreads();
-    rows_sum(C.gate_up, work, gu, C.gate_up.rows);
+    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float) { if ((threadIdx.x & 3) == 0) gu[i] = y; });
     __syncthreads();
-    for (int i = tid; i < C.nf; i += NTE)                           // h = up * silu(gate) (ops.c:49-51)
-        h[i] = silu_mul(gu[(2 * (i >> 4) + 1) * 16 + (i & 15)], gu[(2 * (i >> 4)) * 16 + (i & 15)]);
+    // h = up * silu(gate) (ops.c:49-51) for the owned 4 rows (gate tile t and up tile t interleave), prepared
+    const int kf = kpad(C.nf);
+    float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * tid < C.nf) {
+        float hh[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = 4 * tid + e, gi = (2 * (i >> 4)) * 16 + (i & 15);
+            hh[e] = silu_mul(gu[gi + 16], gu[gi]);
+        }
+        hv = make_float4(hh[0], hh[1], hh[2], hh[3]);
+    }
+    prep_owned<DT>(hv, act2, kf);
+    mv<DT, nslot_b<DT>()>(pb, C.down, act2, kf, work);
     __syncthreads();
-    norm_prep<DT>(h, act2, C.nf, kpad(C.nf), nullptr, 0.f, scr);
-    mv<DT, nslot_b<DT>()>(pb, C.down, act2, kpad(C.nf), work);
-    __syncthreads();
-    rows_sum(C.down, work, M.pd + (size_t)blockIdx.x * dim, dim);
+    float *pd = M.pd + (size_t)blockIdx.x * dim;
+    rows_sum4(C.down, work, dim, [&](int i, float y, float) { if ((threadIdx.x & 3) == 0) pd[i] = y; });
     if (advance && blockIdx.x == 0 && tid == 0) *M.pos += 1;
 }
 
@@ -890,24 +1042,25 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
     V.rows = nt * 16 < M.vocab - t0 * 16 ? nt * 16 : M.vocab - t0 * 16;
     const int pos = *M.pos, dim = M.dim, kp = kpad(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
-    float *xs = (float *)(smem + L.xs), *work = (float *)(smem + L.work), *y = (float *)(smem + L.y), *scr = (float *)(smem + L.scr);
+    float *work = (float *)(smem + L.work), *y = (float *)(smem + L.y), *scr = (float *)(smem + L.scr);
     uint8_t *act = smem + L.act;
+    Red red{scr, 0};
 
-    Fill F;
-    fill_load(F, M.xb, M.pd, M.n_chunks, dim, M.embed, false, 0);     // x += down (engine.c:275), last layer
+    Pro P;
+    pro_load(P, M.xb, M.pd, M.n_chunks, dim, M.norm, M.embed, false, 0, nullptr, 0);     // x += down (engine.c:275), last layer
     Pref<DT, nslot_a<DT>() + nslot_b<DT>()> pa;
     pref_load<DT, nslot_a<DT>() + nslot_b<DT>()>(pa, V, 0);
-    fill_finish(F, xs, M.pd, M.n_chunks, dim, (float4 *)work, nullptr, false);
-    norm_prep<DT>(xs, act, dim, kp, M.norm, M.eps, scr);
+    const float4 x = pro_finish(P, M.pd, M.n_chunks, dim, false, (float4 *)work, nullptr, nullptr, 0);
+    norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>() + nslot_b<DT>()>(pa, V, act, kp, work);
     __syncthreads();
-    rows_sum(V, work, y, V.rows);
+    rows_sum4(V, work, V.rows, [&](int i, float yy, float) { if ((threadIdx.x & 3) == 0) y[i] = yy; });
     __syncthreads();
     float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab + (size_t)t0 * 16;
     float v = -INFINITY;
     int idx = 0x7FFFFFFF;
     if (tid < V.rows) { lg[tid] = y[tid]; v = y[tid]; idx = t0 * 16 + tid; }
-    wge_argmax(v, idx, scr);
+    wge_argmax(v, idx, scr, (int *)scr + 16);
     __shared__ int last;
     if (tid == 0) {
         M.part_val[blockIdx.x] = v;
@@ -925,7 +1078,7 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
         const int pi = __hip_atomic_load(M.part_idx + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         better(v, idx, pv, pi);
     }
-    wge_argmax(v, idx, scr);
+    wge_argmax(v, idx, scr, (int *)scr + 16);
     if (tid == 0) {
         if (advance) {
             M.tokens[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
