@@ -58,24 +58,23 @@ _Static_assert(sizeof(l3m_block_q8_0) == 34 && sizeof(l3m_block_q4_0) == 18 && s
 static const int8_t L3M_E2M1X2[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
 
 static inline const char *l3m_dtype_name(int dtype) {
-    static const char *const names[L3M_NDTYPES] = {"f32", "bf16", "q8_0", "q4_0", "mxfp4"};
-    return dtype >= 0 && dtype < L3M_NDTYPES ? names[dtype] : "?";
-}
-
-static inline int l3m_header_ok(const l3m_header *h) {
-    return h->magic[0] == 'l' && h->magic[1] == '3' && h->magic[2] == 'm' && h->version == L3M_VERSION;
+    switch (dtype) {
+    case L3M_F32: return "f32";
+    case L3M_BF16: return "bf16";
+    case L3M_Q8_0: return "q8_0";
+    case L3M_Q4_0: return "q4_0";
+    case L3M_MXFP4: return "mxfp4";
+    }
+    return "?";
 }
 
 // Bytes of one file row of k inputs (pack.c:10-19).
 static inline size_t l3m_file_row_bytes(int dtype, int k) {
-    switch (dtype) {
-    case L3M_F32:   return (size_t)k * 4;
-    case L3M_BF16:  return (size_t)k * 2;
-    case L3M_Q8_0:  return (size_t)(k / L3M_QBLOCK) * sizeof(l3m_block_q8_0);
-    case L3M_Q4_0:  return (size_t)(k / L3M_QBLOCK) * sizeof(l3m_block_q4_0);
-    case L3M_MXFP4: return (size_t)(k / L3M_QBLOCK) * sizeof(l3m_block_mxfp4);
-    }
-    return 0;
+    static const unsigned per_block[L3M_NDTYPES] = {4 * L3M_QBLOCK, 2 * L3M_QBLOCK, sizeof(l3m_block_q8_0), sizeof(l3m_block_q4_0),
+                                                    sizeof(l3m_block_mxfp4)};
+    if (dtype < 0 || dtype >= L3M_NDTYPES) return 0;
+    if (dtype <= L3M_BF16) return (size_t)k * (per_block[dtype] / L3M_QBLOCK);   // f32, bf16: any width
+    return (size_t)(k / L3M_QBLOCK) * per_block[dtype];
 }
 
 static inline float l3m_bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }

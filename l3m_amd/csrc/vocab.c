@@ -1,31 +1,48 @@
-// The tokenizer section of a .l3m file as a byte table (format: src/model.h:27-28; header checks:
-// src/tokenizer.c:17-45). Decoding is exact. Encoding maps each input byte to its single-byte piece and
-// does not apply merges: text tokenization is not on the decode hot path, and for files whose pieces
-// never merge (the synthetic models, whose pieces are the 256 bytes and empty strings) it gives the
-// reference's ids.
+// The tokenizer section of a .l3m file as a table of byte strings. Section layout (src/model.h:27-28):
+// a 16-byte header {u32 n_tokens, i32 bos, i32 eos, u32 max_len}, then per token {f32 score, u16 len,
+// len bytes}. The header is accepted under the reference's conditions (src/tokenizer.c:17-45): the
+// count must fit the section at 6 bytes per token at least, and bos must be an id or negative (none).
+//
+// Decoding is exact. Encoding maps each input byte to its single-byte piece and applies no merges: text
+// tokenization is not on the decode hot path, and for files whose pieces never merge (the synthetic
+// models: the 256 bytes and empty pieces) it gives the reference's ids.
 #include <stdlib.h>
 #include <string.h>
 #include "host.h"
 
+typedef struct {
+    const uint8_t *at, *end;
+} cursor;
+
+static int take(cursor *c, void *dst, size_t n) {
+    if ((size_t)(c->end - c->at) < n) return -1;
+    if (dst) memcpy(dst, c->at, n);
+    c->at += n;
+    return 0;
+}
+
 int l3m_vocab_init(l3m_vocab_table *t, const void *section, size_t size) {
-    l3m_tok_header h;
     memset(t, 0, sizeof *t);
-    if (size < sizeof h) return -1;
-    memcpy(&h, section, sizeof h);
-    if (h.n_tokens > (size - sizeof h) / 6 || h.bos >= (int64_t)h.n_tokens) return -1;
-    t->n = (int)h.n_tokens; t->bos = h.bos < 0 ? -1 : h.bos; t->eos = h.eos; t->max_len = (int)h.max_len;
-    t->bytes = malloc(((size_t)t->n + 1) * sizeof *t->bytes);
-    uint16_t *len = malloc(((size_t)t->n + 1) * sizeof *len);
+    cursor c = {(const uint8_t *)section, (const uint8_t *)section + size};
+    l3m_tok_header hdr;
+    if (take(&c, &hdr, sizeof hdr)) return -1;
+    const size_t room = (size_t)(c.end - c.at);
+    if ((size_t)hdr.n_tokens > room / 6 || (int64_t)hdr.bos >= (int64_t)hdr.n_tokens) return -1;
+    const size_t n = hdr.n_tokens;
+    const uint8_t **bytes = calloc(n + 1, sizeof *bytes);
+    uint16_t *len = calloc(n + 1, sizeof *len);
+    t->bytes = bytes;
     t->len = len;
-    if (!t->bytes || !len) { l3m_vocab_free(t); return -1; }
-    const uint8_t *p = (const uint8_t *)section + sizeof h, *end = (const uint8_t *)section + size;
-    for (int i = 0; i < t->n; i++) {
-        if (end - p < 6) { l3m_vocab_free(t); return -1; }
-        memcpy(&len[i], p + 4, 2);
-        if (end - p - 6 < len[i]) { l3m_vocab_free(t); return -1; }
-        t->bytes[i] = p + 6;
-        p += 6 + len[i];
+    if (!bytes || !len) { l3m_vocab_free(t); return -1; }
+    for (size_t i = 0; i < n; i++) {
+        if (take(&c, NULL, 4) || take(&c, &len[i], 2)) { l3m_vocab_free(t); return -1; }   // score unused
+        bytes[i] = c.at;
+        if (take(&c, NULL, len[i])) { l3m_vocab_free(t); return -1; }
     }
+    t->n = (int)n;
+    t->bos = hdr.bos < 0 ? -1 : hdr.bos;
+    t->eos = hdr.eos;
+    t->max_len = (int)hdr.max_len;
     return 0;
 }
 
@@ -35,25 +52,33 @@ void l3m_vocab_free(l3m_vocab_table *t) {
     memset(t, 0, sizeof *t);
 }
 
-static int single_byte_id(const l3m_vocab_table *t, uint8_t c) {
-    for (int i = 0; i < t->n; i++) if (t->len[i] == 1 && t->bytes[i][0] == c) return i;
+static int piece_of_byte(const l3m_vocab_table *t, uint8_t b) {
+    for (int id = 0; id < t->n; id++)
+        if (t->len[id] == 1 && t->bytes[id][0] == b) return id;
     return -1;
 }
 
 int l3m_vocab_encode(const l3m_vocab_table *t, const char *text, int add_bos, int32_t *out, int max) {
     int n = 0;
-    if (add_bos && t->bos >= 0) { if (n == max) return -1; out[n++] = t->bos; }
-    for (const uint8_t *p = (const uint8_t *)text; *p; p++) {
-        int id = single_byte_id(t, *p);
-        if (id < 0) continue;
-        if (n == max) return -1;
+    if (add_bos && t->bos >= 0) {
+        if (max < 1) return -1;
+        out[n++] = t->bos;
+    }
+    for (const char *p = text; *p; p++) {
+        const int id = piece_of_byte(t, (uint8_t)*p);
+        if (id < 0) continue;               // a byte with no piece of its own is dropped
+        if (n >= max) return -1;
         out[n++] = id;
     }
     return n;
 }
 
 const uint8_t *l3m_vocab_decode(const l3m_vocab_table *t, int32_t tok, int *len) {
-    if (tok < 0 || tok >= t->n) { *len = 0; return (const uint8_t *)""; }
+    static const uint8_t empty[1] = {0};
+    if (tok < 0 || tok >= t->n) {
+        *len = 0;
+        return empty;
+    }
     *len = t->len[tok];
     return t->bytes[tok];
 }

@@ -11,9 +11,11 @@ from pathlib import Path
 
 import numpy as np
 
+import l3m_amd
+from l3m_amd import TOKEN_CALLBACK, Opts, Perf
+
 HERE = Path(__file__).resolve().parent
 F32, BF16, Q8_0, Q4_0, MXFP4 = range(5)
-_CB = C.CFUNCTYPE(C.c_int, C.c_int32, C.c_void_p)
 
 _f = C.POINTER(C.c_float)
 _i8 = C.POINTER(C.c_int8)
@@ -133,16 +135,6 @@ class OracleModel:
         return np.ctypeslib.as_array(self.o.lib.or_logits(self.h), shape=(self.vocab,)).copy()
 
 
-class _Opts(C.Structure):
-    _fields_ = [("cpus", C.POINTER(C.c_int)), ("n_cpus", C.c_int), ("ctx", C.c_int),
-                ("reference", C.c_int), ("force", C.c_int), ("verbose", C.c_int), ("cold", C.c_int)]
-
-
-class _Perf(C.Structure):
-    _fields_ = [(f, C.c_double) for f in ("tokens", "ns_token", "ns_compute", "ns_wait", "bytes_token", "l2_bytes",
-                                           "l3_miss", "dram_bytes", "energy_j", "llc_occupancy")]
-
-
 class _Vec(C.Structure):
     _fields_ = [("f32", _f), ("bf16", _u16), ("q8", _i8), ("scale", _f), ("sum", _i32)]
 
@@ -167,24 +159,20 @@ class Reference:
         if not self.available():
             raise OSError(f"{self.PATH} missing: build it with `make -C oracle ref` where /root/reference exists")
         lib = self.lib = C.CDLL(str(self.PATH))
-        sig = {
-            "l3m_load": (C.c_void_p, [C.c_char_p, C.POINTER(_Opts)]),
-            "l3m_free": (None, [C.c_void_p]),
-            "l3m_generate": (C.c_int, [C.c_void_p, _i32, C.c_int, C.c_int, C.c_float, C.c_uint64, _CB, C.c_void_p]),
-            "l3m_logits": (_f, [C.c_void_p]),
-            "l3m_vocab": (C.c_int, [C.c_void_p]),
-            "l3m_describe": (C.c_char_p, [C.c_void_p]),
-            "l3m_perf_read": (C.c_int, [C.c_void_p, C.POINTER(_Perf)]),
+        # the reference's l3m.h entry points share the product's ctypes structs (same ABI); the rest are its
+        # internal packing and prep functions (pack.c) and the kernel tables (kernels.h)
+        api = {name: l3m_amd._SIG[name] for name in ("l3m_load", "l3m_free", "l3m_generate", "l3m_logits", "l3m_vocab",
+                                                      "l3m_describe", "l3m_perf_read", "l3m_kernels_usable")}
+        internal = {
             "l3m_tile_bytes": (C.c_size_t, [C.c_int, C.c_int]),
             "l3m_row_bytes": (C.c_size_t, [C.c_int, C.c_int]),
             "l3m_pack_tile": (None, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p), C.c_int]),
             "l3m_vec_prepare": (None, [C.POINTER(_Vec), C.c_int, _f, C.c_int, C.c_void_p]),
             "l3m_dequant_row": (None, [_f, C.c_int, C.c_void_p, C.c_int]),
-            "l3m_kernels_usable": (C.c_int, [C.c_void_p]),
         }
-        for name, (res, args) in sig.items():
-            fn = getattr(lib, name)
-            fn.restype, fn.argtypes = res, args
+        for name, (restype, argtypes) in {**api, **internal}.items():
+            entry = getattr(lib, name)
+            entry.restype, entry.argtypes = restype, argtypes
         self.tables = {n: _Table.in_dll(lib, f"l3m_kernels_{n}") for n in ("scalar", "avx2", "avx512")}
 
     def usable(self, name):
@@ -227,7 +215,7 @@ class Reference:
         return out
 
     def load(self, path, ctx=0, reference=False, cpus=None):
-        opts = _Opts(ctx=ctx, reference=int(reference), force=1)
+        opts = Opts(ctx=ctx, reference=int(reference), force=1)
         if cpus:
             arr = (C.c_int * len(cpus))(*cpus)
             opts.cpus, opts.n_cpus = arr, len(cpus)
@@ -252,7 +240,7 @@ class RefModel:
 
     def generate(self, prompt, max_new):
         out = []
-        cb = _CB(lambda t, u: out.append(t) or 1)
+        cb = TOKEN_CALLBACK(lambda t, u: out.append(t) or 1)
         p = np.ascontiguousarray(prompt, np.int32)
         n = self.r.lib.l3m_generate(self.h, _p(p, _i32), len(p), max_new, 0.0, 0, cb, None)
         assert n == len(out)
@@ -262,7 +250,7 @@ class RefModel:
         return np.ctypeslib.as_array(self.r.lib.l3m_logits(self.h), shape=(self.vocab,)).copy()
 
     def perf(self):
-        p = _Perf()
+        p = Perf()
         if self.r.lib.l3m_perf_read(self.h, C.byref(p)):
             return None
-        return {f: getattr(p, f) for f, _ in _Perf._fields_}
+        return {f: getattr(p, f) for f, _ in Perf._fields_}

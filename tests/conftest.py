@@ -69,3 +69,12 @@ class ModelCache:
 @pytest.fixture(scope="session")
 def models(tmp_path_factory):
     return ModelCache(tmp_path_factory.mktemp("models"))
+
+
+@pytest.fixture(scope="session")
+def dev_free():
+    """Host-side packing helpers of l3m_amd.Device, without initialising a GPU."""
+    import l3m_amd
+    d = l3m_amd.Device.__new__(l3m_amd.Device)
+    d.lib = l3m_amd.lib()
+    return d

@@ -150,13 +150,20 @@ def test_callback_stop_logits_and_perf(oracle, models):
     path = models.get(SMALL, "q8_0", seed=6, std=0.08, norm_jitter=0.2)
     ids = A.prompt(6, SMALL.vocab, 4)
     m = A.Model(path)
-    m.perf()
-    seen = []
-    out = m.generate(ids, 50, on_token=lambda t: seen.append(t) or len(seen) < 5)
-    assert out == seen and len(out) == 5
-    p = m.perf()
-    assert p["tokens"] == len(ids) + len(out) - 1 and p["ns_token"] > 0 and p["bytes_token"] > 0
-    assert all(np.isnan(v) for v in m.perf().values())
+    m.perf()                                   # start the counters from here
+    stop_after, heard = 5, []
+
+    def listener(tok):
+        heard.append(tok)
+        return len(heard) < stop_after
+
+    out = m.generate(ids, 50, on_token=listener)
+    assert out == heard
+    assert len(out) == stop_after
+    counters = m.perf()
+    assert counters["tokens"] == len(ids) - 1 + stop_after     # forward passes, the prompt included
+    assert counters["ns_token"] > 0 < counters["bytes_token"]
+    assert np.isnan(list(m.perf().values())).all()             # nothing ran since the last read
     # logits are the prediction after the last token fed: position len(ids) + 3
     om = oracle.load(path)
     full = om.generate(ids, 4)
