@@ -87,6 +87,28 @@ def matvec_bench(A, dtypes, iters=50):
     return out
 
 
+def measured_traffic(cfg_name, dtype, kernel):
+    """HBM bytes per launch of a step kernel (read + written), from the committed counter profile of this
+    configuration (profiles/decode_<config>_<dtype>_traffic.json: two rocprofv3 --pmc passes, FETCH_SIZE
+    and WRITE_SIZE, scaled by the plain copy kernel's readings); None when no profile covers it."""
+    import json
+    p = ROOT / "profiles" / f"decode_{cfg_name}_{dtype}_traffic.json"
+    if not p.exists():
+        return None
+    k = json.loads(p.read_text())["kernels"].get("k_" + kernel)
+    return None if k is None else k["read_bytes"] + k["write_bytes"]
+
+
+def copy_calibration(A, nbytes):
+    """One launch of the plain copy kernel over nbytes (read nbytes, write nbytes), for scaling counters."""
+    lib, dev = A.lib(), A.Device()
+    src, dst = dev.alloc(nbytes), dev.alloc(nbytes)
+    if lib.l3m_dev_copy(dst, src, nbytes, None) or lib.l3m_dev_sync():
+        raise RuntimeError("copy kernel failed")
+    dev.free_all()
+    log(f"copy: {nbytes} bytes")
+
+
 def host_cores():
     """One CPU per physical core of this process's affinity, at most 16 (the box's share for one GPU)."""
     seen, cpus = set(), []
@@ -130,6 +152,8 @@ def main():
     ap.add_argument("--dtype", default=None)
     ap.add_argument("--matvec", default="bf16,q8_0,q4_0,mxfp4", help="dtypes for the matvec microbench ('' to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="reference CPU sample length (0 to skip)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run the plain copy kernel once over this many MiB (counter calibration under rocprofv3)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this backend runs one model on one GPU; --gpus {a.gpus} is not a configuration it has "
@@ -162,6 +186,8 @@ def main():
         if cpu:
             log(f"bench: reference CPU {cpu['value']} tok/s on {cpu['cores']} cores")
     matvec = matvec_bench(A, [s for s in a.matvec.split(",") if s]) if a.matvec else None
+    if a.copy_mib:
+        copy_calibration(A, a.copy_mib << 20)
     pub = PUBLISHED.get((cfg.name, dtype))
     line = {
         "metric": "batch-1 decode tok/s + matvec weight GB/s vs roofline, per dtype",
@@ -173,7 +199,8 @@ def main():
                    "dim": cfg.dim, "layers": cfg.n_layers, "heads": cfg.n_heads, "kv_heads": cfg.n_kv_heads,
                    "ffn": cfg.ffn_dim, "vocab": cfg.vocab, "ctx": cfg.ctx, "weights": "random-init N(0,0.02), seed 1"},
         "roofline": {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic(cfg.name, dtype, dom["kernel"]),
                      "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us"], 3)},
         "step_kernels": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in kt],
         "weight_bytes_per_token": wbytes,

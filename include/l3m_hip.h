@@ -95,6 +95,7 @@ void        l3m_dev_free(void *p);
 int         l3m_dev_upload(void *dst, const void *src, size_t bytes);
 int         l3m_dev_download(void *dst, const void *src, size_t bytes);
 int         l3m_dev_sync(void);
+int         l3m_dev_copy(void *dst, const void *src, size_t bytes, void *stream);   // plain copy kernel (counter calibration)
 void       *l3m_dev_stream(void);
 
 // Lane-tile layout sizes and host-side packing (the GPU analogue of l3m_tile_bytes / l3m_pack_tile,

@@ -325,6 +325,12 @@ int pick_split(int nb) { return nb >= 16 ? 4 : nb >= 8 ? 2 : 1; }
 
 extern "C" __global__ void __launch_bounds__(NT) k_dummy() {}
 
+// A plain streaming copy of n16 16-byte words: the known-size kernel that calibrates the HBM counters
+// (FETCH_SIZE, WRITE_SIZE) against which the step kernels' traffic is read.
+__global__ void __launch_bounds__(NT) k_copy(u32x4 *__restrict__ dst, const u32x4 *__restrict__ src, size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n16; i += (size_t)gridDim.x * NT) dst[i] = src[i];
+}
+
 template <int DT>
 __global__ void __launch_bounds__(NT) k_prep(const float *__restrict__ x, int k, uint8_t *__restrict__ out) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1272,6 +1278,15 @@ int l3m_k_rope(float *v, int n_heads, int hd, int pos, const float *table, void 
 int l3m_k_silu_mul(float *h, const float *g, int n, void *stream) {
     hipLaunchKernelGGL(k_silu_mul, dim3((n + NT - 1) / NT), dim3(NT), 0, as_stream(stream), h, g, n);
     CKL("k_silu_mul");
+    return 0;
+}
+
+int l3m_dev_copy(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes % 16 || ((uintptr_t)dst | (uintptr_t)src) % 16) return fail_msg("copy: 16-byte multiples and alignment");
+    const size_t n16 = bytes / 16;
+    const unsigned grid = (unsigned)(n16 / NT < 4096 ? (n16 + NT - 1) / NT : 4096);
+    if (grid) hipLaunchKernelGGL(k_copy, dim3(grid), dim3(NT), 0, as_stream(stream), (u32x4 *)dst, (const u32x4 *)src, n16);
+    CKL("k_copy");
     return 0;
 }
 
