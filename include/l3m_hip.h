@@ -126,6 +126,9 @@ double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, f
 double l3m_bench_kernel(l3m_model *m, int kind, int layer, int pos, int iters);
 double l3m_kernel_bytes(const l3m_model *m, int kind, int pos);   // weight bytes one launch of that kernel reads
 double l3m_weight_bytes(const l3m_model *m);                       // weight bytes streamed per token
+// 1 when decode runs as one persistent cooperative kernel per chunk of steps (L3M_PERSIST=0 at load
+// selects the one-graph-per-step path), 0 otherwise.
+int    l3m_decode_persistent(const l3m_model *m);
 
 // Synthetic .l3m models (seeded, host-independent bytes).
 typedef struct {

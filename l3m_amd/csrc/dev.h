@@ -55,6 +55,15 @@ typedef struct {
     const float *norm;
 } l3m_dmodel;
 
+// One launch of the persistent decode kernel: steps at positions pos0 .. pos0 + nsteps - 1; logits (and
+// the argmax token at pos + 1) for positions >= head_from.
+typedef struct {
+    int                pos0, nsteps, head_from;
+    int                head_tpw;       // head tiles per workgroup
+    unsigned          *sync;           // [2 * n_layers + 3]: attn[L], ffn[L], head, tok, abort; zero at launch
+    unsigned long long spin_limit;     // longest wait, in ticks of the 100 MHz clock
+} l3m_run;
+
 // ------------------------------------------------------------------ runtime
 int         l3m_dev_init(void);                 // 0 when a gfx9 HIP device is usable
 const char *l3m_dev_error(void);                // sticky: the first error seen, or NULL
@@ -87,6 +96,13 @@ unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c);
 unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg);
 int      l3m_step_slots(int dtype, int which);   // weight slots per lane (matrix A / B of a step kernel), 64 pairs each
 int l3m_step_enqueue(const l3m_dmodel *m, const l3m_dlayer *layers, int with_head, void *stream);
+
+// The persistent decode kernel (one cooperative launch for R->nsteps steps; layers_dev in device memory).
+int l3m_dev_cus(void);
+int l3m_decode_fits(int dtype, int grid, unsigned lds);     // 1 if grid workgroups with lds bytes can all be resident
+// m_dev, layers_dev, r_dev: device-memory copies (the kernel reads its parameters from there)
+int l3m_decode_launch(int dtype, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev, int grid, unsigned lds,
+                      void *stream);
 
 // Timing (microseconds per launch, hipEvents on the library stream, after one untimed launch).
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);

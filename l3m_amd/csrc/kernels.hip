@@ -35,6 +35,9 @@ __host__ __device__ inline size_t align16(size_t n) { return (n + 15) & ~(size_t
 // barrier would wait for the weight stream in flight.
 #define GLOBAL __attribute__((address_space(1)))
 template <class T> __device__ __forceinline__ const GLOBAL T *gp(const void *p) { return (const GLOBAL T *)p; }
+// Stores through explicit global pointers too: a flat store also counts against the LDS counter, so the
+// next barrier would wait for it to reach memory.
+template <class T> __device__ __forceinline__ GLOBAL T *gw(T *p) { return (GLOBAL T *)p; }
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -45,6 +48,22 @@ __device__ __forceinline__ uint4 ldg16(const void *p, size_t i) {
 __device__ __forceinline__ float4 ldg16f(const void *p, size_t i) {
     const f32x4 v = gp<f32x4>(p)[i];
     return make_float4(v.x, v.y, v.z, v.w);
+}
+// 16 bytes that another workgroup wrote during this kernel: two device-coherent 8-byte loads (they read
+// past any stale copy in this XCD's L2, so no cache-wide invalidation is needed to see the data).
+__device__ __forceinline__ uint4 ldcoh16(const void *p, size_t i) {
+    const GLOBAL uint64_t *q = gp<uint64_t>(p) + 2 * i;
+    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+}
+template <bool COH> __device__ __forceinline__ uint4 ld16(const void *p, size_t i) { return COH ? ldcoh16(p, i) : ldg16(p, i); }
+template <bool COH> __device__ __forceinline__ float4 ld16f(const void *p, size_t i) {
+    if constexpr (COH) {
+        const uint4 u = ldcoh16(p, i);
+        return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+    }
+    return ldg16f(p, i);
 }
 
 // ------------------------------------------------------------------------------------------ scalars
@@ -463,6 +482,16 @@ __global__ void __launch_bounds__(NT) k_argmax(const float *x, int n, int32_t *o
 
 constexpr int NTE = 1024, NWE = NTE / 64;
 
+// The thread's index, read through an opaque move: values derived from it are then computed where they
+// are used. Otherwise the compiler hoists every lane-dependent address out of the persistent kernel's
+// layer and step loops and keeps them all live across it, which spills.
+__device__ __forceinline__ int tidx() {
+    int t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+    return t;
+}
+
+
 // Weight slots per lane: a step kernel streams matrix A (qkv, gate/up, head rows) and matrix B (Wo,
 // Wdown columns), each through its own register array; 64 (tile, block) pairs per slot and workgroup.
 template <int DT> constexpr int nslot_a() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 5 : 6; }
@@ -484,7 +513,7 @@ struct Pref {
 template <int DT, int NS>
 __device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, int s0) {
     constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
-    const int wave = threadIdx.x >> 6, sub = (threadIdx.x >> 4) & 3, row = threadIdx.x & 15, n = m.tiles * m.nb;
+    const int wave = tidx() >> 6, sub = (tidx() >> 4) & 3, row = tidx() & 15, n = m.tiles * m.nb;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         int p = (wave + (s0 + s) * NWE) * 4 + sub;
@@ -501,7 +530,7 @@ __device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, i
 // res[pair * 16 + row] for this lane's slots.
 template <int DT, int NS>
 __device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m, int s0, const uint8_t *act, int kp, float *res) {
-    const int wave = threadIdx.x >> 6, sub = (threadIdx.x >> 4) & 3, row = threadIdx.x & 15, n = m.tiles * m.nb;
+    const int wave = tidx() >> 6, sub = (tidx() >> 4) & 3, row = tidx() & 15, n = m.tiles * m.nb;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         // Pin the loaded registers here: otherwise the compiler hoists their first use (the f16 scale
@@ -516,7 +545,7 @@ __device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m
 
 // All pairs of m: the prefetched batch, then any further batches (loaded here).
 template <int DT, int NS>
-__device__ void mv(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int kp, float *res) {
+__device__ __forceinline__ void mv(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int kp, float *res) {
     pref_compute<DT, NS>(pf, m, 0, act, kp, res);
     for (int s0 = NS; s0 * NWE * 4 < m.tiles * m.nb; s0 += NS) {
         pref_load<DT, NS>(pf, m, s0);
@@ -595,16 +624,16 @@ struct Red {
 };
 __device__ __forceinline__ const float *red_publish(Red &r, float v) {
     float *s = r.scr + 16 * (r.k++ & 1);
-    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = v;
+    if ((tidx() & 63) == 0) s[tidx() >> 6] = v;
     __syncthreads();
     return s;
 }
-__device__ float red_sum(Red &r, float v) {
+__device__ __forceinline__ float red_sum(Red &r, float v) {
     const float4 *s = (const float4 *)red_publish(r, lanes_sum<64>(v));
     const float4 a = s[0], b = s[1], c = s[2], d = s[3];
     return (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) + (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
 }
-__device__ float red_max(Red &r, float v) {
+__device__ __forceinline__ float red_max(Red &r, float v) {
     const float4 *s = (const float4 *)red_publish(r, lanes_max<64>(v));
     const float4 a = s[0], b = s[1], c = s[2], d = s[3];
     return fmaxf(fmaxf(fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)), fmaxf(fmaxf(b.x, b.y), fmaxf(b.z, b.w))),
@@ -618,7 +647,7 @@ __device__ void wge_argmax(float &v, int &i, float *sv, int *si) {
         better(v, i, v2, i2);
     }
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = v; si[threadIdx.x >> 6] = i; }
+    if ((tidx() & 63) == 0) { sv[tidx() >> 6] = v; si[tidx() >> 6] = i; }
     __syncthreads();
     v = sv[0]; i = si[0];
     for (int w = 1; w < NWE; w++) better(v, i, sv[w], si[w]);
@@ -629,9 +658,9 @@ __device__ void wge_argmax(float &v, int &i, float *sv, int *si) {
 // f(i, y, partner) runs in every lane for rows i < rows, partner being row i ^ 1's value.
 template <class F>
 __device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, int rows, F f) {
-    const int nb = m.nb, q = threadIdx.x & 3, b0 = q * nb >> 2, b1 = (q + 1) * nb >> 2;
+    const int nb = m.nb, q = tidx() & 3, b0 = q * nb >> 2, b1 = (q + 1) * nb >> 2;
     for (int base = 0; base < rows; base += NTE / 4) {
-        const int i = base + (threadIdx.x >> 2);
+        const int i = base + (tidx() >> 2);
         float y = 0.f;
         if (i < rows) {
             const float *p = res + (size_t)(i >> 4) * nb * 16 + (i & 15);
@@ -671,17 +700,18 @@ __device__ __forceinline__ ProGeom pro_geom(int dim, int nparts) {
 // Loads are unconditional (indices clamped into range) wherever possible: a load under a branch that
 // later merges makes the compiler wait for it there, before the weight stream is issued.
 // embed is passed by value: a pointer into the kernel's argument struct would move that struct to scratch.
+template <bool COH>
 __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float *parts, int nparts, int dim, const float *nw,
                                          l3m_dmat embed, bool use_embed, int tok, const float *rope_row, int hd) {
-    const int tid = threadIdx.x;
+    const int tid = tidx();
     const ProGeom G = pro_geom(dim, nparts);
     const int f = tid % G.n4, grp = tid / G.n4, j0 = grp * G.per, own = tid < G.n4 ? tid : G.n4 - 1;
     P.nw = ldg16f(nw, own);
-    P.base = ldg16f(base, f);
+    P.base = ld16f<COH>(base, f);
 #pragma unroll
     for (int j = 0; j < FILL_PER; j++) {
         const int pj = j0 + j < nparts ? j0 + j : nparts - 1;
-        P.p[j] = ldg16f(parts + (size_t)pj * dim, f);
+        P.p[j] = ld16f<COH>(parts + (size_t)pj * dim, f);
     }
     if (rope_row) {
         const int i = tid < (hd >> 1) ? tid : (hd >> 1) - 1;
@@ -692,9 +722,10 @@ __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float 
 }
 // Returns x[4f, 4f+4) to owner f (zeros to the other threads); stores it to keep when given; writes the
 // RoPE angles to cs_lds when given. pbuf: NTE float4 of LDS. All threads call it.
-__device__ float4 pro_finish(Pro &P, const float *parts, int nparts, int dim, bool use_embed, float4 *pbuf, float *keep,
+template <bool COH>
+__device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, int nparts, int dim, bool use_embed, float4 *pbuf, float *keep,
                              float *cs_lds, int hd) {
-    const int tid = threadIdx.x;
+    const int tid = tidx();
     const ProGeom G = pro_geom(dim, nparts);
     const int f = tid % G.n4, grp = tid / G.n4, j0 = grp * G.per;
     if (cs_lds && tid < (hd >> 1)) ((float2 *)cs_lds)[tid] = P.cs;
@@ -710,7 +741,7 @@ __device__ float4 pro_finish(Pro &P, const float *parts, int nparts, int dim, bo
                 v.x += use ? P.p[j].x : 0.f; v.y += use ? P.p[j].y : 0.f; v.z += use ? P.p[j].z : 0.f; v.w += use ? P.p[j].w : 0.f;
             }
             for (int j = FILL_PER; j < G.per && j0 + j < nparts; j++) {   // beyond one batch: in order
-                const float4 p = ldg16f(parts + (size_t)(j0 + j) * dim, f);
+                const float4 p = ld16f<COH>(parts + (size_t)(j0 + j) * dim, f);
                 v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
             }
             if (G.groups > 1) pbuf[grp * G.n4 + f] = v;
@@ -727,7 +758,10 @@ __device__ float4 pro_finish(Pro &P, const float *parts, int nparts, int dim, bo
             }
         }
     }
-    if (keep && tid < G.n4) ((float4 *)keep)[tid] = x;
+    if (keep && tid < G.n4) {
+        const f32x4 v = {x.x, x.y, x.z, x.w};
+        gw((f32x4 *)keep)[tid] = v;
+    }
     return x;
 }
 
@@ -735,8 +769,8 @@ __device__ float4 pro_finish(Pro &P, const float *parts, int nparts, int dim, bo
 // (zero beyond k): the reference's per-32-block int8 quantization (8 lanes per block), bf16 or f32.
 // Ends with a barrier.
 template <int DT>
-__device__ void prep_owned(float4 y, uint8_t *act, int kp) {
-    const int f = threadIdx.x;
+__device__ __forceinline__ void prep_owned(float4 y, uint8_t *act, int kp) {
+    const int f = tidx();
     if constexpr (quantized(DT)) {
         float am = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
         am = lanes_max<8>(am);
@@ -762,11 +796,11 @@ __device__ void prep_owned(float4 y, uint8_t *act, int kp) {
 
 // RMSNorm (ops.c:13-18: s = 1/sqrt(sum x^2 / n + eps), y = x * s * w) of the owned x, then its prep.
 template <int DT>
-__device__ void norm_prep(float4 x, float4 nw, int k, int kp, float eps, uint8_t *act, Red &red) {
+__device__ __forceinline__ void norm_prep(float4 x, float4 nw, int k, int kp, float eps, uint8_t *act, Red &red) {
     const float tot = red_sum(red, x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
     const float s = 1.0f / sqrtf(tot / (float)k + eps);
     float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * (int)threadIdx.x < k) y = make_float4(x.x * s * nw.x, x.y * s * nw.y, x.z * s * nw.z, x.w * s * nw.w);
+    if (4 * (int)tidx() < k) y = make_float4(x.x * s * nw.x, x.y * s * nw.y, x.z * s * nw.z, x.w * s * nw.w);
     prep_owned<DT>(y, act, kp);
 }
 
@@ -823,8 +857,9 @@ __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg)
 // K and V rows 0..pos-1 of the group's kv heads, copied from the cache into LDS [K | V][nkv][ctx][hd] by
 // the memory unit (global_load_lds_dwordx4: 64 lanes x 16 bytes into 1 KiB of LDS, no registers).
 // Rows up to pos - 1 were written by earlier steps, so the copy can start at the top of the kernel.
+template <bool COH>
 __device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int kv0, int nkv, int pos) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = tidx() >> 6, lane = tidx() & 63;
     const size_t win = (size_t)M.ctx * M.hd, total = (size_t)pos * M.hd * 2;     // bytes per head, K or V
     const int nch = (int)((total + 1023) / 1024), items = 2 * nkv * nch;
     for (int it = wave; it < items; it += NWE) {
@@ -834,7 +869,7 @@ __device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int
         uint8_t *dst = (uint8_t *)(kvb + ((size_t)which * nkv + j) * win) + (size_t)c * 1024;
         if (byte < total)
             __builtin_amdgcn_global_load_lds((const GLOBAL void *)((const uint8_t *)src + byte),
-                                             (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+                                             (__attribute__((address_space(3))) void *)dst, 16, 0, COH ? 16 : 0);   // 16: sc1
     }
 }
 
@@ -852,11 +887,11 @@ __device__ __forceinline__ float dot8_bf16(const float *q, uint4 k, float acc) {
 // positions g, g + NTE/LP, ... per lane group, then across lane groups (in a wavefront, then over the
 // wavefronts through LDS). K, V rows before pos come from the LDS window (WIN) or the cache, row pos
 // from cur (this step's rows, bf16 as the cache holds them).
-template <bool WIN>
+template <bool WIN, bool COH>
 __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer, int pos, const float *qh, const uint16_t *cur,
                              const uint16_t *kvb, float *sc, float *vred, float *att, Red &red) {
     const int hd = M.hd, nv = hd >> 3, LP = nv <= 4 ? 4 : nv <= 8 ? 8 : nv <= 16 ? 16 : 32;
-    const int tid = threadIdx.x, lane = tid & 63, j = tid & (LP - 1), g = tid / LP, NG = NTE / LP, n = pos + 1;
+    const int tid = tidx(), lane = tid & 63, j = tid & (LP - 1), g = tid / LP, NG = NTE / LP, n = pos + 1;
     const int hpk = M.n_heads / M.n_kv;
     const float scale = 1.0f / sqrtf((float)hd);
     const size_t win = (size_t)M.ctx * hd;
@@ -879,7 +914,7 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
                 uint4 kk;
                 if (t == pos) kk = kcur[j];
                 else if (WIN) kk = ((const uint4 *)(kw + (size_t)t * hd))[j];
-                else kk = ldg16(kw + (size_t)t * hd, j);
+                else kk = ld16<COH>(kw + (size_t)t * hd, j);
                 part = dot8_bf16(q, kk, 0.f);
             }
             const float s = lanes_sum_n(part, LP) * scale;
@@ -903,7 +938,7 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
                 uint4 vv;
                 if (t == pos) vv = vcur[j];
                 else if (WIN) vv = ((const uint4 *)(vw + (size_t)t * hd))[j];
-                else vv = ldg16(vw + (size_t)t * hd, j);
+                else vv = ld16<COH>(vw + (size_t)t * hd, j);
                 o[0] = fmaf(p, bf16_f32(vv.x & 0xFFFF), o[0]); o[1] = fmaf(p, bf16_f32(vv.x >> 16), o[1]);
                 o[2] = fmaf(p, bf16_f32(vv.y & 0xFFFF), o[2]); o[3] = fmaf(p, bf16_f32(vv.y >> 16), o[3]);
                 o[4] = fmaf(p, bf16_f32(vv.z & 0xFFFF), o[4]); o[5] = fmaf(p, bf16_f32(vv.z >> 16), o[5]);
@@ -926,12 +961,36 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
     }
 }
 
-// Kernel A: the attention block of one head group (engine.c:236-258).
-template <int DT>
-__global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw, int layer) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const l3m_dgroup G = Lw.groups[blockIdx.x];
-    const int tid = threadIdx.x, pos = *M.pos, dim = M.dim, hd = M.hd, kp = kpad(dim);
+// ------------------------------------------------------------------ step blocks (device functions)
+// One block each for the attention of a head group, the FFN of a chunk and a slice of the head. The
+// graph path launches each as its own kernel (k_attn_block, k_ffn_block, k_head_block); the persistent
+// path (k_decode) calls them from resident workgroups. PRE: the block's weights were issued into w
+// already (the persistent path issues them while it waits for the block's inputs); otherwise they are
+// issued right after the prologue's loads.
+
+template <int DT> struct AttnW { Pref<DT, nslot_a<DT>()> a; Pref<DT, nslot_wo<DT>()> b; };
+template <int DT> struct FfnW { Pref<DT, nslot_a<DT>()> a; Pref<DT, nslot_b<DT>()> b; };
+template <int DT> struct HeadW { Pref<DT, nslot_a<DT>() + nslot_b<DT>()> a; };
+
+template <int DT> __device__ __forceinline__ void attn_issue(AttnW<DT> &w, const l3m_dgroup &G) {
+    pref_load<DT, nslot_a<DT>()>(w.a, G.qkv, 0);
+    pref_load<DT, nslot_wo<DT>()>(w.b, G.wo, 0);
+}
+template <int DT> __device__ __forceinline__ void ffn_issue(FfnW<DT> &w, const l3m_dchunk &C) {
+    pref_load<DT, nslot_a<DT>()>(w.a, C.gate_up, 0);
+    pref_load<DT, nslot_b<DT>()>(w.b, C.down, 0);
+}
+template <int DT> __device__ __forceinline__ void head_issue(HeadW<DT> &w, const l3m_dmat &V) {
+    pref_load<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, 0);
+}
+
+// The attention block of head group gi (engine.c:236-258) at `layer`, position pos: x = xb + the FFN
+// partials (layer 0: the embedding row of tokens[pos]), RMSNorm, prep, the group's q/k/v rows, RoPE,
+// bf16 K/V into the cache, attention, prep, the group's Wo columns -> po[gi]. Group 0 keeps x in xa.
+template <int DT, bool PRE>
+__device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dgroup &G, int layer, int pos,
+                                           int tok, int gi, AttnW<DT> &w, uint8_t *smem) {
+    const int tid = tidx(), dim = M.dim, hd = M.hd, kp = kpad(dim);
     const LdsA L = lds_a(DT, dim, M.ctx, hd, G, M.kv_lds);
     float *work = (float *)(smem + L.work), *qh = (float *)(smem + L.q), *cs = (float *)(smem + L.cs);
     float *sc = (float *)(smem + L.sc), *vred = (float *)(smem + L.vred), *att = (float *)(smem + L.att);
@@ -940,19 +999,15 @@ __global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw,
     Red red{(float *)(smem + L.scr), 0};
 
     Pro P;
-    pro_load(P, M.xb, M.pd, M.n_chunks, dim, Lw.attn_norm, M.embed, layer == 0, layer ? 0 : M.tokens[pos],
-             M.rope + (size_t)pos * hd, hd);
-    Pref<DT, nslot_a<DT>()> pa;
-    Pref<DT, nslot_wo<DT>()> pb;
-    pref_load<DT, nslot_a<DT>()>(pa, G.qkv, 0);
-    pref_load<DT, nslot_wo<DT>()>(pb, G.wo, 0);
-    const float4 x = pro_finish(P, M.pd, M.n_chunks, dim, layer == 0, (float4 *)work, blockIdx.x == 0 ? M.xa : nullptr, cs, hd);
+    pro_load<PRE>(P, M.xb, M.pd, M.n_chunks, dim, Lw.attn_norm, M.embed, layer == 0, tok, M.rope + (size_t)pos * hd, hd);
+    if constexpr (!PRE) attn_issue<DT>(w, G);
+    const float4 x = pro_finish<PRE>(P, M.pd, M.n_chunks, dim, layer == 0, (float4 *)work, gi == 0 ? M.xa : nullptr, cs, hd);
     // K, V rows 0..pos-1 (no dependence on this step). Issued after the prologue is consumed: a copy of
     // data-dependent length ahead of it would make the compiler wait for every load in flight there.
-    if (M.kv_lds) kv_window_dma(kvb, M, layer, G.kv0, G.nkv, pos);
+    if (M.kv_lds) kv_window_dma<PRE>(kvb, M, layer, G.kv0, G.nkv, pos);
     norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
 
-    mv<DT, nslot_a<DT>()>(pa, G.qkv, act, kp, work);
+    mv<DT, nslot_a<DT>()>(w.a, G.qkv, act, kp, work);
     __syncthreads();
     // q, k rows: RoPE on pairs (2i, 2i+1) of each head by the angle i (ops.c:29-40); k, v rows rounded
     // to bf16 as the cache holds them (engine.c:247-248), into cur and (for the heads this group writes)
@@ -964,54 +1019,50 @@ __global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw,
             const float2 c = ((const float2 *)cs)[(local % hd) >> 1];
             y = (i & 1) ? partner * c.y + y * c.x : y * c.x - partner * c.y;
         }
-        if ((threadIdx.x & 3) == 0) {
+        if ((tidx() & 3) == 0) {
             if (i < nqd) qh[i] = y;
             else {
                 const int r = i - nqd, kv = r < nkd ? 0 : 1, jj = r - kv * nkd, kvl = jj / hd;
                 const uint16_t hb = f32_bf16(y);
                 cur[kv * nkd + jj] = hb;
                 if (G.write_kv >> kvl & 1u)
-                    (kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + jj % hd] = hb;
+                    gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + jj % hd] = hb;
             }
         }
     });
     if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (M.kv_lds) attend_group<true>(M, G, layer, pos, qh, cur, kvb, sc, vred, att, red);
-    else attend_group<false>(M, G, layer, pos, qh, cur, kvb, sc, vred, att, red);
+    if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, sc, vred, att, red);
+    else attend_group<false, PRE>(M, G, layer, pos, qh, cur, kvb, sc, vred, att, red);
 
     // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
     const int kq = kpad(nqd);
     prep_owned<DT>(4 * tid < nqd ? ((const float4 *)att)[tid] : make_float4(0.f, 0.f, 0.f, 0.f), act2, kq);
-    mv<DT, nslot_wo<DT>()>(pb, G.wo, act2, kq, work);
+    mv<DT, nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
     __syncthreads();
-    float *po = M.po + (size_t)blockIdx.x * dim;
-    rows_sum4(G.wo, work, dim, [&](int i, float y, float) { if ((threadIdx.x & 3) == 0) po[i] = y; });
+    float *po = M.po + (size_t)gi * dim;
+    rows_sum4(G.wo, work, dim, [&](int i, float y, float) { if ((tidx() & 3) == 0) gw(po)[i] = y; });
 }
 
-// Kernel B: the FFN block of one chunk of ffn rows (engine.c:259-275). The last layer of a step without
-// the head advances the position (nothing in this kernel reads it).
-template <int DT>
-__global__ void __launch_bounds__(NTE) k_ffn_block(l3m_dmodel M, l3m_dlayer Lw, int advance) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const l3m_dchunk C = Lw.chunks[blockIdx.x];
-    const int tid = threadIdx.x, dim = M.dim, kp = kpad(dim);
+// The FFN block of chunk ci (engine.c:259-275): x = xa + the attention partials, RMSNorm, prep, the
+// chunk's gate and up rows, SiLU(gate) * up, prep, its Wdown columns -> pd[ci]. Chunk 0 keeps x in xb.
+template <int DT, bool PRE>
+__device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dchunk &C, int ci, FfnW<DT> &w,
+                                          uint8_t *smem) {
+    const int tid = tidx(), dim = M.dim, kp = kpad(dim);
     const LdsB L = lds_b(DT, dim, C);
     float *work = (float *)(smem + L.work), *gu = (float *)(smem + L.gu);
     uint8_t *act = smem + L.act, *act2 = smem + L.act2;
     Red red{(float *)(smem + L.scr), 0};
 
     Pro P;
-    pro_load(P, M.xa, M.po, M.n_groups, dim, Lw.ffn_norm, M.embed, false, 0, nullptr, 0);     // x += proj (engine.c:259)
-    Pref<DT, nslot_a<DT>()> pa;
-    Pref<DT, nslot_b<DT>()> pb;
-    pref_load<DT, nslot_a<DT>()>(pa, C.gate_up, 0);
-    pref_load<DT, nslot_b<DT>()>(pb, C.down, 0);
-    const float4 x = pro_finish(P, M.po, M.n_groups, dim, false, (float4 *)work, blockIdx.x == 0 ? M.xb : nullptr, nullptr, 0);
+    pro_load<PRE>(P, M.xa, M.po, M.n_groups, dim, Lw.ffn_norm, M.embed, false, 0, nullptr, 0);     // x += proj (engine.c:259)
+    if constexpr (!PRE) ffn_issue<DT>(w, C);
+    const float4 x = pro_finish<PRE>(P, M.po, M.n_groups, dim, false, (float4 *)work, ci == 0 ? M.xb : nullptr, nullptr, 0);
     norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
-    mv<DT, nslot_a<DT>()>(pa, C.gate_up, act, kp, work);
+    mv<DT, nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
     __syncthreads();
-    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float) { if ((threadIdx.x & 3) == 0) gu[i] = y; });
+    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float) { if ((tidx() & 3) == 0) gu[i] = y; });
     __syncthreads();
     // h = up * silu(gate) (ops.c:49-51) for the owned 4 rows (gate tile t and up tile t interleave), prepared
     const int kf = kpad(C.nf);
@@ -1026,49 +1077,97 @@ __global__ void __launch_bounds__(NTE) k_ffn_block(l3m_dmodel M, l3m_dlayer Lw, 
         hv = make_float4(hh[0], hh[1], hh[2], hh[3]);
     }
     prep_owned<DT>(hv, act2, kf);
-    mv<DT, nslot_b<DT>()>(pb, C.down, act2, kf, work);
+    mv<DT, nslot_b<DT>()>(w.b, C.down, act2, kf, work);
     __syncthreads();
-    float *pd = M.pd + (size_t)blockIdx.x * dim;
-    rows_sum4(C.down, work, dim, [&](int i, float y, float) { if ((threadIdx.x & 3) == 0) pd[i] = y; });
-    if (advance && blockIdx.x == 0 && tid == 0) *M.pos += 1;
+    float *pd = M.pd + (size_t)ci * dim;
+    rows_sum4(C.down, work, dim, [&](int i, float y, float) { if ((tidx() & 3) == 0) gw(pd)[i] = y; });
 }
 
-// Final norm + head rows -> logits slot, then the greedy argmax (engine.c:277-301): each workgroup
-// reduces its rows; the last workgroup to finish reduces the partials in index order, writes
-// tokens[pos + 1], resets the counter and (advance) moves pos on.
-template <int DT>
-__global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x, tpw = M.head_tiles_per_wg, t0 = blockIdx.x * tpw;
-    l3m_dmat V = M.head;                                    // this workgroup's tiles of the head
+// Tiles [t0, t0 + tpw) of the head as a matrix of their own (the last slice may be short).
+__device__ __forceinline__ l3m_dmat head_slice(const l3m_dmodel &M, int t0, int tpw) {
+    l3m_dmat V = M.head;
     const int nt = t0 + tpw <= V.tiles ? tpw : V.tiles - t0;
-    V.q += (size_t)t0 * V.nb * 16 * qbytes(DT);
-    if (sbytes(DT)) V.s += (size_t)t0 * V.nb * 16 * sbytes(DT);
+    V.q += (size_t)t0 * V.nb * 16 * qbytes(V.dtype);
+    if (sbytes(V.dtype)) V.s += (size_t)t0 * V.nb * 16 * sbytes(V.dtype);
     V.tiles = nt;
     V.rows = nt * 16 < M.vocab - t0 * 16 ? nt * 16 : M.vocab - t0 * 16;
-    const int pos = *M.pos, dim = M.dim, kp = kpad(dim);
+    return V;
+}
+
+// Final norm and the head rows of slice V (tiles from t0) at position pos (engine.c:277-301): logits
+// into slot pos % nslots, and this slice's (max, lowest index) in v, idx for every thread.
+template <int DT, bool PRE>
+__device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &V, int t0, int tpw, int pos, HeadW<DT> &w,
+                                           uint8_t *smem, float &v, int &idx) {
+    const int tid = tidx(), dim = M.dim, kp = kpad(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
     float *work = (float *)(smem + L.work), *y = (float *)(smem + L.y), *scr = (float *)(smem + L.scr);
     uint8_t *act = smem + L.act;
     Red red{scr, 0};
 
     Pro P;
-    pro_load(P, M.xb, M.pd, M.n_chunks, dim, M.norm, M.embed, false, 0, nullptr, 0);     // x += down (engine.c:275), last layer
-    Pref<DT, nslot_a<DT>() + nslot_b<DT>()> pa;
-    pref_load<DT, nslot_a<DT>() + nslot_b<DT>()>(pa, V, 0);
-    const float4 x = pro_finish(P, M.pd, M.n_chunks, dim, false, (float4 *)work, nullptr, nullptr, 0);
+    pro_load<PRE>(P, M.xb, M.pd, M.n_chunks, dim, M.norm, M.embed, false, 0, nullptr, 0);     // x += down (engine.c:275), last layer
+    if constexpr (!PRE) head_issue<DT>(w, V);
+    const float4 x = pro_finish<PRE>(P, M.pd, M.n_chunks, dim, false, (float4 *)work, nullptr, nullptr, 0);
     norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
-    mv<DT, nslot_a<DT>() + nslot_b<DT>()>(pa, V, act, kp, work);
+    mv<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work);
     __syncthreads();
-    rows_sum4(V, work, V.rows, [&](int i, float yy, float) { if ((threadIdx.x & 3) == 0) y[i] = yy; });
+    rows_sum4(V, work, V.rows, [&](int i, float yy, float) { if ((tidx() & 3) == 0) y[i] = yy; });
     __syncthreads();
     float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab + (size_t)t0 * 16;
-    float v = -INFINITY;
-    int idx = 0x7FFFFFFF;
-    if (tid < V.rows) { lg[tid] = y[tid]; v = y[tid]; idx = t0 * 16 + tid; }
+    v = -INFINITY;
+    idx = 0x7FFFFFFF;
+    if (tid < V.rows) { gw(lg)[tid] = y[tid]; v = y[tid]; idx = t0 * 16 + tid; }
     wge_argmax(v, idx, scr, (int *)scr + 16);
+}
+
+// The argmax over n (value, index) partials, in index order (engine.c:294-300), into every thread.
+__device__ void reduce_partials(const float *val, const int *idx_in, int n, float *scr, float &v, int &idx) {
+    v = -INFINITY;
+    idx = 0x7FFFFFFF;
+    for (int w = tidx(); w < n; w += NTE) {
+        const float pv = __hip_atomic_load(gp<float>(val + w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int pi = __hip_atomic_load(gp<int>(idx_in + w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        better(v, idx, pv, pi);
+    }
+    wge_argmax(v, idx, scr, (int *)scr + 16);
+}
+
+// ------------------------------------------------------------------ the graph path: one kernel per block
+
+template <int DT>
+__global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw, int layer) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const l3m_dgroup G = Lw.groups[blockIdx.x];
+    AttnW<DT> w;
+    const int pos = *M.pos;
+    attn_block<DT, false>(M, Lw, G, layer, pos, layer ? 0 : M.tokens[pos], blockIdx.x, w, smem);
+}
+
+// The last layer of a step without the head advances the position (nothing in this kernel reads it).
+template <int DT>
+__global__ void __launch_bounds__(NTE) k_ffn_block(l3m_dmodel M, l3m_dlayer Lw, int advance) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const l3m_dchunk C = Lw.chunks[blockIdx.x];
+    FfnW<DT> w;
+    ffn_block<DT, false>(M, Lw, C, blockIdx.x, w, smem);
+    if (advance && blockIdx.x == 0 && tidx() == 0) *M.pos += 1;
+}
+
+// Each workgroup reduces its slice; the last one to finish reduces the partials, writes tokens[pos + 1],
+// resets the counter and (advance) moves pos on.
+template <int DT>
+__global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tpw = M.head_tiles_per_wg, t0 = blockIdx.x * tpw, pos = *M.pos;
+    const l3m_dmat V = head_slice(M, t0, tpw);
+    HeadW<DT> w;
+    float v;
+    int idx;
+    head_block<DT, false>(M, V, t0, tpw, pos, w, smem, v, idx);
+    float *scr = (float *)(smem + lds_h(DT, M.dim, M.head.nb, tpw).scr);
     __shared__ int last;
-    if (tid == 0) {
+    if (tidx() == 0) {
         M.part_val[blockIdx.x] = v;
         M.part_idx[blockIdx.x] = idx;
         __threadfence();
@@ -1077,20 +1176,199 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
     __syncthreads();
     if (!last) return;
     __threadfence();
-    v = -INFINITY;
-    idx = 0x7FFFFFFF;
-    for (int w = tid; w < (int)gridDim.x; w += NTE) {
-        const float pv = __hip_atomic_load(M.part_val + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int pi = __hip_atomic_load(M.part_idx + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        better(v, idx, pv, pi);
-    }
-    wge_argmax(v, idx, scr, (int *)scr + 16);
-    if (tid == 0) {
+    reduce_partials(M.part_val, M.part_idx, gridDim.x, scr, v, idx);
+    if (tidx() == 0) {
         if (advance) {
             M.tokens[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
             *M.pos = pos + 1;
         }
         *M.done = 0;
+    }
+}
+
+// ------------------------------------------------------------------ the persistent path
+// k_decode runs R.nsteps decode steps in one cooperative launch. Workgroup w keeps its roles for every
+// layer and step: the attention block of head group w (w < n_groups), the FFN block of chunk
+// w - n_groups (next n_chunks workgroups), and, in steps that need logits, head tiles
+// [w * head_tpw, (w + 1) * head_tpw). Phases hand over through counters in R.sync that only grow during
+// the launch (the host zeroes them before it):
+//   attn[l] += 1 per group after layer l's partial is written; ffn[l] likewise per chunk;
+//   head   += 1 per workgroup after its argmax partial; the last one reduces them and bumps tok.
+// A producer makes its stores visible with an agent-scope release (the L2 of its XCD written back)
+// before its increment; a consumer polls with agent-scope loads and acquires (its L2 invalidated)
+// before reading. Every wait is bounded: past R.spin_limit ticks of the 100 MHz clock the waiter raises
+// R.sync[abort] and every workgroup leaves at its next wait, so the grid always drains.
+
+__device__ bool wait_at_least(const unsigned *ctr, unsigned target, unsigned *abort_flag, unsigned long long limit, int *ok_lds) {
+    if (tidx() == 0) {
+        int ok = 1;
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        for (unsigned spin = 0; __hip_atomic_load(gp<unsigned>(ctr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; spin++) {
+            if ((spin & 31) == 31) {
+                if (__hip_atomic_load(gp<unsigned>(abort_flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) { ok = 0; break; }
+                if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
+                    __hip_atomic_store(gw(abort_flag), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = 0;
+                    break;
+                }
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        // No acquire fence (it would invalidate this XCD's whole L2): what the producers wrote is read
+        // with device-coherent loads (ldcoh16, the K/V copy with sc1, atomic loads of tokens and partials).
+        *ok_lds = ok;
+    }
+    __syncthreads();
+    const int ok = *ok_lds;
+    __syncthreads();                                  // ok_lds is free again
+    return ok != 0;
+}
+
+// Every thread's stores, then one increment that publishes them (returns the old count to thread 0).
+__device__ unsigned publish(unsigned *ctr) {
+    __syncthreads();
+    unsigned old = 0;
+    if (tidx() == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        old = __hip_atomic_fetch_add(gw(ctr), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return old;
+}
+
+// A 64-bit value through readfirstlane, one 32-bit half at a time. The builtin returns a signed int, so
+// each half is taken back as uint32_t before it is widened (a sign-extended low half would set every
+// high bit of the address).
+__device__ __forceinline__ uint64_t first_lane64(uint64_t u) {
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+    return (uint64_t)hi << 32 | (uint64_t)lo;
+}
+// Arguments of a function that is not inlined arrive in vector registers; these are uniform, so say so
+// (scalar registers, scalar loads, uniform branches).
+template <class T> __device__ __forceinline__ T *uniform(T *p) { return (T *)first_lane64((uint64_t)p); }
+// Parameters that stay fixed during a launch (the model, the run, the layer descriptors), read through the
+// constant address space: scalar loads into scalar registers.
+#define CONSTANT __attribute__((address_space(4)))
+template <class T> __device__ __forceinline__ T fixed(const T *p, int i = 0) {
+    static_assert(sizeof(T) % 4 == 0, "copied as 32-bit words");
+    const CONSTANT uint32_t *src = (const CONSTANT uint32_t *)uniform(p) + (size_t)i * (sizeof(T) / 4);
+    T v;
+    uint32_t *dst = (uint32_t *)&v;
+#pragma unroll
+    for (size_t k = 0; k < sizeof(T) / 4; k++) dst[k] = src[k];
+    return v;
+}
+// The same pointer, hidden from the optimizer, so loads through it are redone inside a loop (where
+// they are used) instead of being hoisted in front of it and held in registers across the whole loop.
+template <class T> __device__ __forceinline__ const T *per_iteration(const T *p) {
+    uint64_t u = first_lane64((uint64_t)p);
+    asm volatile("" : "+s"(u));
+    return (const T *)u;
+}
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ unsigned uniform(unsigned v) { return (unsigned)__builtin_amdgcn_readfirstlane((int)v); }
+
+// The roles of one step, each in a function of its own (so each gets its own register allocation and
+// nothing of one role stays live in the other). They return false when the run is being abandoned.
+template <int DT>
+__device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *layers, const l3m_run *Rp, int w, int s, unsigned heads) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int ok_lds;
+    w = uniform(w); s = uniform(s); heads = uniform(heads);
+    const int nl = fixed(Mp).n_layers;
+    for (int l = 0; l < nl; l++) {
+        const l3m_dmodel M = fixed(per_iteration(Mp));
+        const l3m_run R = fixed(per_iteration(Rp));
+        const int pos = R.pos0 + s;
+        unsigned *attn_cnt = R.sync, *ffn_cnt = R.sync + nl, *tok_cnt = R.sync + 2 * nl + 1, *abort_flag = R.sync + 2 * nl + 2;
+        const bool prev_head = s > 0 && pos - 1 >= R.head_from;
+        const l3m_dlayer Lw = fixed(layers, l);
+        const l3m_dgroup G = fixed(Lw.groups, w);
+        AttnW<DT> wt;
+        attn_issue<DT>(wt, G);
+        bool ok = true;
+        if (l > 0) ok = wait_at_least(ffn_cnt + l - 1, (unsigned)(s + 1) * M.n_chunks, abort_flag, R.spin_limit, &ok_lds);
+        else if (prev_head) ok = wait_at_least(tok_cnt, heads, abort_flag, R.spin_limit, &ok_lds);
+        else if (s > 0) ok = wait_at_least(ffn_cnt + nl - 1, (unsigned)s * M.n_chunks, abort_flag, R.spin_limit, &ok_lds);
+        if (!ok) return false;
+        // the step's token was written by another workgroup during this launch: an agent-scope load
+        const int tok = l ? 0 : (int)__hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        attn_block<DT, true>(M, Lw, G, l, pos, tok, w, wt, smem);
+        publish(attn_cnt + l);
+    }
+    return true;
+}
+
+template <int DT>
+__device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *layers, const l3m_run *Rp, int ci, int s) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int ok_lds;
+    ci = uniform(ci); s = uniform(s);
+    const int nl = fixed(Mp).n_layers;
+    for (int l = 0; l < nl; l++) {
+        const l3m_dmodel M = fixed(per_iteration(Mp));
+        const l3m_run R = fixed(per_iteration(Rp));
+        unsigned *attn_cnt = R.sync, *ffn_cnt = R.sync + nl, *abort_flag = R.sync + 2 * nl + 2;
+        const l3m_dlayer Lw = fixed(layers, l);
+        const l3m_dchunk C = fixed(Lw.chunks, ci);
+        FfnW<DT> wt;
+        ffn_issue<DT>(wt, C);
+        if (!wait_at_least(attn_cnt + l, (unsigned)(s + 1) * M.n_groups, abort_flag, R.spin_limit, &ok_lds)) return false;
+        ffn_block<DT, true>(M, Lw, C, ci, wt, smem);
+        publish(ffn_cnt + l);
+    }
+    return true;
+}
+
+// Every workgroup, with head tiles or not, waits for this step's last FFN before it publishes its
+// partial: that wait orders it after the previous step's reduction, so the head count of one step never
+// mixes with the next step's. The last workgroup in reduces the partials, writes tokens[pos + 1] and
+// publishes it.
+template <int DT>
+__device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, int w, int s, unsigned heads) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int ok_lds, last_lds;
+    w = uniform(w); s = uniform(s); heads = uniform(heads);
+    const l3m_dmodel M = fixed(Mp);
+    const l3m_run R = fixed(Rp);
+    const int nl = M.n_layers, grid = gridDim.x, pos = R.pos0 + s, t0 = w * R.head_tpw;
+    unsigned *ffn_cnt = R.sync + nl, *head_cnt = R.sync + 2 * nl, *tok_cnt = head_cnt + 1, *abort_flag = head_cnt + 2;
+    const bool has_tiles = t0 < M.head.tiles;
+    float v = -INFINITY;
+    int idx = 0x7FFFFFFF;
+    const l3m_dmat V = head_slice(M, has_tiles ? t0 : 0, R.head_tpw);
+    HeadW<DT> wt;
+    if (has_tiles) head_issue<DT>(wt, V);
+    if (!wait_at_least(ffn_cnt + nl - 1, (unsigned)(s + 1) * M.n_chunks, abort_flag, R.spin_limit, &ok_lds)) return false;
+    if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx);
+    if (tidx() == 0) {
+        gw(M.part_val)[w] = v;
+        gw(M.part_idx)[w] = idx;
+    }
+    const unsigned old = publish(head_cnt);
+    if (tidx() == 0) last_lds = old == (heads + 1) * (unsigned)grid - 1;
+    __syncthreads();
+    if (last_lds) {
+        float *scr = (float *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).scr);
+        reduce_partials(M.part_val, M.part_idx, grid, scr, v, idx);
+        if (tidx() == 0) gw(M.tokens)[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
+        publish(tok_cnt);
+    }
+    __syncthreads();
+    return true;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(NTE) k_decode(const l3m_dmodel *__restrict__ Mp, const l3m_dlayer *__restrict__ layers,
+                                                const l3m_run *__restrict__ Rp) {
+    const int w = blockIdx.x, n_groups = Mp->n_groups, n_chunks = Mp->n_chunks, nsteps = Rp->nsteps;
+    unsigned heads = 0;                               // steps with logits finished before step s
+    for (int s = 0; s < nsteps; s++) {
+        if (w < n_groups && !attn_role<DT>(Mp, layers, Rp, w, s, heads)) return;
+        if (w >= n_groups && w < n_groups + n_chunks && !ffn_role<DT>(Mp, layers, Rp, w - n_groups, s)) return;
+        if (Rp->pos0 + s < Rp->head_from) continue;
+        if (!head_role<DT>(Mp, Rp, w, s, heads)) return;
+        heads++;
     }
 }
 
@@ -1155,6 +1433,26 @@ template <int DT> void launch_ffn(const l3m_dmodel &M, const l3m_dlayer &L, int 
 template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t st) {
     lds_opt_in(k_head_block<DT>, M.lds_h);
     hipLaunchKernelGGL(k_head_block<DT>, dim3(M.head_grid), dim3(NTE), M.lds_h, st, M, advance);
+}
+// The persistent kernel needs every workgroup resident at once: a cooperative launch, which the runtime
+// refuses (instead of starting it) when the grid does not fit.
+template <int DT> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *layers, const l3m_run *R_dev, int grid, unsigned lds,
+                                    hipStream_t st) {
+    lds_opt_in(k_decode<DT>, lds);
+    const l3m_dmodel *m = M_dev;
+    const l3m_dlayer *ly = layers;
+    const l3m_run *r = R_dev;
+    void *args[] = {&m, &ly, &r};
+    const hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode<DT>, dim3(grid), dim3(NTE), args, lds, st);
+    return e == hipSuccess ? 0 : fail("decode launch", e);
+}
+template <int DT> int decode_fits(int grid, unsigned lds) {
+    lds_opt_in(k_decode<DT>, lds);
+    int per_cu = 0, cus = 0, coop = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode<DT>, NTE, lds) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, 0) != hipSuccess || !coop) return 0;
+    return per_cu >= 1 && grid <= per_cu * cus;
 }
 
 }  // namespace
@@ -1313,6 +1611,37 @@ int l3m_step_enqueue(const l3m_dmodel *M, const l3m_dlayer *layers, int with_hea
     if (with_head) DISPATCH(M->head.dtype, launch_head, *M, 1, st);
     CKL("decode step");
     return 0;
+}
+
+int l3m_dev_cus(void) {
+    int cus = 0;
+    if (l3m_dev_init() || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) return 0;
+    return cus;
+}
+
+int l3m_decode_fits(int dtype, int grid, unsigned lds) {
+    if (l3m_dev_init()) return 0;
+    switch (dtype) {
+    case L3M_F32: return decode_fits<L3M_F32>(grid, lds);
+    case L3M_BF16: return decode_fits<L3M_BF16>(grid, lds);
+    case L3M_Q8_0: return decode_fits<L3M_Q8_0>(grid, lds);
+    case L3M_Q4_0: return decode_fits<L3M_Q4_0>(grid, lds);
+    case L3M_MXFP4: return decode_fits<L3M_MXFP4>(grid, lds);
+    }
+    return 0;
+}
+
+int l3m_decode_launch(int dtype, const l3m_dmodel *M_dev, const l3m_dlayer *layers_dev, const l3m_run *R_dev, int grid, unsigned lds,
+                      void *stream) {
+    hipStream_t st = as_stream(stream);
+    switch (dtype) {
+    case L3M_F32: return launch_decode<L3M_F32>(M_dev, layers_dev, R_dev, grid, lds, st);
+    case L3M_BF16: return launch_decode<L3M_BF16>(M_dev, layers_dev, R_dev, grid, lds, st);
+    case L3M_Q8_0: return launch_decode<L3M_Q8_0>(M_dev, layers_dev, R_dev, grid, lds, st);
+    case L3M_Q4_0: return launch_decode<L3M_Q4_0>(M_dev, layers_dev, R_dev, grid, lds, st);
+    case L3M_MXFP4: return launch_decode<L3M_MXFP4>(M_dev, layers_dev, R_dev, grid, lds, st);
+    }
+    return fail_msg("decode: bad dtype");
 }
 
 l3m_graphs *l3m_graphs_build(const l3m_dmodel *M, const l3m_dlayer *layers) {

@@ -177,3 +177,28 @@ def test_bad_prompt_ids(models):
     with pytest.raises(ValueError):
         m.generate([SMALL.vocab], 2)
     assert m.generate([], 2) == []
+
+
+@pytest.mark.parametrize("key", [("tiny", "q4_0"), ("stories15M", "bf16"), ("stories110M", "q4_0"), ("smollm2", "mxfp4")],
+                         ids=lambda k: f"{k[0]}-{k[1]}")
+def test_persistent_kernel_equals_graph_path(models, monkeypatch, key):
+    """The persistent decode kernel runs the same blocks in the same order as the one-graph-per-step path:
+    tokens and final logits are bit-identical, over a launch boundary (more than 64 steps) and the
+    restart of a second generate."""
+    cfg = SMALL if key[0] == "tiny" else A.CONFIGS[key[0]]
+    path = models.get(cfg, key[1], seed=3)
+    ids = A.prompt(3, cfg.vocab, cfg.n_prompt)
+    n = min(cfg.ctx - len(ids) - 1, 70)
+    out = {}
+    for persist in ("1", "0"):
+        monkeypatch.setenv("L3M_PERSIST", persist)
+        with A.Model(path) as m:
+            if persist == "1":
+                assert m.persistent, "the persistent kernel should fit this model"
+            else:
+                assert not m.persistent
+            first = m.generate(ids, n)
+            second = m.generate(ids[:2], 5)
+            out[persist] = (first, second, m.logits)
+    assert out["1"][0] == out["0"][0] and out["1"][1] == out["0"][1]
+    np.testing.assert_array_equal(out["1"][2], out["0"][2])
