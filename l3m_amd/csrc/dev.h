@@ -45,6 +45,7 @@ typedef struct {
     float       *xa, *xb;        // residual stream entering the attention block / the FFN block
     float       *po;             // [n_groups][dim] attention-block partials (Wo column slices)
     float       *pd;             // [n_chunks][dim] FFN partials (Wdown column slices)
+    float       *xf;             // [dim] the final residual (persistent kernel: summed once per step for the head)
     float       *logits;         // [nslots][vocab], slot = pos % nslots
     float       *part_val;       // [head_grid] argmax partials
     int         *part_idx;
@@ -56,13 +57,17 @@ typedef struct {
 } l3m_dmodel;
 
 // One launch of the persistent decode kernel: steps at positions pos0 .. pos0 + nsteps - 1; logits (and
-// the argmax token at pos + 1) for positions >= head_from.
+// the argmax token at pos + 1) for positions >= head_from. The body runs on the workgroups of XCD
+// body_xcc (at least n_groups + n_chunks of the grid land there); n_head workgroups take head_tpw tiles each.
 typedef struct {
     int                pos0, nsteps, head_from;
-    int                head_tpw;       // head tiles per workgroup
-    unsigned          *sync;           // [2 * n_layers + 3]: attn[L], ffn[L], head, tok, abort; zero at launch
+    int                head_tpw, n_head, body_xcc;
+    unsigned          *sync;           // L3M_SYNC_WORDS: flags, tickets, argmax keys; zero at launch
     unsigned long long spin_limit;     // longest wait, in ticks of the 100 MHz clock
 } l3m_run;
+#define L3M_SYNC_WORDS(n_head) (256 + 2 * (n_head))   // flag words, then one 64-bit key per head workgroup
+#define L3M_SYNC_ABORT 192                           // the word a timed-out wait sets
+#define L3M_MAX_HEAD_WGS 1024
 
 // ------------------------------------------------------------------ runtime
 int         l3m_dev_init(void);                 // 0 when a gfx9 HIP device is usable
@@ -99,6 +104,9 @@ int l3m_step_enqueue(const l3m_dmodel *m, const l3m_dlayer *layers, int with_hea
 
 // The persistent decode kernel (one cooperative launch for R->nsteps steps; layers_dev in device memory).
 int l3m_dev_cus(void);
+// The XCD each block of a cooperative grid of `grid` 1024-thread workgroups with lds bytes lands on
+// (xcc[grid]); 0, or -1 on a device error.
+int l3m_decode_placement(int grid, unsigned lds, int *xcc);
 int l3m_decode_fits(int dtype, int grid, unsigned lds);     // 1 if grid workgroups with lds bytes can all be resident
 // m_dev, layers_dev, r_dev: device-memory copies (the kernel reads its parameters from there)
 int l3m_decode_launch(int dtype, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev, int grid, unsigned lds,

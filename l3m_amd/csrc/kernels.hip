@@ -49,13 +49,25 @@ __device__ __forceinline__ float4 ldg16f(const void *p, size_t i) {
     const f32x4 v = gp<f32x4>(p)[i];
     return make_float4(v.x, v.y, v.z, v.w);
 }
-// 16 bytes that another workgroup wrote during this kernel: two device-coherent 8-byte loads (they read
-// past any stale copy in this XCD's L2, so no cache-wide invalidation is needed to see the data).
+// Device-scope cache policy (sc1) of a buffer access: a load sees the newest data in this XCD's L2 or
+// in memory, never a stale clean copy; a store writes through to memory.
+constexpr int SC1 = 16;
+// A raw buffer over p (a workgroup-uniform base): 16-byte accesses at a per-lane byte offset, with the
+// cache policy the global instructions cannot take from C++.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, 0, 0x7FFFFFFF, 0x00020000);
+}
+// 16 bytes that another workgroup wrote during this kernel, element i of a uniform base p: one
+// device-coherent load (it reads past any stale copy in this XCD's L2, so no cache-wide invalidation is
+// needed to see the data).
 __device__ __forceinline__ uint4 ldcoh16(const void *p, size_t i) {
-    const GLOBAL uint64_t *q = gp<uint64_t>(p) + 2 * i;
-    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(buf(p), (uint32_t)(16 * i), 0, SC1));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+// 16 bytes stored through to memory (for readers on another XCD), element i of a uniform base p.
+__device__ __forceinline__ void stcoh16(void *p, size_t i, float4 x) {
+    const u32x4 v = {__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), buf(p), (uint32_t)(16 * i), 0, SC1);
 }
 template <bool COH> __device__ __forceinline__ uint4 ld16(const void *p, size_t i) { return COH ? ldcoh16(p, i) : ldg16(p, i); }
 template <bool COH> __device__ __forceinline__ float4 ld16f(const void *p, size_t i) {
@@ -711,7 +723,7 @@ __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float 
 #pragma unroll
     for (int j = 0; j < FILL_PER; j++) {
         const int pj = j0 + j < nparts ? j0 + j : nparts - 1;
-        P.p[j] = ld16f<COH>(parts + (size_t)pj * dim, f);
+        P.p[j] = ld16f<COH>(parts, (size_t)pj * (dim >> 2) + f);
     }
     if (rope_row) {
         const int i = tid < (hd >> 1) ? tid : (hd >> 1) - 1;
@@ -741,7 +753,7 @@ __device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, int npa
                 v.x += use ? P.p[j].x : 0.f; v.y += use ? P.p[j].y : 0.f; v.z += use ? P.p[j].z : 0.f; v.w += use ? P.p[j].w : 0.f;
             }
             for (int j = FILL_PER; j < G.per && j0 + j < nparts; j++) {   // beyond one batch: in order
-                const float4 p = ld16f<COH>(parts + (size_t)(j0 + j) * dim, f);
+                const float4 p = ld16f<COH>(parts, (size_t)(j0 + j) * (dim >> 2) + f);
                 v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
             }
             if (G.groups > 1) pbuf[grp * G.n4 + f] = v;
@@ -762,6 +774,39 @@ __device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, int npa
         const f32x4 v = {x.x, x.y, x.z, x.w};
         gw((f32x4 *)keep)[tid] = v;
     }
+    return x;
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
+// x[4f, 4f+4) as pro_finish forms it from the same inputs, for one thread: base and the parts grouped
+// and added in the same order (a group that leaves some of its FILL_PER slots unused adds +0.0 for
+// them, which turns a -0.0 sum into +0.0), read with device-coherent loads.
+__device__ __forceinline__ float4 parts_sum_at(const float *base, const float *parts, int nparts, int dim, int f) {
+    constexpr int B = 16;                             // parts loaded at once; the rest one at a time
+    const ProGeom G = pro_geom(dim, nparts);
+    const size_t stride = (size_t)(dim >> 2);
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 p[B];
+#pragma unroll
+    for (int k = 0; k < B; k++) p[k] = k < nparts ? ld16f<true>(parts, (size_t)k * stride + f) : zero;
+    float4 x = zero, v = ld16f<true>(base, f);
+    int g = 0;
+    auto close = [&]() {
+        const int c = nparts - g * G.per < G.per ? nparts - g * G.per : G.per;
+        if (c < FILL_PER) v = add4(v, zero);
+        x = g == 0 ? v : add4(x, v);
+    };
+    auto take = [&](int k, float4 pk) {
+        if (k == (g + 1) * G.per) { close(); v = zero; g++; }
+        v = add4(v, pk);
+    };
+#pragma unroll
+    for (int k = 0; k < B; k++)
+        if (k < nparts) take(k, p[k]);
+    for (int k = B; k < nparts; k++) take(k, ld16f<true>(parts, (size_t)k * stride + f));
+    close();
+    for (int e = g + 1; e < G.groups; e++) x = add4(x, zero);
     return x;
 }
 
@@ -914,7 +959,7 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
                 uint4 kk;
                 if (t == pos) kk = kcur[j];
                 else if (WIN) kk = ((const uint4 *)(kw + (size_t)t * hd))[j];
-                else kk = ld16<COH>(kw + (size_t)t * hd, j);
+                else kk = ld16<COH>(kw, (size_t)t * (hd >> 3) + j);
                 part = dot8_bf16(q, kk, 0.f);
             }
             const float s = lanes_sum_n(part, LP) * scale;
@@ -938,7 +983,7 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
                 uint4 vv;
                 if (t == pos) vv = vcur[j];
                 else if (WIN) vv = ((const uint4 *)(vw + (size_t)t * hd))[j];
-                else vv = ld16<COH>(vw + (size_t)t * hd, j);
+                else vv = ld16<COH>(vw, (size_t)t * (hd >> 3) + j);
                 o[0] = fmaf(p, bf16_f32(vv.x & 0xFFFF), o[0]); o[1] = fmaf(p, bf16_f32(vv.x >> 16), o[1]);
                 o[2] = fmaf(p, bf16_f32(vv.y & 0xFFFF), o[2]); o[3] = fmaf(p, bf16_f32(vv.y >> 16), o[3]);
                 o[4] = fmaf(p, bf16_f32(vv.z & 0xFFFF), o[4]); o[5] = fmaf(p, bf16_f32(vv.z >> 16), o[5]);
@@ -1105,11 +1150,21 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
     uint8_t *act = smem + L.act;
     Red red{scr, 0};
 
-    Pro P;
-    pro_load<PRE>(P, M.xb, M.pd, M.n_chunks, dim, M.norm, M.embed, false, 0, nullptr, 0);     // x += down (engine.c:275), last layer
-    if constexpr (!PRE) head_issue<DT>(w, V);
-    const float4 x = pro_finish<PRE>(P, M.pd, M.n_chunks, dim, false, (float4 *)work, nullptr, nullptr, 0);
-    norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
+    float4 x, nw;
+    if constexpr (PRE) {
+        // the persistent path sums the final residual once per step (reduce_final) into xf
+        const int n4 = dim >> 2, own = tid < n4 ? tid : n4 - 1;
+        nw = ldg16f(M.norm, own);
+        const float4 xv = ld16f<true>(M.xf, own);
+        x = tid < n4 ? xv : make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+        Pro P;
+        pro_load<false>(P, M.xb, M.pd, M.n_chunks, dim, M.norm, M.embed, false, 0, nullptr, 0);   // x += down (engine.c:275), last layer
+        head_issue<DT>(w, V);
+        x = pro_finish<false>(P, M.pd, M.n_chunks, dim, false, (float4 *)work, nullptr, nullptr, 0);
+        nw = P.nw;
+    }
+    norm_prep<DT>(x, nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work);
     __syncthreads();
     rows_sum4(V, work, V.rows, [&](int i, float yy, float) { if ((tidx() & 3) == 0) y[i] = yy; });
@@ -1187,36 +1242,64 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
 }
 
 // ------------------------------------------------------------------ the persistent path
-// k_decode runs R.nsteps decode steps in one cooperative launch. Workgroup w keeps its roles for every
-// layer and step: the attention block of head group w (w < n_groups), the FFN block of chunk
-// w - n_groups (next n_chunks workgroups), and, in steps that need logits, head tiles
-// [w * head_tpw, (w + 1) * head_tpw). Phases hand over through counters in R.sync that only grow during
-// the launch (the host zeroes them before it):
-//   attn[l] += 1 per group after layer l's partial is written; ffn[l] likewise per chunk;
-//   head   += 1 per workgroup after its argmax partial; the last one reduces them and bumps tok.
-// A producer makes its stores visible with an agent-scope release (the L2 of its XCD written back)
-// before its increment; a consumer polls with agent-scope loads and acquires (its L2 invalidated)
-// before reading. Every wait is bounded: past R.spin_limit ticks of the 100 MHz clock the waiter raises
-// R.sync[abort] and every workgroup leaves at its next wait, so the grid always drains.
+// k_decode runs R.nsteps decode steps in one cooperative launch, one workgroup per CU. The body (the
+// attention blocks of the n_groups head groups and the FFN blocks of the n_chunks chunks) runs on the
+// workgroups of one XCD (R.body_xcc): their hand-overs then meet in that XCD's L2. Every other workgroup
+// takes head tiles. Roles are dealt at launch from per-XCD tickets, so they follow where the hardware
+// placed each workgroup.
+//
+// Hand-over, inside the body: each producer owns a flag word that it sets to its epoch once its stores
+// have reached L2 (s_waitcnt, barrier, then the flag); consumers poll the producers' flags with
+// device-scope loads (one lane per producer) and read the data the same way. Epochs only grow during a
+// launch (the host zeroes R.sync first): attention group g sets attn[g] = s*L + l + 1 after layer l of
+// step s, FFN chunk c sets ffn[c] likewise. A layer's blocks wait for all flags of the block before them.
+//
+// Hand-over to and from the head (other XCDs, so through memory): after the last layer of a step with
+// logits, attention group g sums its slice of the final residual into xf with write-through stores and
+// sets xf_flag[g] = s + 1; head workgroups wait for all of them, compute their tiles' logits and argmax,
+// and store one 64-bit key per workgroup (the step's tag, the value in an order-preserving code, the
+// index); the attention groups of the next step wait for every key with that tag and take the maximum.
+//
+// Every wait is bounded: past R.spin_limit ticks of the 100 MHz clock the waiter raises the abort flag
+// and every workgroup leaves at its next wait, so the grid always drains.
+enum { SY_ATTN = 0, SY_FFN = 64, SY_XF = 128, SY_ABORT = L3M_SYNC_ABORT, SY_TICKET = 224, SY_HEAD_TICKET = 240, SY_SLOTS = 256 };
+static_assert(L3M_SYNC_WORDS(0) == SY_SLOTS, "keys follow the flag words");
 
-__device__ bool wait_at_least(const unsigned *ctr, unsigned target, unsigned *abort_flag, unsigned long long limit, int *ok_lds) {
-    if (tidx() == 0) {
+__device__ __forceinline__ unsigned xcc_id() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 15;
+}
+__device__ __forceinline__ unsigned ld_flag(const unsigned *p) {
+    return __hip_atomic_load(gp<unsigned>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits, bounded: the shared tail of every poll loop. Returns 0 to stop waiting (abort seen or raised).
+__device__ __forceinline__ int keep_waiting(unsigned spin, unsigned long long t0, unsigned *abort_flag, unsigned long long limit) {
+    if ((spin & 31) != 31) return 1;
+    if (ld_flag(abort_flag)) return 0;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
+        __hip_atomic_store(gw(abort_flag), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return 0;
+    }
+    return 1;
+}
+
+// Wavefront 0 polls flags[0..n) (n <= 64, one lane each) until every one is >= target; the result
+// reaches every thread through ok_lds. SLEEP: s_sleep between polls (64 clocks each).
+template <int SLEEP>
+__device__ bool wait_flags(const unsigned *flags, int n, unsigned target, unsigned *abort_flag, unsigned long long limit, int *ok_lds) {
+    const int tid = tidx();
+    if (tid < 64) {
         int ok = 1;
         const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-        for (unsigned spin = 0; __hip_atomic_load(gp<unsigned>(ctr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; spin++) {
-            if ((spin & 31) == 31) {
-                if (__hip_atomic_load(gp<unsigned>(abort_flag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) { ok = 0; break; }
-                if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
-                    __hip_atomic_store(gw(abort_flag), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    ok = 0;
-                    break;
-                }
-            }
-            __builtin_amdgcn_s_sleep(1);
+        for (unsigned spin = 0;; spin++) {
+            const unsigned v = tid < n ? ld_flag(flags + tid) : target;
+            if (__all(v >= target)) break;
+            if (!keep_waiting(spin, t0, abort_flag, limit)) { ok = 0; break; }
+            __builtin_amdgcn_s_sleep(SLEEP);
         }
-        // No acquire fence (it would invalidate this XCD's whole L2): what the producers wrote is read
-        // with device-coherent loads (ldcoh16, the K/V copy with sc1, atomic loads of tokens and partials).
-        *ok_lds = ok;
+        if (tid == 0) *ok_lds = ok;
     }
     __syncthreads();
     const int ok = *ok_lds;
@@ -1224,15 +1307,74 @@ __device__ bool wait_at_least(const unsigned *ctr, unsigned target, unsigned *ab
     return ok != 0;
 }
 
-// Every thread's stores, then one increment that publishes them (returns the old count to thread 0).
-__device__ unsigned publish(unsigned *ctr) {
+// Every thread's stores have reached L2 (vmcnt), then thread 0 sets the flag: a plain store for readers
+// on this XCD, a write-through one (device) for readers on others.
+template <bool DEVICE>
+__device__ __forceinline__ void set_flag(unsigned *flag, unsigned value) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    unsigned old = 0;
     if (tidx() == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        old = __hip_atomic_fetch_add(gw(ctr), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (DEVICE) __hip_atomic_store(gw(flag), value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else *gw(flag) = value;                       // write-through from L1, so it is in this XCD's L2
     }
-    return old;
+}
+
+// A head workgroup's argmax as a 64-bit key whose unsigned order is the reference's (larger value, then
+// lower index): bits 17..48 the value in an order-preserving code, bits 0..16 0x1FFFF - index, bits 49..63
+// the step's tag. No row (idx past 0x1FFFF) or NaN gives key 0, which never wins.
+constexpr uint64_t KEY_BITS = (1ull << 49) - 1;
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx, unsigned tag) {
+    uint64_t key = 0;
+    if (v == v && idx >= 0 && idx <= 0x1FFFF) {
+        uint32_t u = __float_as_uint(v + 0.0f);       // -0 as +0: they compare equal
+        u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        key = (uint64_t)u << 17 | (uint64_t)(0x1FFFF - idx);
+    }
+    return (uint64_t)tag << 49 | key;
+}
+__device__ __forceinline__ unsigned step_tag(int s) { return (unsigned)(s % 32767) + 1; }
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// The token chosen by step s's head: wavefront 0 polls the n_head keys until all carry the step's tag and
+// reduces them. Returns the token, or -1 when the run is being abandoned.
+__device__ int wait_token(const uint64_t *slots, int n_head, int s, unsigned *abort_flag, unsigned long long limit, int *lds) {
+    const int tid = tidx();
+    if (tid < 64) {
+        const unsigned tag = step_tag(s);
+        int tok = -1;
+        uint64_t best = 0;
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        for (unsigned spin = 0;; spin++) {
+            bool all = true;
+            best = 0;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {             // n_head <= 1024
+                const int i = tid + 64 * r;
+                if (i < n_head) {
+                    const uint64_t v = __hip_atomic_load(gp<uint64_t>(slots + i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    all = all && (unsigned)(v >> 49) == tag;
+                    best = max_u64(best, v & KEY_BITS);
+                }
+            }
+            if (__all(all)) break;
+            if (!keep_waiting(spin, t0, abort_flag, limit)) { best = ~0ull; break; }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (best != ~0ull) {
+#pragma unroll
+            for (int m = 1; m < 64; m <<= 1) {
+                const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(best >> 32), m);
+                const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, m);
+                best = max_u64(best, (uint64_t)hi << 32 | lo);
+            }
+            tok = (best >> 17) == 0 ? 0 : 0x1FFFF - (int)(best & 0x1FFFF);
+        }
+        if (tid == 0) *lds = tok;
+    }
+    __syncthreads();
+    const int tok = *lds;
+    __syncthreads();
+    return tok;
 }
 
 // A 64-bit value through readfirstlane, one 32-bit half at a time. The builtin returns a signed int, so
@@ -1266,35 +1408,57 @@ template <class T> __device__ __forceinline__ const T *per_iteration(const T *p)
     return (const T *)u;
 }
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ unsigned uniform(unsigned v) { return (unsigned)__builtin_amdgcn_readfirstlane((int)v); }
 
-// The roles of one step, each in a function of its own (so each gets its own register allocation and
-// nothing of one role stays live in the other). They return false when the run is being abandoned.
+// Attention group g's share of the final residual (the head's input): x = xb + the last layer's FFN
+// partials, in pro_finish's order of additions, for float4 elements [g * per, (g + 1) * per), stored
+// through to memory for the head workgroups.
+__device__ __noinline__ void reduce_final(const l3m_dmodel *Mp, int g) {
+    g = uniform(g);
+    const l3m_dmodel M = fixed(Mp);
+    const int n4 = M.dim >> 2, per = (n4 + M.n_groups - 1) / M.n_groups;
+    const int f = g * per + tidx();
+    if (tidx() < per && f < n4) stcoh16(M.xf, f, parts_sum_at(M.xb, M.pd, M.n_chunks, M.dim, f));
+}
+
+// The roles, each in a function of its own (so each gets its own register allocation and nothing of one
+// role stays live in another). They return false when the run is being abandoned.
 template <int DT>
-__device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *layers, const l3m_run *Rp, int w, int s, unsigned heads) {
+__device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *layers, const l3m_run *Rp, int g, int s) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int ok_lds;
-    w = uniform(w); s = uniform(s); heads = uniform(heads);
+    g = uniform(g); s = uniform(s);
     const int nl = fixed(Mp).n_layers;
     for (int l = 0; l < nl; l++) {
         const l3m_dmodel M = fixed(per_iteration(Mp));
         const l3m_run R = fixed(per_iteration(Rp));
         const int pos = R.pos0 + s;
-        unsigned *attn_cnt = R.sync, *ffn_cnt = R.sync + nl, *tok_cnt = R.sync + 2 * nl + 1, *abort_flag = R.sync + 2 * nl + 2;
-        const bool prev_head = s > 0 && pos - 1 >= R.head_from;
+        unsigned *sync = R.sync, *abort_flag = sync + SY_ABORT;
         const l3m_dlayer Lw = fixed(layers, l);
-        const l3m_dgroup G = fixed(Lw.groups, w);
+        const l3m_dgroup G = fixed(Lw.groups, g);
         AttnW<DT> wt;
         attn_issue<DT>(wt, G);
-        bool ok = true;
-        if (l > 0) ok = wait_at_least(ffn_cnt + l - 1, (unsigned)(s + 1) * M.n_chunks, abort_flag, R.spin_limit, &ok_lds);
-        else if (prev_head) ok = wait_at_least(tok_cnt, heads, abort_flag, R.spin_limit, &ok_lds);
-        else if (s > 0) ok = wait_at_least(ffn_cnt + nl - 1, (unsigned)s * M.n_chunks, abort_flag, R.spin_limit, &ok_lds);
-        if (!ok) return false;
-        // the step's token was written by another workgroup during this launch: an agent-scope load
-        const int tok = l ? 0 : (int)__hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        attn_block<DT, true>(M, Lw, G, l, pos, tok, w, wt, smem);
-        publish(attn_cnt + l);
+        const unsigned epoch = (unsigned)(s * nl + l);
+        int tok = 0;
+        if (l == 0 && s > 0 && pos - 1 >= R.head_from) {
+            // this step's token is the previous step's argmax (which also orders this step after every
+            // read of the previous step's FFN partials)
+            tok = wait_token((const uint64_t *)(sync + SY_SLOTS), R.n_head, s - 1, abort_flag, R.spin_limit, &ok_lds);
+            if (tok < 0) return false;
+            if (g == 0 && tidx() == 0) gw(M.tokens)[pos] = tok;
+        } else {
+            if (epoch > 0 && !wait_flags<1>(sync + SY_FFN, M.n_chunks, epoch, abort_flag, R.spin_limit, &ok_lds)) return false;
+            if (l == 0) tok = __hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        attn_block<DT, true>(M, Lw, G, l, pos, tok, g, wt, smem);
+        set_flag<false>(sync + SY_ATTN + g, epoch + 1);
+    }
+    const l3m_run R = fixed(per_iteration(Rp));
+    if (R.pos0 + s >= R.head_from) {
+        unsigned *sync = R.sync;
+        if (!wait_flags<1>(sync + SY_FFN, fixed(Mp).n_chunks, (unsigned)((s + 1) * nl), sync + SY_ABORT, R.spin_limit, &ok_lds))
+            return false;
+        reduce_final(Mp, g);
+        set_flag<true>(sync + SY_XF + g, (unsigned)s + 1);
     }
     return true;
 }
@@ -1308,68 +1472,89 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
     for (int l = 0; l < nl; l++) {
         const l3m_dmodel M = fixed(per_iteration(Mp));
         const l3m_run R = fixed(per_iteration(Rp));
-        unsigned *attn_cnt = R.sync, *ffn_cnt = R.sync + nl, *abort_flag = R.sync + 2 * nl + 2;
+        unsigned *sync = R.sync;
         const l3m_dlayer Lw = fixed(layers, l);
         const l3m_dchunk C = fixed(Lw.chunks, ci);
         FfnW<DT> wt;
         ffn_issue<DT>(wt, C);
-        if (!wait_at_least(attn_cnt + l, (unsigned)(s + 1) * M.n_groups, abort_flag, R.spin_limit, &ok_lds)) return false;
+        const unsigned epoch = (unsigned)(s * nl + l);
+        if (!wait_flags<1>(sync + SY_ATTN, M.n_groups, epoch + 1, sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
         ffn_block<DT, true>(M, Lw, C, ci, wt, smem);
-        publish(ffn_cnt + l);
+        set_flag<false>(sync + SY_FFN + ci, epoch + 1);
     }
     return true;
 }
 
-// Every workgroup, with head tiles or not, waits for this step's last FFN before it publishes its
-// partial: that wait orders it after the previous step's reduction, so the head count of one step never
-// mixes with the next step's. The last workgroup in reduces the partials, writes tokens[pos + 1] and
-// publishes it.
+// Head workgroup h: tiles [h * head_tpw, (h + 1) * head_tpw) of step s, once the final residual is out.
 template <int DT>
-__device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, int w, int s, unsigned heads) {
+__device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, int h, int s) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int ok_lds, last_lds;
-    w = uniform(w); s = uniform(s); heads = uniform(heads);
+    __shared__ int ok_lds;
+    h = uniform(h); s = uniform(s);
     const l3m_dmodel M = fixed(Mp);
     const l3m_run R = fixed(Rp);
-    const int nl = M.n_layers, grid = gridDim.x, pos = R.pos0 + s, t0 = w * R.head_tpw;
-    unsigned *ffn_cnt = R.sync + nl, *head_cnt = R.sync + 2 * nl, *tok_cnt = head_cnt + 1, *abort_flag = head_cnt + 2;
+    const int pos = R.pos0 + s, t0 = h * R.head_tpw;
     const bool has_tiles = t0 < M.head.tiles;
     float v = -INFINITY;
     int idx = 0x7FFFFFFF;
     const l3m_dmat V = head_slice(M, has_tiles ? t0 : 0, R.head_tpw);
     HeadW<DT> wt;
     if (has_tiles) head_issue<DT>(wt, V);
-    if (!wait_at_least(ffn_cnt + nl - 1, (unsigned)(s + 1) * M.n_chunks, abort_flag, R.spin_limit, &ok_lds)) return false;
+    if (!wait_flags<4>(R.sync + SY_XF, M.n_groups, (unsigned)s + 1, R.sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
     if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx);
-    if (tidx() == 0) {
-        gw(M.part_val)[w] = v;
-        gw(M.part_idx)[w] = idx;
-    }
-    const unsigned old = publish(head_cnt);
-    if (tidx() == 0) last_lds = old == (heads + 1) * (unsigned)grid - 1;
-    __syncthreads();
-    if (last_lds) {
-        float *scr = (float *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).scr);
-        reduce_partials(M.part_val, M.part_idx, grid, scr, v, idx);
-        if (tidx() == 0) gw(M.tokens)[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
-        publish(tok_cnt);
-    }
-    __syncthreads();
+    if (tidx() == 0)
+        __hip_atomic_store(gw((uint64_t *)(R.sync + SY_SLOTS) + h), argmax_key(v, idx, step_tag(s)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     return true;
+}
+
+// Roles from where the workgroup runs: the first n_body workgroups to arrive on the body XCD take the
+// attention groups then the FFN chunks; every other workgroup takes the next head index.
+__device__ int deal_role(const l3m_run &R, int n_body, int *lds) {
+    if (tidx() == 0) {
+        const unsigned x = xcc_id();
+        int role = -1;
+        if ((int)x == R.body_xcc) {
+            const unsigned t = __hip_atomic_fetch_add(gw(R.sync + SY_TICKET + x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((int)t < n_body) role = (int)t;
+        }
+        if (role < 0)
+            role = n_body + (int)__hip_atomic_fetch_add(gw(R.sync + SY_HEAD_TICKET), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *lds = role;
+    }
+    __syncthreads();
+    const int role = *lds;
+    __syncthreads();
+    return role;
 }
 
 template <int DT>
 __global__ void __launch_bounds__(NTE) k_decode(const l3m_dmodel *__restrict__ Mp, const l3m_dlayer *__restrict__ layers,
                                                 const l3m_run *__restrict__ Rp) {
-    const int w = blockIdx.x, n_groups = Mp->n_groups, n_chunks = Mp->n_chunks, nsteps = Rp->nsteps;
-    unsigned heads = 0;                               // steps with logits finished before step s
-    for (int s = 0; s < nsteps; s++) {
-        if (w < n_groups && !attn_role<DT>(Mp, layers, Rp, w, s, heads)) return;
-        if (w >= n_groups && w < n_groups + n_chunks && !ffn_role<DT>(Mp, layers, Rp, w - n_groups, s)) return;
-        if (Rp->pos0 + s < Rp->head_from) continue;
-        if (!head_role<DT>(Mp, Rp, w, s, heads)) return;
-        heads++;
+    __shared__ int role_lds;
+    const l3m_run R = fixed(Rp);
+    const int n_groups = Mp->n_groups, n_chunks = Mp->n_chunks, n_body = n_groups + n_chunks;
+    const int role = deal_role(R, n_body, &role_lds);
+    for (int s = 0; s < R.nsteps; s++) {
+        if (role < n_groups) {
+            if (!attn_role<DT>(Mp, layers, Rp, role, s)) return;
+        } else if (role < n_body) {
+            if (!ffn_role<DT>(Mp, layers, Rp, role - n_groups, s)) return;
+        } else if (R.pos0 + s >= R.head_from && role - n_body < R.n_head) {
+            if (!head_role<DT>(Mp, Rp, role - n_body, s)) return;
+        }
     }
+    // the last step's token has no next step in this launch to take it: group 0 writes it
+    const int last = R.pos0 + R.nsteps - 1;
+    if (role == 0 && R.nsteps > 0 && last >= R.head_from) {
+        const int tok = wait_token((const uint64_t *)(R.sync + SY_SLOTS), R.n_head, R.nsteps - 1, R.sync + SY_ABORT, R.spin_limit, &role_lds);
+        if (tok >= 0 && tidx() == 0) gw(Mp->tokens)[last + 1] = tok;
+    }
+}
+
+// Where the workgroups of a grid land: out[b] = the XCD of block b (the decode kernel's launch shape).
+__global__ void __launch_bounds__(NTE) k_where(int *out) {
+    if (tidx() == 0) out[blockIdx.x] = (int)xcc_id();
 }
 
 // ----------------------------------------------------------------------------------------- runtime
@@ -1629,6 +1814,20 @@ int l3m_decode_fits(int dtype, int grid, unsigned lds) {
     case L3M_MXFP4: return decode_fits<L3M_MXFP4>(grid, lds);
     }
     return 0;
+}
+
+int l3m_decode_placement(int grid, unsigned lds, int *xcc) {
+    if (l3m_dev_init()) return -1;
+    if (grid <= 0) return fail_msg("placement: empty grid");
+    int *d = nullptr;
+    CK(hipMalloc(&d, (size_t)grid * 4));
+    lds_opt_in(k_where, lds);
+    void *args[] = {&d};
+    hipError_t e = hipLaunchCooperativeKernel((const void *)k_where, dim3(grid), dim3(NTE), args, lds, g_stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(xcc, d, (size_t)grid * 4, hipMemcpyDeviceToHost, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    (void)hipFree(d);
+    return e == hipSuccess ? 0 : fail("placement probe", e);
 }
 
 int l3m_decode_launch(int dtype, const l3m_dmodel *M_dev, const l3m_dlayer *layers_dev, const l3m_run *R_dev, int grid, unsigned lds,
