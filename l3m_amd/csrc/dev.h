@@ -18,7 +18,9 @@ typedef struct {
     l3m_dmat wo;                 // dim rows x the group's nq * hd Wo columns
     int      q0, nq, kv0, nkv;   // first query head, count; first kv head, count
     unsigned write_kv;           // bit i: this group writes kv head kv0 + i into the cache
-    int      pad_;
+    int      att_wl;             // log2 of the most wavefronts one query head takes in the attention
+    unsigned lds[10];            // LDS byte offsets of the attention block's regions (l3m_group_layout)
+    int      pad_[2];
 } l3m_dgroup;
 
 // One chunk of a layer's FFN block: ffn rows [f0, f0 + nf), nf a multiple of 32.
@@ -26,6 +28,8 @@ typedef struct {
     l3m_dmat gate_up;            // 2 * ceil16(nf) rows: gate tile t, up tile t, ... x dim
     l3m_dmat down;               // dim rows x the chunk's nf Wdown columns
     int      f0, nf;
+    unsigned lds[5];             // LDS byte offsets of the FFN block's regions (l3m_chunk_layout)
+    int      pad_;
 } l3m_dchunk;
 
 typedef struct {
@@ -39,6 +43,10 @@ typedef struct {
     int          n_groups, n_chunks, head_grid, head_tiles_per_wg, body_dtype;
     int          kv_lds;         // attention copies the K, V rows of its kv heads into LDS (they fit)
     float        eps;
+    float        att_scale;      // 1 / sqrt(hd)
+    int          hpk;            // query heads per kv head
+    int          pro_groups[2], pro_per[2];   // prologue thread groups and parts per group: [0] over the
+                                              // n_chunks FFN partials, [1] over the n_groups attention ones
     unsigned     lds_a, lds_b, lds_h;   // dynamic LDS bytes of the three step kernels
     int         *pos;            // [1] position of the step being run
     int32_t     *tokens;         // [ctx + 1]: prompt ids, then each step's argmax at pos + 1
@@ -96,6 +104,11 @@ int    l3m_k_argmax(const float *x, int n, int32_t *out, void *stream);
 // group) and the FFN block (one per chunk); with_head adds the final norm, the head and the argmax written
 // to tokens[pos + 1]. Always advances pos. LDS sizes in m must come from l3m_step_lds.
 unsigned l3m_lds_attn(int dtype, int dim, int ctx, int hd, const l3m_dgroup *g, int kv_lds);
+// Fill g->lds (region offsets, the same with or without the K/V window, which comes last) and g->att_wl;
+// fill c->lds; fill m->pro_groups / pro_per / att_scale / hpk from the model's shape.
+void     l3m_group_layout(int dtype, int dim, int ctx, int hd, l3m_dgroup *g);
+void     l3m_chunk_layout(int dtype, int dim, l3m_dchunk *c);
+void     l3m_model_layout(l3m_dmodel *m);
 unsigned l3m_dev_lds_max(void);       // dynamic LDS one workgroup may use on this device
 unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c);
 unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg);

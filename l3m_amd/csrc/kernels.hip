@@ -522,10 +522,13 @@ struct Pref {
 // 64 * QBYTES run per wavefront. Loads are unconditional (past the end they repeat the last pair) so that
 // no branch ties a load to its use (a branch around them would make the compiler copy the loaded
 // registers at the join, which waits for the loads). m has at least one pair.
+// The wavefront index as a scalar (uniform) value, so index arithmetic on it runs on the scalar unit.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tidx() >> 6); }
+
 template <int DT, int NS>
 __device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, int s0) {
     constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
-    const int wave = tidx() >> 6, sub = (tidx() >> 4) & 3, row = tidx() & 15, n = m.tiles * m.nb;
+    const int wave = wave_id(), sub = (tidx() >> 4) & 3, row = tidx() & 15, n = m.tiles * m.nb;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         int p = (wave + (s0 + s) * NWE) * 4 + sub;
@@ -539,10 +542,16 @@ __device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, i
     }
 }
 
-// res[pair * 16 + row] for this lane's slots.
+// res[pair * 16 + row] for this lane's slots. The lane's pair advances by 4 * NWE from slot to slot, so
+// its block (pair % nb) advances by (4 * NWE) % nb, with one wrap.
 template <int DT, int NS>
 __device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m, int s0, const uint8_t *act, int kp, float *res) {
-    const int wave = tidx() >> 6, sub = (tidx() >> 4) & 3, row = tidx() & 15, n = m.tiles * m.nb;
+    const int wave = wave_id(), lane = tidx() & 63, nb = m.nb, n = m.tiles * nb;
+    // x % nb = x - nb * floor((x + 0.5) / nb) with a reciprocal good to 1 ulp: exact for x < 2^20
+    const float inb = __builtin_amdgcn_rcpf((float)nb);
+    const int x0 = (tidx() >> 4) + 4 * NWE * s0;      // the lane's pair in slot 0
+    int b = x0 - (int)(((float)x0 + 0.5f) * inb) * nb;
+    const int step = 4 * NWE - (int)(((float)(4 * NWE) + 0.5f) * inb) * nb;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         // Pin the loaded registers here: otherwise the compiler hoists their first use (the f16 scale
@@ -550,8 +559,10 @@ __device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m
         asm volatile("" : "+v"(pf.sc[s]));
 #pragma unroll
         for (int v = 0; v < qbytes(DT) / 16; v++) asm volatile("" : "+v"(pf.w[s][v].x), "+v"(pf.w[s][v].y), "+v"(pf.w[s][v].z), "+v"(pf.w[s][v].w));
-        const int p = (wave + (s0 + s) * NWE) * 4 + sub;
-        if (p < n) res[p * 16 + row] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, p % m.nb);
+        const int p0 = (wave + (s0 + s) * NWE) * 4;
+        if (p0 + (lane >> 4) < n) res[p0 * 16 + lane] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b);
+        b += step;                                    // step < nb
+        b -= b >= nb ? nb : 0;
     }
 }
 
@@ -627,30 +638,13 @@ __device__ __forceinline__ float strided_sum(float v, int n) {
     return lo + hi;
 }
 
-// Workgroup (16 wavefronts) reductions, one barrier each: the wavefront results go to one of two
-// 16-float slots of scr, used alternately, so a slot is only rewritten after every thread has passed
-// the barrier of the reduction in between. All threads call them, in the same order.
+// Scratch for workgroup reductions (norm_prep): the wavefront results go to one of two 16-float slots of
+// scr, used alternately, so a slot is only rewritten after every thread has passed the barrier of the
+// reduction in between. All threads take part, in the same order.
 struct Red {
     float *scr;    // 32 floats of LDS
     int k;
 };
-__device__ __forceinline__ const float *red_publish(Red &r, float v) {
-    float *s = r.scr + 16 * (r.k++ & 1);
-    if ((tidx() & 63) == 0) s[tidx() >> 6] = v;
-    __syncthreads();
-    return s;
-}
-__device__ __forceinline__ float red_sum(Red &r, float v) {
-    const float4 *s = (const float4 *)red_publish(r, lanes_sum<64>(v));
-    const float4 a = s[0], b = s[1], c = s[2], d = s[3];
-    return (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) + (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
-}
-__device__ __forceinline__ float red_max(Red &r, float v) {
-    const float4 *s = (const float4 *)red_publish(r, lanes_max<64>(v));
-    const float4 a = s[0], b = s[1], c = s[2], d = s[3];
-    return fmaxf(fmaxf(fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)), fmaxf(fmaxf(b.x, b.y), fmaxf(b.z, b.w))),
-                 fmaxf(fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w)), fmaxf(fmaxf(d.x, d.y), fmaxf(d.z, d.w))));
-}
 // (value, index) maximum with the reference's tie rule (better()); sv, si: 16 words each.
 __device__ void wge_argmax(float &v, int &i, float *sv, int *si) {
     for (int o = 32; o; o >>= 1) {
@@ -699,25 +693,42 @@ struct Pro {
     float2 cs;        // RoPE (cos, sin) of angle index tid (tid < hd / 2)
 };
 struct ProGeom {
-    int n4, groups, per;
+    int n4, groups, per, nparts;
 };
-__device__ __forceinline__ ProGeom pro_geom(int dim, int nparts) {
+// groups = NTE / n4 (at least 1), per = ceil(nparts / groups) (at least 1): computed on the host
+// (l3m_model_layout) so that no workgroup divides by them at run time.
+__host__ __device__ inline void pro_shape(int dim, int nparts, int &groups, int &per) {
+    groups = NTE / (dim >> 2) < 1 ? 1 : NTE / (dim >> 2);
+    per = (nparts + groups - 1) / groups;
+    if (per < 1) per = 1;
+}
+// which 0: over the n_chunks FFN partials (attention and head prologues), 1: over the n_groups ones.
+__device__ __forceinline__ ProGeom pro_geom(const l3m_dmodel &M, int which) {
     ProGeom g;
-    g.n4 = dim >> 2;
-    g.groups = NTE / g.n4 < 1 ? 1 : NTE / g.n4;
-    g.per = (nparts + g.groups - 1) / g.groups;
-    if (g.per < 1) g.per = 1;
+    g.n4 = M.dim >> 2;
+    g.groups = M.pro_groups[which];
+    g.per = M.pro_per[which];
+    g.nparts = which ? M.n_groups : M.n_chunks;
     return g;
+}
+// tid / n4 and tid % n4 (tid < NTE <= 2^10, n4 <= 2^10) without an integer division per thread:
+// (tid + 0.5) / n4 is at least 0.5 / n4 >= 2^-11 away from an integer, far more than the float
+// product's error, so its floor is exact.
+__device__ __forceinline__ void split_tid(int tid, int n4, int &grp, int &f) {
+    const float inv = __builtin_amdgcn_rcpf((float)n4);   // within 1 ulp: the margin above is far larger
+    grp = (int)(((float)tid + 0.5f) * inv);
+    f = tid - grp * n4;
 }
 // Loads are unconditional (indices clamped into range) wherever possible: a load under a branch that
 // later merges makes the compiler wait for it there, before the weight stream is issued.
 // embed is passed by value: a pointer into the kernel's argument struct would move that struct to scratch.
 template <bool COH>
-__device__ __forceinline__ void pro_load(Pro &P, const float *base, const float *parts, int nparts, int dim, const float *nw,
+__device__ __forceinline__ void pro_load(Pro &P, const float *base, const float *parts, const ProGeom &G, const float *nw,
                                          l3m_dmat embed, bool use_embed, int tok, const float *rope_row, int hd) {
-    const int tid = tidx();
-    const ProGeom G = pro_geom(dim, nparts);
-    const int f = tid % G.n4, grp = tid / G.n4, j0 = grp * G.per, own = tid < G.n4 ? tid : G.n4 - 1;
+    const int tid = tidx(), nparts = G.nparts, dim = 4 * G.n4;
+    int f, grp;
+    split_tid(tid, G.n4, grp, f);
+    const int j0 = grp * G.per, own = tid < G.n4 ? tid : G.n4 - 1;
     P.nw = ldg16f(nw, own);
     P.base = ld16f<COH>(base, f);
 #pragma unroll
@@ -735,11 +746,12 @@ __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float 
 // Returns x[4f, 4f+4) to owner f (zeros to the other threads); stores it to keep when given; writes the
 // RoPE angles to cs_lds when given. pbuf: NTE float4 of LDS. All threads call it.
 template <bool COH>
-__device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, int nparts, int dim, bool use_embed, float4 *pbuf, float *keep,
+__device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, const ProGeom &G, bool use_embed, float4 *pbuf, float *keep,
                              float *cs_lds, int hd) {
-    const int tid = tidx();
-    const ProGeom G = pro_geom(dim, nparts);
-    const int f = tid % G.n4, grp = tid / G.n4, j0 = grp * G.per;
+    const int tid = tidx(), nparts = G.nparts, dim = 4 * G.n4;
+    int f, grp;
+    split_tid(tid, G.n4, grp, f);
+    const int j0 = grp * G.per;
     if (cs_lds && tid < (hd >> 1)) ((float2 *)cs_lds)[tid] = P.cs;
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
     if (use_embed) {
@@ -782,9 +794,9 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(
 // x[4f, 4f+4) as pro_finish forms it from the same inputs, for one thread: base and the parts grouped
 // and added in the same order (a group that leaves some of its FILL_PER slots unused adds +0.0 for
 // them, which turns a -0.0 sum into +0.0), read with device-coherent loads.
-__device__ __forceinline__ float4 parts_sum_at(const float *base, const float *parts, int nparts, int dim, int f) {
+__device__ __forceinline__ float4 parts_sum_at(const float *base, const float *parts, const ProGeom &G, int f) {
     constexpr int B = 16;                             // parts loaded at once; the rest one at a time
-    const ProGeom G = pro_geom(dim, nparts);
+    const int nparts = G.nparts, dim = 4 * G.n4;
     const size_t stride = (size_t)(dim >> 2);
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 p[B];
@@ -814,7 +826,7 @@ __device__ __forceinline__ float4 parts_sum_at(const float *base, const float *p
 // (zero beyond k): the reference's per-32-block int8 quantization (8 lanes per block), bf16 or f32.
 // Ends with a barrier.
 template <int DT>
-__device__ __forceinline__ void prep_owned(float4 y, uint8_t *act, int kp) {
+__device__ __forceinline__ void prep_body(float4 y, uint8_t *act, int kp) {
     const int f = tidx();
     if constexpr (quantized(DT)) {
         float am = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
@@ -836,17 +848,36 @@ __device__ __forceinline__ void prep_owned(float4 y, uint8_t *act, int kp) {
     } else {
         if (4 * f < kp) *(float4 *)(act + 16 * f) = y;
     }
+}
+// Only the wavefronts that hold prepared elements (4 per thread) do the work; the others go straight to
+// the barrier, so they take no issue slots from the SIMDs they share.
+template <int DT>
+__device__ __forceinline__ void prep_owned(float4 y, uint8_t *act, int kp) {
+    if (wave_id() * 256 < kp) prep_body<DT>(y, act, kp);
     __syncthreads();
 }
 
 // RMSNorm (ops.c:13-18: s = 1/sqrt(sum x^2 / n + eps), y = x * s * w) of the owned x, then its prep.
+// The sum of squares is red_sum's (same slots, same order of additions); wavefronts past the owned
+// elements write their zero without the reduction work and skip the rest.
 template <int DT>
 __device__ __forceinline__ void norm_prep(float4 x, float4 nw, int k, int kp, float eps, uint8_t *act, Red &red) {
-    const float tot = red_sum(red, x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
-    const float s = 1.0f / sqrtf(tot / (float)k + eps);
-    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * (int)tidx() < k) y = make_float4(x.x * s * nw.x, x.y * s * nw.y, x.z * s * nw.z, x.w * s * nw.w);
-    prep_owned<DT>(y, act, kp);
+    const int wave = wave_id();
+    const bool owner = wave * 256 < kp;               // kp >= k: these waves also write the padding
+    float *slot = red.scr + 16 * (red.k++ & 1);
+    const float part = owner ? lanes_sum<64>(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w) : 0.f;
+    if ((tidx() & 63) == 0) slot[wave] = part;
+    __syncthreads();
+    if (owner) {
+        const float4 *sv = (const float4 *)slot;
+        const float4 a = sv[0], b = sv[1], c = sv[2], d = sv[3];
+        const float tot = (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) + (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
+        const float s = 1.0f / sqrtf(tot / (float)k + eps);
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (4 * (int)tidx() < k) y = make_float4(x.x * s * nw.x, x.y * s * nw.y, x.z * s * nw.z, x.w * s * nw.w);
+        prep_body<DT>(y, act, kp);
+    }
+    __syncthreads();
 }
 
 // LDS regions of the step kernels (byte offsets, 16-aligned) from the layer geometry. `work` holds the
@@ -855,7 +886,7 @@ __host__ __device__ inline size_t work_bytes(size_t pairs) {
     const size_t w = 64 * pairs;
     return align16(w > 16 * (size_t)NTE ? w : 16 * (size_t)NTE);
 }
-struct LdsA { size_t act, work, q, cur, cs, sc, vred, att, act2, scr, kvb, total; };
+struct LdsA { size_t act, work, q, cur, cs, vred, att, act2, scr, kvb, total; };
 __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g, int kv_lds) {
     LdsA L;
     size_t o = 0;
@@ -865,13 +896,19 @@ __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3
     L.q = o;    o += align16(4 * (size_t)g.nq * hd);
     L.cur = o;  o += align16(4 * (size_t)g.nkv * hd);              // this step's k, v rows: bf16 [2][nkv][hd]
     L.cs = o;   o += align16(4 * (size_t)hd);
-    L.sc = o;   o += align16(4 * (size_t)(ctx + 4));
-    L.vred = o; o += align16(4 * (size_t)NWE * hd);
+    L.vred = o; o += align16(4 * (size_t)NWE * (hd + 2));
     L.att = o;  o += align16(4 * (size_t)kpad(g.nq * hd));
     L.act2 = o; o += align16(act_size(dt, g.nq * hd));
     L.scr = o;  o += 4 * 64;
     L.kvb = o;  o += kv_lds ? align16(4 * (size_t)g.nkv * ctx * hd) : 0;   // [K | V][nkv][ctx][hd] bf16
     L.total = o;
+    return L;
+}
+// The offsets as the host stored them in the group descriptor (l3m_group_layout).
+__device__ __forceinline__ LdsA lds_of(const l3m_dgroup &G) {
+    LdsA L;
+    L.act = G.lds[0]; L.work = G.lds[1]; L.q = G.lds[2]; L.cur = G.lds[3]; L.cs = G.lds[4];
+    L.vred = G.lds[5]; L.att = G.lds[6]; L.act2 = G.lds[7]; L.scr = G.lds[8]; L.kvb = G.lds[9]; L.total = 0;
     return L;
 }
 struct LdsB { size_t act, work, gu, act2, scr, total; };
@@ -885,6 +922,11 @@ __host__ __device__ inline LdsB lds_b(int dt, int dim, const l3m_dchunk &c) {
     L.act2 = o; o += align16(act_size(dt, c.nf));
     L.scr = o;  o += 4 * 64;
     L.total = o;
+    return L;
+}
+__device__ __forceinline__ LdsB lds_of(const l3m_dchunk &C) {
+    LdsB L;
+    L.act = C.lds[0]; L.work = C.lds[1]; L.gu = C.lds[2]; L.act2 = C.lds[3]; L.scr = C.lds[4]; L.total = 0;
     return L;
 }
 struct LdsH { size_t act, work, y, scr, total; };
@@ -904,7 +946,7 @@ __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg)
 // Rows up to pos - 1 were written by earlier steps, so the copy can start at the top of the kernel.
 template <bool COH>
 __device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int kv0, int nkv, int pos) {
-    const int wave = tidx() >> 6, lane = tidx() & 63;
+    const int wave = wave_id(), lane = tidx() & 63;
     const size_t win = (size_t)M.ctx * M.hd, total = (size_t)pos * M.hd * 2;     // bytes per head, K or V
     const int nch = (int)((total + 1023) / 1024), items = 2 * nkv * nch;
     for (int it = wave; it < items; it += NWE) {
@@ -926,81 +968,126 @@ __device__ __forceinline__ float dot8_bf16(const float *q, uint4 k, float acc) {
     return acc;
 }
 
-// Attention of the group's query heads over positions 0..pos (ops.c:58-73). Lane j of each aligned
-// group of LP lanes takes dims [8j, 8j+8) of one position (LP = hd/8 rounded up to a power of two):
-// scores are lane-group sums, the softmax is a workgroup max and sum, and the weighted V sum runs over
-// positions g, g + NTE/LP, ... per lane group, then across lane groups (in a wavefront, then over the
-// wavefronts through LDS). K, V rows before pos come from the LDS window (WIN) or the cache, row pos
-// from cur (this step's rows, bf16 as the cache holds them).
+// Attention of the group's query heads over positions 0..pos (ops.c:58-73), split-softmax form: each
+// head takes W wavefronts, W from the context length (at most ATT_IT position rounds per wavefront, and
+// no more wavefronts than the workgroup has per head). In a wavefront, lane j of each aligned group of
+// LP lanes holds dims [8j, 8j+8) of one position (LP = hd/8 rounded up to a power of two); a round scores
+// 64/LP positions (lane-group sums), and the wavefront keeps a running max m, a running sum l of
+// exp(s - m) and the running exp-weighted V sum o, rescaled when m grows. With W > 1 the wavefronts'
+// (m, l, o) meet in LDS after one barrier and combine as exp(m_w - M) weights. K, V rows before pos come
+// from the LDS window (WIN) or the cache, row pos from cur (this step's rows, bf16 as the cache holds
+// them). vred: NWE * (hd + 2) floats of LDS. Ends with a barrier.
+constexpr int ATT_IT = 4;
 template <bool WIN, bool COH>
 __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer, int pos, const float *qh, const uint16_t *cur,
-                             const uint16_t *kvb, float *sc, float *vred, float *att, Red &red) {
-    const int hd = M.hd, nv = hd >> 3, LP = nv <= 4 ? 4 : nv <= 8 ? 8 : nv <= 16 ? 16 : 32;
-    const int tid = tidx(), lane = tid & 63, j = tid & (LP - 1), g = tid / LP, NG = NTE / LP, n = pos + 1;
-    const int hpk = M.n_heads / M.n_kv;
-    const float scale = 1.0f / sqrtf((float)hd);
+                             const uint16_t *kvb, float *vred, float *att) {
+    static_assert(ATT_IT == 4, "the shift below is log2(ATT_IT * 64 / LP)");
+    const int hd = M.hd, nv = hd >> 3, lg = nv <= 4 ? 2 : nv <= 8 ? 3 : nv <= 16 ? 4 : 5, LP = 1 << lg, PPW = 64 >> lg;
+    const int lane = tidx() & 63, wave = wave_id(), j = lane & (LP - 1), gl = lane >> lg, n = pos + 1;
+    const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
     const size_t win = (size_t)M.ctx * hd;
-    for (int h = 0; h < G.nq; h++) {
-        const int kvl = (G.q0 + h) / hpk - G.kv0;
-        const uint16_t *kw = WIN ? kvb + kvl * win : M.kc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
-        const uint16_t *vw = WIN ? kvb + (G.nkv + kvl) * win : M.vc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
-        const uint4 *kcur = (const uint4 *)(cur + kvl * hd), *vcur = (const uint4 *)(cur + (G.nkv + kvl) * hd);
-        float q[8];
-        {
-            const float4 a = j < nv ? ((const float4 *)(qh + h * hd))[2 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 b = j < nv ? ((const float4 *)(qh + h * hd))[2 * j + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
-            q[0] = a.x; q[1] = a.y; q[2] = a.z; q[3] = a.w; q[4] = b.x; q[5] = b.y; q[6] = b.z; q[7] = b.w;
-        }
-        float mx = -INFINITY;
-        for (int t0 = 0; t0 < n; t0 += NG) {
-            const int t = t0 + g;
-            float part = 0.f;
-            if (t < n && j < nv) {
-                uint4 kk;
-                if (t == pos) kk = kcur[j];
-                else if (WIN) kk = ((const uint4 *)(kw + (size_t)t * hd))[j];
-                else kk = ld16<COH>(kw, (size_t)t * (hd >> 3) + j);
-                part = dot8_bf16(q, kk, 0.f);
+    // W = 2^wl wavefronts per head: the fewest that keep each at ATT_IT rounds or less, at most 2^att_wl
+    const int need = (n + (256 >> lg) - 1) >> (8 - lg);
+    int wl = need <= 1 ? 0 : 32 - __builtin_clz((unsigned)(need - 1));
+    wl = wl < G.att_wl ? wl : G.att_wl;
+    const int W = 1 << wl, HB = NWE >> wl;            // heads per batch
+    float *ml = vred + NWE * hd;                      // (m, l) per wavefront
+    for (int h0 = 0; h0 < G.nq; h0 += HB) {
+        const int h = h0 + (wave >> wl), wi = wave & (W - 1);
+        const bool active = h < G.nq;
+        if (active) {
+            // (q0 + h) / hpk by an exact float reciprocal (both far below 2^20)
+            const int kvl = (int)(((float)(G.q0 + h) + 0.5f) * ihpk) - G.kv0;
+            const uint16_t *kw = WIN ? kvb + kvl * win : M.kc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
+            const uint16_t *vw = WIN ? kvb + (G.nkv + kvl) * win : M.vc + ((size_t)layer * M.n_kv + G.kv0 + kvl) * win;
+            const uint4 *kcur = (const uint4 *)(cur + kvl * hd), *vcur = (const uint4 *)(cur + (G.nkv + kvl) * hd);
+            float q[8];
+            {
+                const float4 a = j < nv ? ((const float4 *)(qh + h * hd))[2 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 b = j < nv ? ((const float4 *)(qh + h * hd))[2 * j + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+                q[0] = a.x; q[1] = a.y; q[2] = a.z; q[3] = a.w; q[4] = b.x; q[5] = b.y; q[6] = b.z; q[7] = b.w;
             }
-            const float s = lanes_sum_n(part, LP) * scale;
-            if (t < n) {
-                if (j == 0) sc[t] = s;
-                mx = fmaxf(mx, s);
-            }
-        }
-        mx = red_max(red, mx);
-        float sum = 0.f;
-        for (int t = tid; t < n; t += NTE) {
-            const float e = expf(sc[t] - mx);
-            sc[t] = e;
-            sum += e;
-        }
-        sum = red_sum(red, sum);
-        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (j < nv)
-            for (int t = g; t < n; t += NG) {
-                const float p = sc[t] / sum;
-                uint4 vv;
-                if (t == pos) vv = vcur[j];
-                else if (WIN) vv = ((const uint4 *)(vw + (size_t)t * hd))[j];
-                else vv = ld16<COH>(vw, (size_t)t * (hd >> 3) + j);
-                o[0] = fmaf(p, bf16_f32(vv.x & 0xFFFF), o[0]); o[1] = fmaf(p, bf16_f32(vv.x >> 16), o[1]);
-                o[2] = fmaf(p, bf16_f32(vv.y & 0xFFFF), o[2]); o[3] = fmaf(p, bf16_f32(vv.y >> 16), o[3]);
-                o[4] = fmaf(p, bf16_f32(vv.z & 0xFFFF), o[4]); o[5] = fmaf(p, bf16_f32(vv.z >> 16), o[5]);
-                o[6] = fmaf(p, bf16_f32(vv.w & 0xFFFF), o[6]); o[7] = fmaf(p, bf16_f32(vv.w >> 16), o[7]);
-            }
+            float m = -INFINITY, l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            // rounds r = 0, 1, ... cover positions (r * W + wi) * PPW + gl; ATT_IT rounds per chunk
+            for (int r0 = 0; (r0 * W + wi) * PPW < n; r0 += ATT_IT) {
+                float s[ATT_IT];
+                float cm = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 8; e++) o[e] = strided_sum(o[e], LP);
-        if (lane < LP && j < nv) {
-            float4 *d = (float4 *)(vred + (tid >> 6) * hd + 8 * j);
-            d[0] = make_float4(o[0], o[1], o[2], o[3]);
-            d[1] = make_float4(o[4], o[5], o[6], o[7]);
+                for (int k = 0; k < ATT_IT; k++) {
+                    const int t = ((r0 + k) * W + wi) * PPW + gl;
+                    float part = 0.f;
+                    if (t < n && j < nv) {
+                        uint4 kk;
+                        if (t == pos) kk = kcur[j];
+                        else if (WIN) kk = ((const uint4 *)(kw + (size_t)t * hd))[j];
+                        else kk = ld16<COH>(kw, (size_t)t * (hd >> 3) + j);
+                        part = dot8_bf16(q, kk, 0.f);
+                    }
+                    s[k] = t < n ? lanes_sum_n(part, LP) * scale : -INFINITY;
+                    cm = fmaxf(cm, s[k]);
+                }
+                const float mn = fmaxf(m, lanes_max<64>(cm));
+                const float alpha = expf(m - mn);     // m = -inf at the start: alpha = 0
+                l *= alpha;
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[e] *= alpha;
+#pragma unroll
+                for (int k = 0; k < ATT_IT; k++) {
+                    const int t = ((r0 + k) * W + wi) * PPW + gl;
+                    if (t < n) {
+                        const float p = expf(s[k] - mn);
+                        l += p;
+                        if (j < nv) {
+                            uint4 vv;
+                            if (t == pos) vv = vcur[j];
+                            else if (WIN) vv = ((const uint4 *)(vw + (size_t)t * hd))[j];
+                            else vv = ld16<COH>(vw, (size_t)t * (hd >> 3) + j);
+                            o[0] = fmaf(p, bf16_f32(vv.x & 0xFFFF), o[0]); o[1] = fmaf(p, bf16_f32(vv.x >> 16), o[1]);
+                            o[2] = fmaf(p, bf16_f32(vv.y & 0xFFFF), o[2]); o[3] = fmaf(p, bf16_f32(vv.y >> 16), o[3]);
+                            o[4] = fmaf(p, bf16_f32(vv.z & 0xFFFF), o[4]); o[5] = fmaf(p, bf16_f32(vv.z >> 16), o[5]);
+                            o[6] = fmaf(p, bf16_f32(vv.w & 0xFFFF), o[6]); o[7] = fmaf(p, bf16_f32(vv.w >> 16), o[7]);
+                        }
+                    }
+                }
+                m = mn;
+            }
+            // over the wavefront's position groups: lanes j < LP end up with the sums
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = strided_sum(o[e], LP);
+            l = strided_sum(l, LP);
+            if (W == 1) {
+                if (lane < LP && j < nv) {
+                    const float inv = 1.0f / l;
+                    float4 *d = (float4 *)(att + h * hd + 8 * j);
+                    d[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+                    d[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
+                }
+            } else {
+                if (lane < LP && j < nv) {
+                    float4 *d = (float4 *)(vred + wave * hd + 8 * j);
+                    d[0] = make_float4(o[0], o[1], o[2], o[3]);
+                    d[1] = make_float4(o[4], o[5], o[6], o[7]);
+                }
+                if (lane == 0) { ml[2 * wave] = m; ml[2 * wave + 1] = l; }
+            }
         }
-        __syncthreads();
-        if (tid < hd) {
-            float a = vred[tid];
-            for (int w = 1; w < NWE; w++) a += vred[w * hd + tid];
-            att[h * hd + tid] = a;
+        if (W > 1) {
+            __syncthreads();
+            // head h's W wavefronts combine: dims d = wi * 64 + lane, + 64 * W, ... of the head
+            if (active) {
+                const int w0 = wave - wi;
+                float mx = ml[2 * w0];
+                for (int k = 1; k < W; k++) mx = fmaxf(mx, ml[2 * (w0 + k)]);
+                for (int d = wi * 64 + lane; d < hd; d += 64 * W) {
+                    float num = 0.f, den = 0.f;
+                    for (int k = 0; k < W; k++) {
+                        const float a = expf(ml[2 * (w0 + k)] - mx);
+                        den = fmaf(a, ml[2 * (w0 + k) + 1], den);
+                        num = fmaf(a, vred[(w0 + k) * hd + d], num);
+                    }
+                    att[h * hd + d] = num / den;
+                }
+            }
         }
         __syncthreads();
     }
@@ -1029,6 +1116,15 @@ template <int DT> __device__ __forceinline__ void head_issue(HeadW<DT> &w, const
     pref_load<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, 0);
 }
 
+// The persistent path's K/V window copy for the attention block of group G at (layer, pos): rows
+// 0..pos-1 were written in earlier steps, so it can run while the block waits for its inputs.
+template <int DT>
+__device__ __forceinline__ void attn_kv_window(const l3m_dmodel &M, const l3m_dgroup &G, int layer, int pos, uint8_t *smem) {
+    if (!M.kv_lds) return;
+    const LdsA L = lds_of(G);
+    kv_window_dma<true>((uint16_t *)(smem + L.kvb), M, layer, G.kv0, G.nkv, pos);
+}
+
 // The attention block of head group gi (engine.c:236-258) at `layer`, position pos: x = xb + the FFN
 // partials (layer 0: the embedding row of tokens[pos]), RMSNorm, prep, the group's q/k/v rows, RoPE,
 // bf16 K/V into the cache, attention, prep, the group's Wo columns -> po[gi]. Group 0 keeps x in xa.
@@ -1036,20 +1132,22 @@ template <int DT, bool PRE>
 __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dgroup &G, int layer, int pos,
                                            int tok, int gi, AttnW<DT> &w, uint8_t *smem) {
     const int tid = tidx(), dim = M.dim, hd = M.hd, kp = kpad(dim);
-    const LdsA L = lds_a(DT, dim, M.ctx, hd, G, M.kv_lds);
+    const LdsA L = lds_of(G);
     float *work = (float *)(smem + L.work), *qh = (float *)(smem + L.q), *cs = (float *)(smem + L.cs);
-    float *sc = (float *)(smem + L.sc), *vred = (float *)(smem + L.vred), *att = (float *)(smem + L.att);
+    float *vred = (float *)(smem + L.vred), *att = (float *)(smem + L.att);
     uint16_t *cur = (uint16_t *)(smem + L.cur), *kvb = (uint16_t *)(smem + L.kvb);
     uint8_t *act = smem + L.act, *act2 = smem + L.act2;
     Red red{(float *)(smem + L.scr), 0};
 
     Pro P;
-    pro_load<PRE>(P, M.xb, M.pd, M.n_chunks, dim, Lw.attn_norm, M.embed, layer == 0, tok, M.rope + (size_t)pos * hd, hd);
+    const ProGeom PG = pro_geom(M, 0);
+    pro_load<PRE>(P, M.xb, M.pd, PG, Lw.attn_norm, M.embed, layer == 0, tok, M.rope + (size_t)pos * hd, hd);
     if constexpr (!PRE) attn_issue<DT>(w, G);
-    const float4 x = pro_finish<PRE>(P, M.pd, M.n_chunks, dim, layer == 0, (float4 *)work, gi == 0 ? M.xa : nullptr, cs, hd);
+    const float4 x = pro_finish<PRE>(P, M.pd, PG, layer == 0, (float4 *)work, gi == 0 ? M.xa : nullptr, cs, hd);
     // K, V rows 0..pos-1 (no dependence on this step). Issued after the prologue is consumed: a copy of
     // data-dependent length ahead of it would make the compiler wait for every load in flight there.
-    if (M.kv_lds) kv_window_dma<PRE>(kvb, M, layer, G.kv0, G.nkv, pos);
+    // The persistent path issues it before it waits for the block's inputs (attn_kv_window).
+    if (!PRE && M.kv_lds) kv_window_dma<false>(kvb, M, layer, G.kv0, G.nkv, pos);
     norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
 
     mv<DT, nslot_a<DT>()>(w.a, G.qkv, act, kp, work);
@@ -1058,27 +1156,28 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // to bf16 as the cache holds them (engine.c:247-248), into cur and (for the heads this group writes)
     // the cache
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
+    const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
     rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner) {
         if (i < nqd + nkd) {
-            const int local = i < nqd ? i : i - nqd;
-            const float2 c = ((const float2 *)cs)[(local % hd) >> 1];
+            const int local = i < nqd ? i : i - nqd, head = (int)(((float)local + 0.5f) * inv_hd);
+            const float2 c = ((const float2 *)cs)[(local - head * hd) >> 1];
             y = (i & 1) ? partner * c.y + y * c.x : y * c.x - partner * c.y;
         }
         if ((tidx() & 3) == 0) {
             if (i < nqd) qh[i] = y;
             else {
-                const int r = i - nqd, kv = r < nkd ? 0 : 1, jj = r - kv * nkd, kvl = jj / hd;
+                const int r = i - nqd, kv = r < nkd ? 0 : 1, jj = r - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
                 const uint16_t hb = f32_bf16(y);
                 cur[kv * nkd + jj] = hb;
                 if (G.write_kv >> kvl & 1u)
-                    gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + jj % hd] = hb;
+                    gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + (jj - kvl * hd)] = hb;
             }
         }
     });
     if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, sc, vred, att, red);
-    else attend_group<false, PRE>(M, G, layer, pos, qh, cur, kvb, sc, vred, att, red);
+    if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
+    else attend_group<false, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
 
     // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
     const int kq = kpad(nqd);
@@ -1095,15 +1194,16 @@ template <int DT, bool PRE>
 __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dchunk &C, int ci, FfnW<DT> &w,
                                           uint8_t *smem) {
     const int tid = tidx(), dim = M.dim, kp = kpad(dim);
-    const LdsB L = lds_b(DT, dim, C);
+    const LdsB L = lds_of(C);
     float *work = (float *)(smem + L.work), *gu = (float *)(smem + L.gu);
     uint8_t *act = smem + L.act, *act2 = smem + L.act2;
     Red red{(float *)(smem + L.scr), 0};
 
     Pro P;
-    pro_load<PRE>(P, M.xa, M.po, M.n_groups, dim, Lw.ffn_norm, M.embed, false, 0, nullptr, 0);     // x += proj (engine.c:259)
+    const ProGeom PG = pro_geom(M, 1);
+    pro_load<PRE>(P, M.xa, M.po, PG, Lw.ffn_norm, M.embed, false, 0, nullptr, 0);     // x += proj (engine.c:259)
     if constexpr (!PRE) ffn_issue<DT>(w, C);
-    const float4 x = pro_finish<PRE>(P, M.po, M.n_groups, dim, false, (float4 *)work, ci == 0 ? M.xb : nullptr, nullptr, 0);
+    const float4 x = pro_finish<PRE>(P, M.po, PG, false, (float4 *)work, ci == 0 ? M.xb : nullptr, nullptr, 0);
     norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
     __syncthreads();
@@ -1159,9 +1259,10 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
         x = tid < n4 ? xv : make_float4(0.f, 0.f, 0.f, 0.f);
     } else {
         Pro P;
-        pro_load<false>(P, M.xb, M.pd, M.n_chunks, dim, M.norm, M.embed, false, 0, nullptr, 0);   // x += down (engine.c:275), last layer
+        const ProGeom PG = pro_geom(M, 0);
+        pro_load<false>(P, M.xb, M.pd, PG, M.norm, M.embed, false, 0, nullptr, 0);   // x += down (engine.c:275), last layer
         head_issue<DT>(w, V);
-        x = pro_finish<false>(P, M.pd, M.n_chunks, dim, false, (float4 *)work, nullptr, nullptr, 0);
+        x = pro_finish<false>(P, M.pd, PG, false, (float4 *)work, nullptr, nullptr, 0);
         nw = P.nw;
     }
     norm_prep<DT>(x, nw, dim, kp, M.eps, act, red);
@@ -1417,7 +1518,7 @@ __device__ __noinline__ void reduce_final(const l3m_dmodel *Mp, int g) {
     const l3m_dmodel M = fixed(Mp);
     const int n4 = M.dim >> 2, per = (n4 + M.n_groups - 1) / M.n_groups;
     const int f = g * per + tidx();
-    if (tidx() < per && f < n4) stcoh16(M.xf, f, parts_sum_at(M.xb, M.pd, M.n_chunks, M.dim, f));
+    if (tidx() < per && f < n4) stcoh16(M.xf, f, parts_sum_at(M.xb, M.pd, pro_geom(M, 0), f));
 }
 
 // The roles, each in a function of its own (so each gets its own register allocation and nothing of one
@@ -1437,6 +1538,7 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
         const l3m_dgroup G = fixed(Lw.groups, g);
         AttnW<DT> wt;
         attn_issue<DT>(wt, G);
+        attn_kv_window<DT>(M, G, l, pos, smem);
         const unsigned epoch = (unsigned)(s * nl + l);
         int tok = 0;
         if (l == 0 && s > 0 && pos - 1 >= R.head_from) {
@@ -1780,6 +1882,25 @@ int l3m_k_argmax(const float *x, int n, int32_t *out, void *stream) {
 }
 
 unsigned l3m_lds_attn(int dtype, int dim, int ctx, int hd, const l3m_dgroup *g, int kv_lds) { return (unsigned)lds_a(dtype, dim, ctx, hd, *g, kv_lds).total; }
+void l3m_group_layout(int dtype, int dim, int ctx, int hd, l3m_dgroup *g) {
+    const LdsA L = lds_a(dtype, dim, ctx, hd, *g, 1);
+    const size_t off[10] = {L.act, L.work, L.q, L.cur, L.cs, L.vred, L.att, L.act2, L.scr, L.kvb};
+    for (int i = 0; i < 10; i++) g->lds[i] = (unsigned)off[i];
+    int wmax = g->nq < NWE ? NWE / g->nq : 1, wl = 0;
+    while ((2 << wl) <= wmax) wl++;
+    g->att_wl = wl;
+}
+void l3m_chunk_layout(int dtype, int dim, l3m_dchunk *c) {
+    const LdsB L = lds_b(dtype, dim, *c);
+    const size_t off[5] = {L.act, L.work, L.gu, L.act2, L.scr};
+    for (int i = 0; i < 5; i++) c->lds[i] = (unsigned)off[i];
+}
+void l3m_model_layout(l3m_dmodel *m) {
+    pro_shape(m->dim, m->n_chunks, m->pro_groups[0], m->pro_per[0]);
+    pro_shape(m->dim, m->n_groups, m->pro_groups[1], m->pro_per[1]);
+    m->att_scale = 1.0f / sqrtf((float)m->hd);
+    m->hpk = m->n_heads / m->n_kv;
+}
 unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c) { return (unsigned)lds_b(dtype, dim, *c).total; }
 unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg) { return (unsigned)lds_h(dtype, dim, nb, tiles_per_wg).total; }
 int l3m_step_slots(int dtype, int which) {
