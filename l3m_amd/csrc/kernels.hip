@@ -659,12 +659,31 @@ __device__ void wge_argmax(float &v, int &i, float *sv, int *si) {
     for (int w = 1; w < NWE; w++) better(v, i, sv[w], si[w]);
 }
 
-// Matvec results res[pair * 16 + row] summed per row in block order by 4 adjacent lanes (each a
-// quarter of the blocks, quarters added pairwise); every lane of the quad gets the row's value y.
-// f(i, y, partner) runs in every lane for rows i < rows, partner being row i ^ 1's value.
+// Matvec results res[pair * 16 + row] summed per row: four quarter sums of the blocks, each in block
+// order, added pairwise ((q0 + q1) + (q2 + q3)). Rows of more than 4 blocks take 4 adjacent lanes (one
+// quarter each); shorter rows one lane (all four quarters), which gives the same sums in a quarter of the
+// passes. f(i, y, partner, lead) runs in every lane for rows i < rows, partner being row i ^ 1's value
+// and lead true in one lane per row.
 template <class F>
 __device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, int rows, F f) {
-    const int nb = m.nb, q = tidx() & 3, b0 = q * nb >> 2, b1 = (q + 1) * nb >> 2;
+    const int nb = m.nb;
+    if (nb <= 4) {
+        for (int base = 0; base < rows; base += NTE) {
+            const int i = base + tidx();
+            float s[4] = {0.f, 0.f, 0.f, 0.f};
+            if (i < rows) {
+                const float *p = res + (size_t)(i >> 4) * nb * 16 + (i & 15);
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    for (int b = q * nb >> 2; b < (q + 1) * nb >> 2; b++) s[q] += p[b * 16];
+            }
+            const float y = (s[0] + s[1]) + (s[2] + s[3]);
+            const float partner = dppf<QP_X1>(y);     // row i ^ 1 is the neighbouring lane
+            if (i < rows) f(i, y, partner, true);
+        }
+        return;
+    }
+    const int q = tidx() & 3, b0 = q * nb >> 2, b1 = (q + 1) * nb >> 2;
     for (int base = 0; base < rows; base += NTE / 4) {
         const int i = base + (tidx() >> 2);
         float y = 0.f;
@@ -675,7 +694,7 @@ __device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, i
         }
         y = lanes_sum<4>(y);
         const float partner = dppf<ROW_HALF_MIRROR>(y);
-        if (i < rows) f(i, y, partner);
+        if (i < rows) f(i, y, partner, q == 0);
     }
 }
 
@@ -1157,13 +1176,13 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // the cache
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
     const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
-    rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner) {
+    rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner, bool lead) {
         if (i < nqd + nkd) {
             const int local = i < nqd ? i : i - nqd, head = (int)(((float)local + 0.5f) * inv_hd);
             const float2 c = ((const float2 *)cs)[(local - head * hd) >> 1];
             y = (i & 1) ? partner * c.y + y * c.x : y * c.x - partner * c.y;
         }
-        if ((tidx() & 3) == 0) {
+        if (lead) {
             if (i < nqd) qh[i] = y;
             else {
                 const int r = i - nqd, kv = r < nkd ? 0 : 1, jj = r - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
@@ -1185,7 +1204,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     mv<DT, nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
     __syncthreads();
     float *po = M.po + (size_t)gi * dim;
-    rows_sum4(G.wo, work, dim, [&](int i, float y, float) { if ((tidx() & 3) == 0) gw(po)[i] = y; });
+    rows_sum4(G.wo, work, dim, [&](int i, float y, float, bool lead) { if (lead) gw(po)[i] = y; });
 }
 
 // The FFN block of chunk ci (engine.c:259-275): x = xa + the attention partials, RMSNorm, prep, the
@@ -1207,7 +1226,7 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
     __syncthreads();
-    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float) { if ((tidx() & 3) == 0) gu[i] = y; });
+    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float, bool lead) { if (lead) gu[i] = y; });
     __syncthreads();
     // h = up * silu(gate) (ops.c:49-51) for the owned 4 rows (gate tile t and up tile t interleave), prepared
     const int kf = kpad(C.nf);
@@ -1225,7 +1244,7 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     mv<DT, nslot_b<DT>()>(w.b, C.down, act2, kf, work);
     __syncthreads();
     float *pd = M.pd + (size_t)ci * dim;
-    rows_sum4(C.down, work, dim, [&](int i, float y, float) { if ((tidx() & 3) == 0) gw(pd)[i] = y; });
+    rows_sum4(C.down, work, dim, [&](int i, float y, float, bool lead) { if (lead) gw(pd)[i] = y; });
 }
 
 // Tiles [t0, t0 + tpw) of the head as a matrix of their own (the last slice may be short).
@@ -1268,7 +1287,7 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
     norm_prep<DT>(x, nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work);
     __syncthreads();
-    rows_sum4(V, work, V.rows, [&](int i, float yy, float) { if ((tidx() & 3) == 0) y[i] = yy; });
+    rows_sum4(V, work, V.rows, [&](int i, float yy, float, bool lead) { if (lead) y[i] = yy; });
     __syncthreads();
     float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab + (size_t)t0 * 16;
     v = -INFINITY;
