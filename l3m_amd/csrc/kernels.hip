@@ -551,16 +551,22 @@ __device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m
     const float inb = __builtin_amdgcn_rcpf((float)nb);
     const int x0 = (tidx() >> 4) + 4 * NWE * s0;      // the lane's pair in slot 0
     int b = x0 - (int)(((float)x0 + 0.5f) * inb) * nb;
-    const int step = 4 * NWE - (int)(((float)(4 * NWE) + 0.5f) * inb) * nb;
+    const int step = __builtin_amdgcn_readfirstlane(4 * NWE - (int)(((float)(4 * NWE) + 0.5f) * inb) * nb);
+    // Pin the loaded registers here: otherwise the compiler hoists their first use (the f16 scale
+    // conversion) up to the loads, and every wavefront stalls on its first load at entry.
 #pragma unroll
     for (int s = 0; s < NS; s++) {
-        // Pin the loaded registers here: otherwise the compiler hoists their first use (the f16 scale
-        // conversion) up to the loads, and every wavefront stalls on its first load at entry.
         asm volatile("" : "+v"(pf.sc[s]));
 #pragma unroll
         for (int v = 0; v < qbytes(DT) / 16; v++) asm volatile("" : "+v"(pf.w[s][v].x), "+v"(pf.w[s][v].y), "+v"(pf.w[s][v].z), "+v"(pf.w[s][v].w));
+    }
+    // a wavefront stops at its first slot past the end (a scalar branch); in its last slot the up to 3
+    // pairs past the end (loads repeat the last pair) write into the padding of res (res_bytes)
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
         const int p0 = (wave + (s0 + s) * NWE) * 4;
-        if (p0 + (lane >> 4) < n) res[p0 * 16 + lane] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b);
+        if (p0 >= n) break;
+        res[p0 * 16 + lane] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b);
         b += step;                                    // step < nb
         b -= b >= nb ? nb : 0;
     }
@@ -901,17 +907,21 @@ __device__ __forceinline__ void norm_prep(float4 x, float4 nw, int k, int kp, fl
 
 // LDS regions of the step kernels (byte offsets, 16-aligned) from the layer geometry. `work` holds the
 // prologue's group sums, then the per-pair matvec results.
-__host__ __device__ inline size_t work_bytes(size_t pairs) {
-    const size_t w = 64 * pairs;
+// Matvec results take 64 bytes per (tile, block) pair; a wavefront writes whole groups of 4 pairs
+// (those past the end into padding).
+__host__ __device__ inline size_t res_bytes(size_t pairs) { return 64 * ((pairs + 3) / 4 * 4); }
+__host__ __device__ inline size_t work_bytes(size_t a, size_t b) {
+    const size_t w = a > b ? a : b;
     return align16(w > 16 * (size_t)NTE ? w : 16 * (size_t)NTE);
 }
+
 struct LdsA { size_t act, work, q, cur, cs, vred, att, act2, scr, kvb, total; };
 __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g, int kv_lds) {
     LdsA L;
     size_t o = 0;
     const size_t pq = (size_t)g.qkv.tiles * g.qkv.nb, pw = (size_t)g.wo.tiles * g.wo.nb;
     L.act = o;  o += align16(act_size(dt, dim));
-    L.work = o; o += work_bytes(pq > pw ? pq : pw);
+    L.work = o; o += work_bytes(res_bytes(pq), res_bytes(pw));
     L.q = o;    o += align16(4 * (size_t)g.nq * hd);
     L.cur = o;  o += align16(4 * (size_t)g.nkv * hd);              // this step's k, v rows: bf16 [2][nkv][hd]
     L.cs = o;   o += align16(4 * (size_t)hd);
@@ -936,7 +946,7 @@ __host__ __device__ inline LdsB lds_b(int dt, int dim, const l3m_dchunk &c) {
     size_t o = 0;
     const size_t pg = (size_t)c.gate_up.tiles * c.gate_up.nb, pw = (size_t)c.down.tiles * c.down.nb;
     L.act = o;  o += align16(act_size(dt, dim));
-    L.work = o; o += work_bytes(pg > pw ? pg : pw);
+    L.work = o; o += work_bytes(res_bytes(pg), res_bytes(pw));
     L.gu = o;   o += align16(64 * (size_t)c.gate_up.tiles);
     L.act2 = o; o += align16(act_size(dt, c.nf));
     L.scr = o;  o += 4 * 64;
@@ -953,7 +963,7 @@ __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg)
     LdsH L;
     size_t o = 0;
     L.act = o;  o += align16(act_size(dt, dim));
-    L.work = o; o += work_bytes((size_t)tiles_per_wg * nb);
+    L.work = o; o += work_bytes(res_bytes((size_t)tiles_per_wg * nb), 0);
     L.y = o;    o += align16(64 * (size_t)tiles_per_wg);
     L.scr = o;  o += 4 * 64;
     L.total = o;
@@ -996,17 +1006,20 @@ __device__ __forceinline__ float dot8_bf16(const float *q, uint4 k, float acc) {
 // (m, l, o) meet in LDS after one barrier and combine as exp(m_w - M) weights. K, V rows before pos come
 // from the LDS window (WIN) or the cache, row pos from cur (this step's rows, bf16 as the cache holds
 // them). vred: NWE * (hd + 2) floats of LDS. Ends with a barrier.
-constexpr int ATT_IT = 4;
+#ifndef L3M_ATT_LOG_IT
+#define L3M_ATT_LOG_IT 2
+#endif
+constexpr int ATT_LOG_IT = L3M_ATT_LOG_IT, ATT_IT = 1 << ATT_LOG_IT;
 template <bool WIN, bool COH>
 __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer, int pos, const float *qh, const uint16_t *cur,
                              const uint16_t *kvb, float *vred, float *att) {
-    static_assert(ATT_IT == 4, "the shift below is log2(ATT_IT * 64 / LP)");
     const int hd = M.hd, nv = hd >> 3, lg = nv <= 4 ? 2 : nv <= 8 ? 3 : nv <= 16 ? 4 : 5, LP = 1 << lg, PPW = 64 >> lg;
     const int lane = tidx() & 63, wave = wave_id(), j = lane & (LP - 1), gl = lane >> lg, n = pos + 1;
     const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
     const size_t win = (size_t)M.ctx * hd;
     // W = 2^wl wavefronts per head: the fewest that keep each at ATT_IT rounds or less, at most 2^att_wl
-    const int need = (n + (256 >> lg) - 1) >> (8 - lg);
+    const int sh = ATT_LOG_IT + 6 - lg;               // ATT_IT * PPW = 2^sh positions per wavefront
+    const int need = (n + (1 << sh) - 1) >> sh;
     int wl = need <= 1 ? 0 : 32 - __builtin_clz((unsigned)(need - 1));
     wl = wl < G.att_wl ? wl : G.att_wl;
     const int W = 1 << wl, HB = NWE >> wl;            // heads per batch
