@@ -7,9 +7,12 @@ layers, 12 heads, ffn 2048, vocab 32000, ctx 128, tied q4_0 head, random-init N(
 seeded prompt and restarted when the context fills (the reference's bench loop, main.c:247-251).
 Weights are resident in HBM before the timed region. One JSON line on stdout:
   value / ms_per_step  generated tokens per second over exactly --steps tokens
-  roofline             the dominant step kernel (largest time per token; the attention block, the FFN block
-                       or the head): weight bytes per launch over its average duration (hipEvents on the
-                       library stream), against 8 TB/s HBM3E
+  roofline             the decode kernel (k_decode, one persistent launch per run of up to 64 steps): the
+                       algorithmic bytes of the steps it ran (body weights every step, head weights on steps
+                       with logits, K/V rows read and written) over its average launch duration (hipEvents
+                       around each launch on the library stream), against 8 TB/s HBM3E; traffic = the HBM
+                       bytes per launch that rocprofv3 counted for the same command (profiles/)
+  step_kernels         the one-graph-per-step path's three kernels, each timed alone at ctx/2
   matvec               per-dtype matvec GB/s at the microbench shapes, warm
                        (cache-resident) and cold (rotating over > 512 MiB of copies)
   cpu_baseline         fpedd/l3m itself (built from its sources into oracle/_ref), AVX2/AVX-512 path,
@@ -87,16 +90,30 @@ def matvec_bench(A, dtypes, iters=50):
     return out
 
 
-def measured_traffic(cfg_name, dtype, kernel):
-    """HBM bytes per launch of a step kernel (read + written), from the committed counter profile of this
+def decode_bytes(A, m, cfg, work):
+    """Algorithmic bytes of `work` = (steps, steps with the head, K/V rows read per kv head and layer)."""
+    lib, h = A.lib(), m._handle()
+    body = cfg.n_layers * (lib.l3m_kernel_bytes(h, 0, 0) + lib.l3m_kernel_bytes(h, 1, 0))
+    head = lib.l3m_kernel_bytes(h, 2, 0)
+    row = cfg.n_layers * cfg.n_kv_heads * 2 * (cfg.dim // cfg.n_heads) * 2      # K and V, bf16, every layer
+    steps, head_steps, kv_rows = work
+    return steps * body + head_steps * head + kv_rows * row + steps * row
+
+
+def measured_traffic(cfg_name, dtype, kernel, steps_per_launch=None):
+    """HBM bytes per launch of a kernel (read + written), from the committed counter profile of this
     configuration (profiles/decode_<config>_<dtype>_traffic.json: two rocprofv3 --pmc passes, FETCH_SIZE
-    and WRITE_SIZE, scaled by the plain copy kernel's readings); None when no profile covers it."""
-    import json
+    and WRITE_SIZE, scaled by the plain copy kernel's readings). k_decode's entry is per step (its launches
+    run different step counts), scaled here by this run's steps per launch. None when no profile covers it."""
     p = ROOT / "profiles" / f"decode_{cfg_name}_{dtype}_traffic.json"
     if not p.exists():
         return None
-    k = json.loads(p.read_text())["kernels"].get("k_" + kernel)
-    return None if k is None else k["read_bytes"] + k["write_bytes"]
+    k = json.loads(p.read_text())["kernels"].get(kernel if kernel.startswith("k_") else "k_" + kernel)
+    if k is None:
+        return None
+    if "read_bytes_per_step" in k:
+        return None if steps_per_launch is None else round((k["read_bytes_per_step"] + k["write_bytes_per_step"]) * steps_per_launch)
+    return k["read_bytes"] + k["write_bytes"]
 
 
 def copy_calibration(A, nbytes):
@@ -168,20 +185,36 @@ def main():
         prompt = A.prompt(1, cfg.vocab, cfg.n_prompt)
         m = A.Model(path)
         log(f"bench: {m.describe()} on {A.lib().l3m_dev_name().decode()}")
+        lib = A.lib()
         m.bench_decode(prompt, max(a.warmup, 1))
-        A.lib().l3m_dev_sync()
+        lib.l3m_dev_sync()
+        w0 = (C.c_double * 3)()
+        lib.l3m_decode_work(m._handle(), w0)
+        lib.l3m_decode_timer(1, None, None)
         t0 = time.perf_counter()
         m.bench_decode(prompt, a.steps)
-        A.lib().l3m_dev_sync()
+        lib.l3m_dev_sync()
         elapsed = time.perf_counter() - t0
+        us, launches = C.c_double(), C.c_int()
+        lib.l3m_decode_timer(0, C.byref(us), C.byref(launches))
+        w1 = (C.c_double * 3)()
+        lib.l3m_decode_work(m._handle(), w1)
         value = a.steps / elapsed
         log(f"bench: {a.steps} tokens in {elapsed * 1e3:.2f} ms = {value:.0f} tok/s")
+        decode = None
+        if m.persistent and launches.value:
+            work = [w1[i] - w0[i] for i in range(3)]
+            nbytes = decode_bytes(A, m, cfg, work)
+            decode = {"kernel": "k_decode", "launches": launches.value, "steps": work[0], "head_steps": work[1],
+                      "us": us.value / launches.value, "bytes": nbytes / launches.value, "GBs": nbytes / (us.value * 1e3)}
+            log(f"bench: k_decode {launches.value} launches, {work[0]:.0f} steps, {us.value / launches.value:.1f} us per launch, "
+                f"{decode['GBs']:.1f} GB/s algorithmic")
         kt = kernel_table(A, m, cfg)
         for r in kt:
             log(f"  {r['kernel']:10s} {r['us']:8.2f} us  {r['GBs']:8.1f} GB/s  x{r['launches_per_token']} = {r['us_per_token']:7.1f} us/token")
         wbytes = A.lib().l3m_weight_bytes(m._handle())
         m.close()
-        dom = max(kt, key=lambda r: r["us_per_token"])
+        dom = decode or max(kt, key=lambda r: r["us_per_token"])
         cpu = cpu_baseline(path, prompt, a.cpu_seconds) if a.cpu_seconds > 0 else None
         if cpu:
             log(f"bench: reference CPU {cpu['value']} tok/s on {cpu['cores']} cores")
@@ -200,8 +233,10 @@ def main():
                    "ffn": cfg.ffn_dim, "vocab": cfg.vocab, "ctx": cfg.ctx, "weights": "random-init N(0,0.02), seed 1"},
         "roofline": {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4),
-                     "traffic": measured_traffic(cfg.name, dtype, dom["kernel"]),
-                     "bytes_per_launch": dom["bytes"], "us_per_launch": round(dom["us"], 3)},
+                     "traffic": measured_traffic(cfg.name, dtype, dom["kernel"],
+                                                 dom["steps"] / dom["launches"] if "launches" in dom else None),
+                     "bytes_per_launch": round(dom["bytes"]), "us_per_launch": round(dom["us"], 3),
+                     **({"launches": dom["launches"], "steps": dom["steps"]} if "launches" in dom else {})},
         "step_kernels": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in kt],
         "weight_bytes_per_token": wbytes,
         "weight_GBs_per_token": round(wbytes * value * 1e-9, 1) if wbytes else None,

@@ -124,6 +124,13 @@ double l3m_bench_decode(l3m_model *m, const int32_t *prompt, int n_prompt, int n
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);
 // One kernel of the decode step at position pos: kind 0 attention block, 1 FFN block, 2 head.
 double l3m_bench_kernel(l3m_model *m, int kind, int layer, int pos, int iters);
+// Timing of the persistent decode kernel's launches (hipEvents on the library stream around each launch):
+// mode 1 clears and starts, 2 adds the last finished launch (the library calls it after each), 0 stops;
+// every call reports the total microseconds and launches so far.
+int    l3m_decode_timer(int mode, double *us, int *launches);
+// What the persistent launches of m have processed so far: out[0] steps, out[1] steps with the head,
+// out[2] K/V rows read per kv head and layer (sum of pos + 1).
+void   l3m_decode_work(const l3m_model *m, double *out);
 double l3m_kernel_bytes(const l3m_model *m, int kind, int pos);   // weight bytes one launch of that kernel reads
 double l3m_weight_bytes(const l3m_model *m);                       // weight bytes streamed per token
 // 1 when decode runs as one persistent cooperative kernel per chunk of steps (L3M_PERSIST=0 at load

@@ -1755,6 +1755,11 @@ template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t
 }
 // The persistent kernel needs every workgroup resident at once: a cooperative launch, which the runtime
 // refuses (instead of starting it) when the grid does not fit.
+// Optional timing of the decode launches: hipEvents around each launch on its stream, collected after
+// the host has waited for it (l3m_decode_timer).
+hipEvent_t g_dec_ev[2];
+int g_dec_timing, g_dec_launches, g_dec_pending;
+double g_dec_us;
 template <int DT> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *layers, const l3m_run *R_dev, int grid, unsigned lds,
                                     hipStream_t st) {
     lds_opt_in(k_decode<DT>, lds);
@@ -1762,8 +1767,14 @@ template <int DT> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *l
     const l3m_dlayer *ly = layers;
     const l3m_run *r = R_dev;
     void *args[] = {&m, &ly, &r};
+    if (g_dec_timing) CK(hipEventRecord(g_dec_ev[0], st));
     const hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode<DT>, dim3(grid), dim3(NTE), args, lds, st);
-    return e == hipSuccess ? 0 : fail("decode launch", e);
+    if (e != hipSuccess) return fail("decode launch", e);
+    if (g_dec_timing) {
+        CK(hipEventRecord(g_dec_ev[1], st));
+        g_dec_pending = 1;
+    }
+    return 0;
 }
 template <int DT> int decode_fits(int grid, unsigned lds) {
     lds_opt_in(k_decode<DT>, lds);
@@ -1966,6 +1977,31 @@ int l3m_decode_fits(int dtype, int grid, unsigned lds) {
     case L3M_Q4_0: return decode_fits<L3M_Q4_0>(grid, lds);
     case L3M_MXFP4: return decode_fits<L3M_MXFP4>(grid, lds);
     }
+    return 0;
+}
+
+int l3m_decode_timer(int mode, double *us, int *launches) {
+    if (l3m_dev_init()) return -1;
+    if (!g_dec_ev[0]) {
+        CK(hipEventCreate(&g_dec_ev[0]));
+        CK(hipEventCreate(&g_dec_ev[1]));
+    }
+    if (mode == 1) {                                   // start: clear and time from now on
+        g_dec_timing = 1; g_dec_us = 0; g_dec_launches = 0; g_dec_pending = 0;
+    } else if (mode == 2) {                            // collect the last launch (its stream has been waited for)
+        if (g_dec_pending) {
+            float ms = 0.f;
+            CK(hipEventSynchronize(g_dec_ev[1]));
+            CK(hipEventElapsedTime(&ms, g_dec_ev[0], g_dec_ev[1]));
+            g_dec_us += 1000.0 * ms;
+            g_dec_launches++;
+            g_dec_pending = 0;
+        }
+    } else {                                           // stop
+        g_dec_timing = 0;
+    }
+    if (us) *us = g_dec_us;
+    if (launches) *launches = g_dec_launches;
     return 0;
 }
 
