@@ -651,18 +651,31 @@ struct Red {
     float *scr;    // 32 floats of LDS
     int k;
 };
-// (value, index) maximum with the reference's tie rule (better()); sv, si: 16 words each.
-__device__ void wge_argmax(float &v, int &i, float *sv, int *si) {
-    for (int o = 32; o; o >>= 1) {
-        const float v2 = __shfl_xor(v, o);
-        const int i2 = __shfl_xor(i, o);
-        better(v, i, v2, i2);
-    }
+template <int N> __device__ __forceinline__ int lanes_mini(int v) {
+    if constexpr (N >= 2) v = min(v, dppi<QP_X1>(v));
+    if constexpr (N >= 4) v = min(v, dppi<QP_X2>(v));
+    if constexpr (N >= 8) v = min(v, dppi<ROW_HALF_MIRROR>(v));
+    if constexpr (N >= 16) v = min(v, dppi<ROW_MIRROR>(v));
+    if constexpr (N >= 32) { float lo, hi; swap16(__int_as_float(v), lo, hi); v = min(__float_as_int(lo), __float_as_int(hi)); }
+    if constexpr (N >= 64) { float lo, hi; swap32(__int_as_float(v), lo, hi); v = min(__float_as_int(lo), __float_as_int(hi)); }
+    return v;
+}
+// (value, index) maximum with the reference's tie rule (better(): the larger value, then the lower index;
+// a NaN never wins) into every thread: a wavefront's largest value (fmaxf passes NaN over), then the
+// lowest index that holds it; then the same over the wavefronts' results, which every wavefront reads
+// after one barrier. sv, si: NWE words each, not read again before a later barrier.
+__device__ void block_argmax(float &v, int &i, float *sv, int *si) {
+    float m = lanes_max<64>(v);
+    int ci = lanes_mini<64>(v == m ? i : 0x7FFFFFFF);
+    if ((tidx() & 63) == 0) { sv[wave_id()] = m; si[wave_id()] = ci; }
     __syncthreads();
-    if ((tidx() & 63) == 0) { sv[tidx() >> 6] = v; si[tidx() >> 6] = i; }
-    __syncthreads();
-    v = sv[0]; i = si[0];
-    for (int w = 1; w < NWE; w++) better(v, i, sv[w], si[w]);
+    const int k = tidx() & (NWE - 1);                 // each aligned group of NWE lanes holds every result
+    const float vk = sv[k];
+    const int ik = si[k];
+    m = lanes_max<NWE>(vk);
+    ci = lanes_mini<NWE>(vk == m ? ik : 0x7FFFFFFF);
+    v = m;
+    i = ci;
 }
 
 // Matvec results res[pair * 16 + row] summed per row: four quarter sums of the blocks, each in block
@@ -958,13 +971,12 @@ __device__ __forceinline__ LdsB lds_of(const l3m_dchunk &C) {
     L.act = C.lds[0]; L.work = C.lds[1]; L.gu = C.lds[2]; L.act2 = C.lds[3]; L.scr = C.lds[4]; L.total = 0;
     return L;
 }
-struct LdsH { size_t act, work, y, scr, total; };
+struct LdsH { size_t act, work, scr, total; };
 __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg) {
     LdsH L;
     size_t o = 0;
     L.act = o;  o += align16(act_size(dt, dim));
     L.work = o; o += work_bytes(res_bytes((size_t)tiles_per_wg * nb), 0);
-    L.y = o;    o += align16(64 * (size_t)tiles_per_wg);
     L.scr = o;  o += 4 * 64;
     L.total = o;
     return L;
@@ -1278,7 +1290,7 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
                                            uint8_t *smem, float &v, int &idx) {
     const int tid = tidx(), dim = M.dim, kp = kpad(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
-    float *work = (float *)(smem + L.work), *y = (float *)(smem + L.y), *scr = (float *)(smem + L.scr);
+    float *work = (float *)(smem + L.work), *scr = (float *)(smem + L.scr);
     uint8_t *act = smem + L.act;
     Red red{scr, 0};
 
@@ -1300,13 +1312,14 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
     norm_prep<DT>(x, nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work);
     __syncthreads();
-    rows_sum4(V, work, V.rows, [&](int i, float yy, float, bool lead) { if (lead) y[i] = yy; });
-    __syncthreads();
+    // each row's logit from the lane that sums it: stored, and kept if it beats the lane's earlier rows
     float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab + (size_t)t0 * 16;
     v = -INFINITY;
     idx = 0x7FFFFFFF;
-    if (tid < V.rows) { gw(lg)[tid] = y[tid]; v = y[tid]; idx = t0 * 16 + tid; }
-    wge_argmax(v, idx, scr, (int *)scr + 16);
+    rows_sum4(V, work, V.rows, [&](int i, float yy, float, bool lead) {
+        if (lead) { gw(lg)[i] = yy; better(v, idx, yy, t0 * 16 + i); }
+    });
+    block_argmax(v, idx, scr, (int *)scr + 16);
 }
 
 // The argmax over n (value, index) partials, in index order (engine.c:294-300), into every thread.
@@ -1318,7 +1331,7 @@ __device__ void reduce_partials(const float *val, const int *idx_in, int n, floa
         const int pi = __hip_atomic_load(gp<int>(idx_in + w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         better(v, idx, pv, pi);
     }
-    wge_argmax(v, idx, scr, (int *)scr + 16);
+    block_argmax(v, idx, scr, (int *)scr + 16);
 }
 
 // ------------------------------------------------------------------ the graph path: one kernel per block
@@ -1467,6 +1480,21 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int idx, unsigned tag) {
 }
 __device__ __forceinline__ unsigned step_tag(int s) { return (unsigned)(s % 32767) + 1; }
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// The maximum over the wavefront's 64 lanes, into every lane (DPP and permlane moves of both halves).
+__device__ __forceinline__ uint64_t lanes_max_u64(uint64_t v) {
+    auto hi = [](uint64_t x) { return (int)(uint32_t)(x >> 32); };
+    auto lo = [](uint64_t x) { return (int)(uint32_t)x; };
+    auto join = [](int h, int l) { return (uint64_t)(uint32_t)h << 32 | (uint32_t)l; };
+    v = max_u64(v, join(dppi<QP_X1>(hi(v)), dppi<QP_X1>(lo(v))));
+    v = max_u64(v, join(dppi<QP_X2>(hi(v)), dppi<QP_X2>(lo(v))));
+    v = max_u64(v, join(dppi<ROW_HALF_MIRROR>(hi(v)), dppi<ROW_HALF_MIRROR>(lo(v))));
+    v = max_u64(v, join(dppi<ROW_MIRROR>(hi(v)), dppi<ROW_MIRROR>(lo(v))));
+    float h0, h1, l0, l1;
+    swap16(__int_as_float(hi(v)), h0, h1); swap16(__int_as_float(lo(v)), l0, l1);
+    v = max_u64(join(__float_as_int(h0), __float_as_int(l0)), join(__float_as_int(h1), __float_as_int(l1)));
+    swap32(__int_as_float(hi(v)), h0, h1); swap32(__int_as_float(lo(v)), l0, l1);
+    return max_u64(join(__float_as_int(h0), __float_as_int(l0)), join(__float_as_int(h1), __float_as_int(l1)));
+}
 
 // The token chosen by step s's head: wavefront 0 polls the n_head keys until all carry the step's tag and
 // reduces them. Returns the token, or -1 when the run is being abandoned.
@@ -1494,12 +1522,7 @@ __device__ int wait_token(const uint64_t *slots, int n_head, int s, unsigned *ab
             __builtin_amdgcn_s_sleep(1);
         }
         if (best != ~0ull) {
-#pragma unroll
-            for (int m = 1; m < 64; m <<= 1) {
-                const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(best >> 32), m);
-                const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, m);
-                best = max_u64(best, (uint64_t)hi << 32 | lo);
-            }
+            best = lanes_max_u64(best);
             tok = (best >> 17) == 0 ? 0 : 0x1FFFF - (int)(best & 0x1FFFF);
         }
         if (tid == 0) *lds = tok;
