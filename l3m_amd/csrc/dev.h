@@ -113,6 +113,7 @@ unsigned l3m_dev_lds_max(void);       // dynamic LDS one workgroup may use on th
 unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c);
 unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg);
 int      l3m_step_slots(int dtype, int which);   // weight slots per lane (matrix A / B of a step kernel), 64 pairs each
+int      l3m_step_a_dtype(int dtype);            // storage dtype of a step kernel's matrix A for a body of dtype
 int l3m_step_enqueue(const l3m_dmodel *m, const l3m_dlayer *layers, int with_head, void *stream);
 
 // The persistent decode kernel (one cooperative launch for R->nsteps steps; layers_dev in device memory).

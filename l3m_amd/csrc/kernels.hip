@@ -1144,16 +1144,21 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
 // already (the persistent path issues them while it waits for the block's inputs); otherwise they are
 // issued right after the prologue's loads.
 
-template <int DT> struct AttnW { Pref<DT, nslot_a<DT>()> a; Pref<DT, nslot_wo<DT>()> b; };
-template <int DT> struct FfnW { Pref<DT, nslot_a<DT>()> a; Pref<DT, nslot_b<DT>()> b; };
+// The storage dtype of a step block's first matrix (q/k/v rows, gate/up rows) for a body of dtype DT. A
+// q4_0 body holds them as q8_0: the same blocks with each nibble q widened to the byte q - 8 and the same
+// scale, so every integer dot and every float operation is the one q4_0 would do, while the slot loop
+// skips the nibble unpacking. The second matrices (Wo, Wdown columns) and the head stay q4_0.
+template <int DT> constexpr int a_dtype() { return DT == L3M_Q4_0 ? L3M_Q8_0 : DT; }
+template <int DT> struct AttnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<DT, nslot_wo<DT>()> b; };
+template <int DT> struct FfnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<DT, nslot_b<DT>()> b; };
 template <int DT> struct HeadW { Pref<DT, nslot_a<DT>() + nslot_b<DT>()> a; };
 
 template <int DT> __device__ __forceinline__ void attn_issue(AttnW<DT> &w, const l3m_dgroup &G) {
-    pref_load<DT, nslot_a<DT>()>(w.a, G.qkv, 0);
+    pref_load<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, 0);
     pref_load<DT, nslot_wo<DT>()>(w.b, G.wo, 0);
 }
 template <int DT> __device__ __forceinline__ void ffn_issue(FfnW<DT> &w, const l3m_dchunk &C) {
-    pref_load<DT, nslot_a<DT>()>(w.a, C.gate_up, 0);
+    pref_load<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, 0);
     pref_load<DT, nslot_b<DT>()>(w.b, C.down, 0);
 }
 template <int DT> __device__ __forceinline__ void head_issue(HeadW<DT> &w, const l3m_dmat &V) {
@@ -1194,7 +1199,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     if (!PRE && M.kv_lds) kv_window_dma<false>(kvb, M, layer, G.kv0, G.nkv, pos);
     norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
 
-    mv<DT, nslot_a<DT>()>(w.a, G.qkv, act, kp, work);
+    mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, act, kp, work);
     __syncthreads();
     // q, k rows: RoPE on pairs (2i, 2i+1) of each head by the angle i (ops.c:29-40); k, v rows rounded
     // to bf16 as the cache holds them (engine.c:247-248), into cur and (for the heads this group writes)
@@ -1249,7 +1254,7 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     if constexpr (!PRE) ffn_issue<DT>(w, C);
     const float4 x = pro_finish<PRE>(P, M.po, PG, false, (float4 *)work, ci == 0 ? M.xb : nullptr, nullptr, 0);
     norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
-    mv<DT, nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
+    mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
     __syncthreads();
     rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float, bool lead) { if (lead) gu[i] = y; });
     __syncthreads();
@@ -1401,10 +1406,13 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
 // step s, FFN chunk c sets ffn[c] likewise. A layer's blocks wait for all flags of the block before them.
 //
 // Hand-over to and from the head (other XCDs, so through memory): after the last layer of a step with
-// logits, attention group g sums its slice of the final residual into xf with write-through stores and
-// sets xf_flag[g] = s + 1; head workgroups wait for all of them, compute their tiles' logits and argmax,
-// and store one 64-bit key per workgroup (the step's tag, the value in an order-preserving code, the
-// index); the attention groups of the next step wait for every key with that tag and take the maximum.
+// logits, FFN chunk c waits for every chunk's partial, sums its slice of the final residual into xf with
+// write-through stores and sets xf_flag[c] = s + 1; head workgroups wait for all of them, compute their
+// tiles' logits and argmax, and store one 64-bit key per workgroup (the step's tag, the value in an
+// order-preserving code, the index); the attention groups of the next step wait for every key with that
+// tag and take the maximum. The chunks do the final sum so that the attention groups are free after
+// their last block: they issue the next step's first weights while the head runs, and those loads are
+// complete by the time they poll for the token (a wavefront's loads return in order).
 //
 // Every wait is bounded: past R.spin_limit ticks of the 100 MHz clock the waiter raises the abort flag
 // and every workgroup leaves at its next wait, so the grid always drains.
@@ -1565,14 +1573,14 @@ template <class T> __device__ __forceinline__ const T *per_iteration(const T *p)
 }
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// Attention group g's share of the final residual (the head's input): x = xb + the last layer's FFN
-// partials, in pro_finish's order of additions, for float4 elements [g * per, (g + 1) * per), stored
-// through to memory for the head workgroups.
-__device__ __noinline__ void reduce_final(const l3m_dmodel *Mp, int g) {
-    g = uniform(g);
+// FFN chunk c's share of the final residual (the head's input): x = xb + the last layer's FFN partials,
+// in pro_finish's order of additions, for float4 elements [c * per, (c + 1) * per), stored through to
+// memory for the head workgroups.
+__device__ __noinline__ void reduce_final(const l3m_dmodel *Mp, int c) {
+    c = uniform(c);
     const l3m_dmodel M = fixed(Mp);
-    const int n4 = M.dim >> 2, per = (n4 + M.n_groups - 1) / M.n_groups;
-    const int f = g * per + tidx();
+    const int n4 = M.dim >> 2, per = (n4 + M.n_chunks - 1) / M.n_chunks;
+    const int f = c * per + tidx();
     if (tidx() < per && f < n4) stcoh16(M.xf, f, parts_sum_at(M.xb, M.pd, pro_geom(M, 0), f));
 }
 
@@ -1609,14 +1617,6 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
         attn_block<DT, true>(M, Lw, G, l, pos, tok, g, wt, smem);
         set_flag<false>(sync + SY_ATTN + g, epoch + 1);
     }
-    const l3m_run R = fixed(per_iteration(Rp));
-    if (R.pos0 + s >= R.head_from) {
-        unsigned *sync = R.sync;
-        if (!wait_flags<1>(sync + SY_FFN, fixed(Mp).n_chunks, (unsigned)((s + 1) * nl), sync + SY_ABORT, R.spin_limit, &ok_lds))
-            return false;
-        reduce_final(Mp, g);
-        set_flag<true>(sync + SY_XF + g, (unsigned)s + 1);
-    }
     return true;
 }
 
@@ -1639,6 +1639,14 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
         ffn_block<DT, true>(M, Lw, C, ci, wt, smem);
         set_flag<false>(sync + SY_FFN + ci, epoch + 1);
     }
+    const l3m_run R = fixed(per_iteration(Rp));
+    if (R.pos0 + s >= R.head_from) {
+        unsigned *sync = R.sync;
+        if (!wait_flags<1>(sync + SY_FFN, fixed(Mp).n_chunks, (unsigned)((s + 1) * nl), sync + SY_ABORT, R.spin_limit, &ok_lds))
+            return false;
+        reduce_final(Mp, ci);
+        set_flag<true>(sync + SY_XF + ci, (unsigned)s + 1);
+    }
     return true;
 }
 
@@ -1657,7 +1665,7 @@ __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, 
     const l3m_dmat V = head_slice(M, has_tiles ? t0 : 0, R.head_tpw);
     HeadW<DT> wt;
     if (has_tiles) head_issue<DT>(wt, V);
-    if (!wait_flags<4>(R.sync + SY_XF, M.n_groups, (unsigned)s + 1, R.sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
+    if (!wait_flags<4>(R.sync + SY_XF, M.n_chunks, (unsigned)s + 1, R.sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
     if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx);
     if (tidx() == 0)
         __hip_atomic_store(gw((uint64_t *)(R.sync + SY_SLOTS) + h), argmax_key(v, idx, step_tag(s)), __ATOMIC_RELAXED,
@@ -1969,6 +1977,9 @@ void l3m_model_layout(l3m_dmodel *m) {
 }
 unsigned l3m_lds_ffn(int dtype, int dim, const l3m_dchunk *c) { return (unsigned)lds_b(dtype, dim, *c).total; }
 unsigned l3m_lds_head(int dtype, int dim, int nb, int tiles_per_wg) { return (unsigned)lds_h(dtype, dim, nb, tiles_per_wg).total; }
+int l3m_step_a_dtype(int dtype) {
+    return dtype == L3M_Q4_0 ? a_dtype<L3M_Q4_0>() : dtype;
+}
 int l3m_step_slots(int dtype, int which) {
     if (which) return dtype == L3M_F32 ? nslot_b<L3M_F32>() : dtype == L3M_BF16 ? nslot_b<L3M_BF16>() : dtype == L3M_Q8_0 ? nslot_b<L3M_Q8_0>() : nslot_b<L3M_Q4_0>();
     return dtype == L3M_F32 ? nslot_a<L3M_F32>() : dtype == L3M_BF16 ? nslot_a<L3M_BF16>() : dtype == L3M_Q8_0 ? nslot_a<L3M_Q8_0>() : nslot_a<L3M_Q4_0>();
