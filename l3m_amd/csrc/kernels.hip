@@ -509,7 +509,7 @@ __device__ __forceinline__ int tidx() {
 template <int DT> constexpr int nslot_a() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 5 : 6; }
 template <int DT> constexpr int nslot_b() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 1 : 3; }
 // The attention block keeps its Wo slots live through the attention; q8_0 gives one up to stay in registers.
-template <int DT> constexpr int nslot_wo() { return DT == L3M_Q8_0 ? 2 : nslot_b<DT>(); }
+template <int DT> constexpr int nslot_wo() { return DT == L3M_Q8_0 || DT == L3M_Q4_0 ? 2 : nslot_b<DT>(); }
 
 template <int DT, int NS>
 struct Pref {
@@ -1144,22 +1144,22 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
 // already (the persistent path issues them while it waits for the block's inputs); otherwise they are
 // issued right after the prologue's loads.
 
-// The storage dtype of a step block's first matrix (q/k/v rows, gate/up rows) for a body of dtype DT. A
-// q4_0 body holds them as q8_0: the same blocks with each nibble q widened to the byte q - 8 and the same
-// scale, so every integer dot and every float operation is the one q4_0 would do, while the slot loop
-// skips the nibble unpacking. The second matrices (Wo, Wdown columns) and the head stay q4_0.
+// The storage dtype of the step blocks' matrices (q/k/v rows, Wo columns, gate/up rows, Wdown columns)
+// for a body of dtype DT. A q4_0 body holds them as q8_0: the same blocks with each nibble q widened to
+// the byte q - 8 and the same scale, so every integer dot and every float operation is the one q4_0 would
+// do, while the slot loop skips the nibble unpacking. The head stays q4_0.
 template <int DT> constexpr int a_dtype() { return DT == L3M_Q4_0 ? L3M_Q8_0 : DT; }
-template <int DT> struct AttnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<DT, nslot_wo<DT>()> b; };
-template <int DT> struct FfnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<DT, nslot_b<DT>()> b; };
+template <int DT> struct AttnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_wo<DT>()> b; };
+template <int DT> struct FfnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_b<DT>()> b; };
 template <int DT> struct HeadW { Pref<DT, nslot_a<DT>() + nslot_b<DT>()> a; };
 
 template <int DT> __device__ __forceinline__ void attn_issue(AttnW<DT> &w, const l3m_dgroup &G) {
     pref_load<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, 0);
-    pref_load<DT, nslot_wo<DT>()>(w.b, G.wo, 0);
+    pref_load<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, 0);
 }
 template <int DT> __device__ __forceinline__ void ffn_issue(FfnW<DT> &w, const l3m_dchunk &C) {
     pref_load<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, 0);
-    pref_load<DT, nslot_b<DT>()>(w.b, C.down, 0);
+    pref_load<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, 0);
 }
 template <int DT> __device__ __forceinline__ void head_issue(HeadW<DT> &w, const l3m_dmat &V) {
     pref_load<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, 0);
@@ -1231,7 +1231,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
     const int kq = kpad(nqd);
     prep_owned<DT>(4 * tid < nqd ? ((const float4 *)att)[tid] : make_float4(0.f, 0.f, 0.f, 0.f), act2, kq);
-    mv<DT, nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
+    mv<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
     __syncthreads();
     float *po = M.po + (size_t)gi * dim;
     rows_sum4(G.wo, work, dim, [&](int i, float y, float, bool lead) { if (lead) gw(po)[i] = y; });
@@ -1271,7 +1271,7 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
         hv = make_float4(hh[0], hh[1], hh[2], hh[3]);
     }
     prep_owned<DT>(hv, act2, kf);
-    mv<DT, nslot_b<DT>()>(w.b, C.down, act2, kf, work);
+    mv<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, act2, kf, work);
     __syncthreads();
     float *pd = M.pd + (size_t)ci * dim;
     rows_sum4(C.down, work, dim, [&](int i, float y, float, bool lead) { if (lead) gw(pd)[i] = y; });
