@@ -39,6 +39,7 @@ template <class T> __device__ __forceinline__ const GLOBAL T *gp(const void *p) 
 // next barrier would wait for it to reach memory.
 template <class T> __device__ __forceinline__ GLOBAL T *gw(T *p) { return (GLOBAL T *)p; }
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 ldg16(const void *p, size_t i) {
@@ -766,17 +767,27 @@ __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float 
     const int tid = tidx(), nparts = G.nparts, dim = 4 * G.n4;
     int f, grp;
     split_tid(tid, G.n4, grp, f);
-    const int j0 = grp * G.per, own = tid < G.n4 ? tid : G.n4 - 1;
-    P.nw = ldg16f(nw, own);
-    P.base = ld16f<COH>(base, f);
+    const int j0 = grp * G.per, own = tid < G.n4 ? tid : G.n4 - 1, wave = wave_id();
+    // Each wavefront issues only the loads its threads use (wave-uniform branches: a memory instruction
+    // costs address-unit time whether or not its lanes are needed). Owners (group 0) take the norm
+    // weights, the base and, at layer 0, the embedding row; grouped threads their parts.
+    if (wave * 64 < G.n4) {
+        P.nw = ldg16f(nw, own);
+        P.base = ld16f<COH>(base, f);
+    }
+    if (wave * 64 < G.groups * G.n4) {
 #pragma unroll
-    for (int j = 0; j < FILL_PER; j++) {
-        const int pj = j0 + j < nparts ? j0 + j : nparts - 1;
-        P.p[j] = ld16f<COH>(parts, (size_t)pj * (dim >> 2) + f);
+        for (int j = 0; j < FILL_PER; j++) {
+            if (j < G.per) {
+                const int pj = j0 + j < nparts ? j0 + j : nparts - 1;
+                P.p[j] = ld16f<COH>(parts, (size_t)pj * (dim >> 2) + f);
+            }
+        }
     }
     if (rope_row) {
         const int i = tid < (hd >> 1) ? tid : (hd >> 1) - 1;
-        P.cs = make_float2(gp<float>(rope_row)[2 * i], gp<float>(rope_row)[2 * i + 1]);
+        const u32x2 c = gp<u32x2>(rope_row)[i];
+        P.cs = make_float2(__uint_as_float(c.x), __uint_as_float(c.y));
     }
     if (use_embed) P.emb = lt_elem4(embed, tok, 4 * own);   // layer 0: x = dequant(embed[tok]) (engine.c:236)
     asm volatile("" ::: "memory");                            // these loads are issued before the weights
