@@ -939,6 +939,10 @@ __host__ __device__ inline size_t work_bytes(size_t a, size_t b) {
     return align16(w > 16 * (size_t)NTE ? w : 16 * (size_t)NTE);
 }
 
+// Row stride (bf16 elements) of the LDS K/V window: hd + 8 keeps rows 16-byte aligned and puts 16
+// consecutive rows' same 16 bytes on 16 different 4-bank groups, so reads down a column (the MFMA
+// operand layout) are free of bank conflicts.
+__host__ __device__ inline int kv_row(int hd) { return hd + 8; }
 struct LdsA { size_t act, work, q, cur, cs, vred, att, act2, scr, kvb, total; };
 __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g, int kv_lds) {
     LdsA L;
@@ -953,7 +957,7 @@ __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3
     L.att = o;  o += align16(4 * (size_t)kpad(g.nq * hd));
     L.act2 = o; o += align16(act_size(dt, g.nq * hd));
     L.scr = o;  o += 4 * 64;
-    L.kvb = o;  o += kv_lds ? align16(4 * (size_t)g.nkv * ctx * hd) : 0;   // [K | V][nkv][ctx][hd] bf16
+    L.kvb = o;  o += kv_lds ? align16(4 * (size_t)g.nkv * ctx * kv_row(hd)) : 0;   // [K | V][nkv][ctx][kv_row] bf16
     L.total = o;
     return L;
 }
@@ -998,17 +1002,19 @@ __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg)
 // Rows up to pos - 1 were written by earlier steps, so the copy can start at the top of the kernel.
 template <bool COH>
 __device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int kv0, int nkv, int pos) {
-    const int wave = wave_id(), lane = tidx() & 63;
-    const size_t win = (size_t)M.ctx * M.hd, total = (size_t)pos * M.hd * 2;     // bytes per head, K or V
-    const int nch = (int)((total + 1023) / 1024), items = 2 * nkv * nch;
-    for (int it = wave; it < items; it += NWE) {
-        const int which = it / (nkv * nch), rem = it % (nkv * nch), j = rem / nch, c = rem % nch;
-        const size_t byte = (size_t)c * 1024 + (size_t)lane * 16;
-        const uint16_t *src = (which ? M.vc : M.kc) + ((size_t)layer * M.n_kv + kv0 + j) * win;
-        uint8_t *dst = (uint8_t *)(kvb + ((size_t)which * nkv + j) * win) + (size_t)c * 1024;
-        if (byte < total)
-            __builtin_amdgcn_global_load_lds((const GLOBAL void *)((const uint8_t *)src + byte),
-                                             (__attribute__((address_space(3))) void *)dst, 16, 0, COH ? 16 : 0);   // 16: sc1
+    const int wave = wave_id(), lane = tidx() & 63, hd = M.hd, rs = kv_row(hd);
+    const size_t cwin = (size_t)M.ctx * hd, lwin = (size_t)M.ctx * rs;      // per head: cache, LDS window
+    // one row per instruction (the window's rows are padded apart, so a copy cannot span rows): hd / 8
+    // lanes of 16 bytes each
+    for (int head = 0; head < 2 * nkv; head++) {
+        const int which = head >= nkv ? 1 : 0, j = head - which * nkv;
+        const uint16_t *src = (which ? M.vc : M.kc) + ((size_t)layer * M.n_kv + kv0 + j) * cwin;
+        uint16_t *dst = kvb + (size_t)head * lwin;
+        for (int t = wave; t < pos; t += NWE)
+            if (lane < (hd >> 3))
+                __builtin_amdgcn_global_load_lds((const GLOBAL void *)(src + (size_t)t * hd + 8 * lane),
+                                                 (__attribute__((address_space(3))) void *)(dst + (size_t)t * rs), 16, 0,
+                                                 COH ? 16 : 0);   // 16: sc1
     }
 }
 
@@ -1039,7 +1045,8 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
     const int hd = M.hd, nv = hd >> 3, lg = nv <= 4 ? 2 : nv <= 8 ? 3 : nv <= 16 ? 4 : 5, LP = 1 << lg, PPW = 64 >> lg;
     const int lane = tidx() & 63, wave = wave_id(), j = lane & (LP - 1), gl = lane >> lg, n = pos + 1;
     const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
-    const size_t win = (size_t)M.ctx * hd;
+    const int rs = WIN ? kv_row(hd) : hd;             // row stride: LDS window or cache
+    const size_t win = (size_t)M.ctx * rs;
     // W = 2^wl wavefronts per head: the fewest that keep each at ATT_IT rounds or less, at most 2^att_wl
     const int sh = ATT_LOG_IT + 6 - lg;               // ATT_IT * PPW = 2^sh positions per wavefront
     const int need = (n + (1 << sh) - 1) >> sh;
@@ -1074,7 +1081,7 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
                     if (t < n && j < nv) {
                         uint4 kk;
                         if (t == pos) kk = kcur[j];
-                        else if (WIN) kk = ((const uint4 *)(kw + (size_t)t * hd))[j];
+                        else if (WIN) kk = ((const uint4 *)(kw + (size_t)t * rs))[j];
                         else kk = ld16<COH>(kw, (size_t)t * (hd >> 3) + j);
                         part = dot8_bf16(q, kk, 0.f);
                     }
@@ -1095,7 +1102,7 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
                         if (j < nv) {
                             uint4 vv;
                             if (t == pos) vv = vcur[j];
-                            else if (WIN) vv = ((const uint4 *)(vw + (size_t)t * hd))[j];
+                            else if (WIN) vv = ((const uint4 *)(vw + (size_t)t * rs))[j];
                             else vv = ld16<COH>(vw, (size_t)t * (hd >> 3) + j);
                             o[0] = fmaf(p, bf16_f32(vv.x & 0xFFFF), o[0]); o[1] = fmaf(p, bf16_f32(vv.x >> 16), o[1]);
                             o[2] = fmaf(p, bf16_f32(vv.y & 0xFFFF), o[2]); o[3] = fmaf(p, bf16_f32(vv.y >> 16), o[3]);
@@ -1143,6 +1150,117 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
                     att[h * hd + d] = num / den;
                 }
             }
+        }
+        __syncthreads();
+    }
+}
+
+// bf16 vectors for the gfx950 MFMA v_mfma_f32_16x16x32_bf16: A is 16 x 32, B 32 x 16, C 16 x 16 f32.
+// Lane l supplies A[l % 16][8 (l / 16) + e] and B[8 (l / 16) + e][l % 16] (e = 0..7) and holds
+// C[4 (l / 16) + r][l % 16] (r = 0..3).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// x as the sum of three bf16 (each rounded to nearest even from what is left): exact to 2^-24 of x, so
+// three bf16 products with an exact bf16 operand give x * y to f32 accuracy.
+__device__ __forceinline__ void split3(float x, __bf16 &h, __bf16 &m, __bf16 &l) {
+    h = (__bf16)x;
+    const float r = x - (float)h;
+    m = (__bf16)r;
+    l = (__bf16)(r - (float)m);
+}
+
+// Attention of the group's query heads over positions 0..pos (ops.c:58-73) on the matrix cores, for a
+// head dimension that is a multiple of 32, with every K, V row in the LDS window (row stride kv_row(hd),
+// row pos included: the block stores this step's rows there first). One head at a time, three passes
+// with a barrier after each:
+//  1. scores: wavefront w takes 16-position tiles w, w + NWE, ...: S = K_tile (16 x hd, from the window
+//     as it lies) times q (in every column of B), q split into three bf16 parts so the products are f32
+//     exact; s_t = S / sqrt(hd) into sc, and each wavefront's maximum into smax;
+//  2. p_t = exp(s_t - m) over the head's maximum m, stored as three bf16 parts (zero past pos, up to a
+//     multiple of 32), and each wavefront's sum of p into lpart;
+//  3. o = P V: wavefront w takes dims [16w, 16w + 16): 32 positions per step, A = the p parts (every row
+//     the same), B = V rows 32 at a time; att = o / sum(lpart).
+// sc: 10 * ceil32(ctx) bytes of LDS; vred: at least 2 * NWE floats. Ends with a barrier.
+__device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, const float *qh, const uint16_t *kvb, float *sc,
+                            float *vred, float *att) {
+    const int hd = M.hd, rs = kv_row(hd), ctx = M.ctx, n = pos + 1;
+    const int lane = tidx() & 63, wave = wave_id(), li = lane & 15, lg = lane >> 4;
+    const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
+    const size_t win = (size_t)ctx * rs;
+    const int tiles = (n + 15) >> 4, steps = (n + 31) >> 5, cap = (ctx + 31) & ~31;
+    float *s_arr = sc, *smax = vred, *lpart = vred + NWE;
+    __bf16 *pp = (__bf16 *)(sc + cap);                // [3][cap]
+    for (int h = 0; h < G.nq; h++) {
+        // (q0 + h) / hpk by an exact float reciprocal (both far below 2^20)
+        const int kvl = (int)(((float)(G.q0 + h) + 0.5f) * ihpk) - G.kv0;
+        const uint16_t *kw = kvb + (size_t)kvl * win, *vw = kvb + (size_t)(G.nkv + kvl) * win;
+        float mx = -INFINITY;
+        for (int T = wave; T < tiles; T += NWE) {
+            const int row = T * 16 + li < n ? T * 16 + li : n - 1;
+            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+            for (int kk = 0; kk < hd; kk += 32) {
+                const bf16x8 a = *(const bf16x8 *)(kw + (size_t)row * rs + kk + 8 * lg);
+                const float4 q0 = *(const float4 *)(qh + h * hd + kk + 8 * lg), q1 = *(const float4 *)(qh + h * hd + kk + 8 * lg + 4);
+                const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                bf16x8 b0, b1, b2;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    __bf16 x, y, z;
+                    split3(qv[e], x, y, z);
+                    b0[e] = x; b1[e] = y; b2[e] = z;
+                }
+                c = mfma_bf16(a, b0, c);
+                c = mfma_bf16(a, b1, c);
+                c = mfma_bf16(a, b2, c);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = T * 16 + 4 * lg + r;
+                const float sv = c[r] * scale;
+                if (li == 0) s_arr[t] = t < n ? sv : -INFINITY;
+                mx = fmaxf(mx, t < n ? sv : -INFINITY);
+            }
+        }
+        {
+            float lo, hi;
+            swap16(mx, lo, hi); mx = fmaxf(lo, hi);
+            swap32(mx, lo, hi); mx = fmaxf(lo, hi);
+        }
+        if (lane == 0) smax[wave] = mx;
+        __syncthreads();
+        const float m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(lanes_max<16>(smax[li]))));
+        float lw = 0.f;
+        for (int t = tidx(); t < 32 * steps; t += NTE) {
+            const float p = t < n ? expf(s_arr[t] - m) : 0.f;
+            split3(p, pp[t], pp[cap + t], pp[2 * cap + t]);
+            lw += p;
+        }
+        lw = lanes_sum<64>(lw);
+        if (lane == 0) lpart[wave] = lw;
+        __syncthreads();
+        for (int dt = wave; dt < (hd >> 4); dt += NWE) {
+            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+            for (int k = 0; k < steps; k++) {
+                const int t0 = 32 * k + 8 * lg;
+                const bf16x8 a0 = *(const bf16x8 *)(pp + t0), a1 = *(const bf16x8 *)(pp + cap + t0), a2 = *(const bf16x8 *)(pp + 2 * cap + t0);
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int ta = t0 + 2 * e < n ? t0 + 2 * e : n - 1, tb = t0 + 2 * e + 1 < n ? t0 + 2 * e + 1 : n - 1;
+                    w[e] = (uint32_t)vw[(size_t)ta * rs + 16 * dt + li] | (uint32_t)vw[(size_t)tb * rs + 16 * dt + li] << 16;
+                }
+                const u32x4 wv = {w[0], w[1], w[2], w[3]};
+                const bf16x8 b = __builtin_bit_cast(bf16x8, wv);
+                c = mfma_bf16(a0, b, c);
+                c = mfma_bf16(a1, b, c);
+                c = mfma_bf16(a2, b, c);
+            }
+            float l = 0.f;
+#pragma unroll
+            for (int k = 0; k < NWE; k++) l += lpart[k];
+            if (lg == 0) att[h * hd + 16 * dt + li] = c[0] / l;
         }
         __syncthreads();
     }
@@ -1213,8 +1331,8 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, act, kp, work);
     __syncthreads();
     // q, k rows: RoPE on pairs (2i, 2i+1) of each head by the angle i (ops.c:29-40); k, v rows rounded
-    // to bf16 as the cache holds them (engine.c:247-248), into cur and (for the heads this group writes)
-    // the cache
+    // to bf16 as the cache holds them (engine.c:247-248), into cur, row pos of the LDS window and, for the
+    // heads this group writes, the cache
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
     const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
     rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner, bool lead) {
@@ -1229,6 +1347,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
                 const int r = i - nqd, kv = r < nkd ? 0 : 1, jj = r - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
                 const uint16_t hb = f32_bf16(y);
                 cur[kv * nkd + jj] = hb;
+                if (M.kv_lds) kvb[((size_t)(kv * G.nkv + kvl) * M.ctx + pos) * kv_row(hd) + (jj - kvl * hd)] = hb;
                 if (G.write_kv >> kvl & 1u)
                     gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + (jj - kvl * hd)] = hb;
             }
@@ -1236,7 +1355,8 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     });
     if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
+    if (M.kv_lds && hd % 32 == 0) attend_mfma(M, G, pos, qh, kvb, work, vred, att);
+    else if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
     else attend_group<false, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
 
     // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
