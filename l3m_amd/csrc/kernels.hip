@@ -1176,20 +1176,21 @@ __device__ __forceinline__ void split3(float x, __bf16 &h, __bf16 &m, __bf16 &l)
 // row pos included: the block stores this step's rows there first). One head at a time, three passes
 // with a barrier after each:
 //  1. scores: wavefront w takes 16-position tiles w, w + NWE, ...: S = K_tile (16 x hd, from the window
-//     as it lies) times q (in every column of B), q split into three bf16 parts so the products are f32
-//     exact; s_t = S / sqrt(hd) into sc, and each wavefront's maximum into smax;
+//     as it lies) times q (in every column of B), q split into three bf16 parts (qp, written with q) so
+//     the products are f32 exact; s_t = S / sqrt(hd) into sc, and each wavefront's maximum into smax;
 //  2. p_t = exp(s_t - m) over the head's maximum m, stored as three bf16 parts (zero past pos, up to a
 //     multiple of 32), and each wavefront's sum of p into lpart;
 //  3. o = P V: wavefront w takes dims [16w, 16w + 16): 32 positions per step, A = the p parts (every row
 //     the same), B = V rows 32 at a time; att = o / sum(lpart).
-// sc: 10 * ceil32(ctx) bytes of LDS; vred: at least 2 * NWE floats. Ends with a barrier.
-__device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, const float *qh, const uint16_t *kvb, float *sc,
+// sc: 10 * ceil32(ctx) bytes of LDS; vred: 2 * NWE floats; qp: [3][nq * hd] bf16. Three accumulators
+// (one per bf16 part) keep the MFMA chains independent. Ends with a barrier.
+__device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, const __bf16 *qp, const uint16_t *kvb, float *sc,
                             float *vred, float *att) {
     const int hd = M.hd, rs = kv_row(hd), ctx = M.ctx, n = pos + 1;
     const int lane = tidx() & 63, wave = wave_id(), li = lane & 15, lg = lane >> 4;
     const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
     const size_t win = (size_t)ctx * rs;
-    const int tiles = (n + 15) >> 4, steps = (n + 31) >> 5, cap = (ctx + 31) & ~31;
+    const int tiles = (n + 15) >> 4, steps = (n + 31) >> 5, cap = (ctx + 31) & ~31, nqd = G.nq * hd;
     float *s_arr = sc, *smax = vred, *lpart = vred + NWE;
     __bf16 *pp = (__bf16 *)(sc + cap);                // [3][cap]
     for (int h = 0; h < G.nq; h++) {
@@ -1199,31 +1200,25 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
         float mx = -INFINITY;
         for (int T = wave; T < tiles; T += NWE) {
             const int row = T * 16 + li < n ? T * 16 + li : n - 1;
-            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+            f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0;
             for (int kk = 0; kk < hd; kk += 32) {
-                const bf16x8 a = *(const bf16x8 *)(kw + (size_t)row * rs + kk + 8 * lg);
-                const float4 q0 = *(const float4 *)(qh + h * hd + kk + 8 * lg), q1 = *(const float4 *)(qh + h * hd + kk + 8 * lg + 4);
-                const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-                bf16x8 b0, b1, b2;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    __bf16 x, y, z;
-                    split3(qv[e], x, y, z);
-                    b0[e] = x; b1[e] = y; b2[e] = z;
-                }
-                c = mfma_bf16(a, b0, c);
-                c = mfma_bf16(a, b1, c);
-                c = mfma_bf16(a, b2, c);
+                const int qo = h * hd + kk + 8 * lg;
+                bf16x8 a = *(const bf16x8 *)(kw + (size_t)row * rs + kk + 8 * lg), b0 = *(const bf16x8 *)(qp + qo),
+                       b1 = *(const bf16x8 *)(qp + nqd + qo), b2 = *(const bf16x8 *)(qp + 2 * nqd + qo);
+                asm volatile("" : "+v"(a), "+v"(b0), "+v"(b1), "+v"(b2));   // all four read before the products
+                c0 = mfma_bf16(a, b0, c0);
+                c1 = mfma_bf16(a, b1, c1);
+                c2 = mfma_bf16(a, b2, c2);
             }
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int t = T * 16 + 4 * lg + r;
-                const float sv = c[r] * scale;
+                const float sv = ((c0[r] + c1[r]) + c2[r]) * scale;
                 if (li == 0) s_arr[t] = t < n ? sv : -INFINITY;
                 mx = fmaxf(mx, t < n ? sv : -INFINITY);
             }
         }
-        {
+        if (wave < tiles) {                           // the four row groups' maxima (lanes 16 apart)
             float lo, hi;
             swap16(mx, lo, hi); mx = fmaxf(lo, hi);
             swap32(mx, lo, hi); mx = fmaxf(lo, hi);
@@ -1237,30 +1232,46 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
             split3(p, pp[t], pp[cap + t], pp[2 * cap + t]);
             lw += p;
         }
-        lw = lanes_sum<64>(lw);
+        if (wave * 64 < 32 * steps) lw = lanes_sum<64>(lw);   // wavefronts past the positions hold 0
         if (lane == 0) lpart[wave] = lw;
         __syncthreads();
         for (int dt = wave; dt < (hd >> 4); dt += NWE) {
-            f32x4 c = {0.f, 0.f, 0.f, 0.f};
-            for (int k = 0; k < steps; k++) {
-                const int t0 = 32 * k + 8 * lg;
-                const bf16x8 a0 = *(const bf16x8 *)(pp + t0), a1 = *(const bf16x8 *)(pp + cap + t0), a2 = *(const bf16x8 *)(pp + 2 * cap + t0);
-                uint32_t w[4];
+            f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0;
+            // two 32-position steps per round, every operand read before the first product; a second
+            // step past the end reads step k's operands again and is not multiplied
+            for (int k = 0; k < steps; k += 2) {
+                bf16x8 a[2][3], b[2];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int ta = t0 + 2 * e < n ? t0 + 2 * e : n - 1, tb = t0 + 2 * e + 1 < n ? t0 + 2 * e + 1 : n - 1;
-                    w[e] = (uint32_t)vw[(size_t)ta * rs + 16 * dt + li] | (uint32_t)vw[(size_t)tb * rs + 16 * dt + li] << 16;
+                for (int u = 0; u < 2; u++) {
+                    const int t0 = 32 * (k + u < steps ? k + u : k) + 8 * lg;
+                    a[u][0] = *(const bf16x8 *)(pp + t0);
+                    a[u][1] = *(const bf16x8 *)(pp + cap + t0);
+                    a[u][2] = *(const bf16x8 *)(pp + 2 * cap + t0);
+                    uint32_t w[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int ta = t0 + 2 * e < n ? t0 + 2 * e : n - 1, tb = t0 + 2 * e + 1 < n ? t0 + 2 * e + 1 : n - 1;
+                        w[e] = (uint32_t)vw[(size_t)ta * rs + 16 * dt + li] | (uint32_t)vw[(size_t)tb * rs + 16 * dt + li] << 16;
+                    }
+                    const u32x4 wv = {w[0], w[1], w[2], w[3]};
+                    b[u] = __builtin_bit_cast(bf16x8, wv);
                 }
-                const u32x4 wv = {w[0], w[1], w[2], w[3]};
-                const bf16x8 b = __builtin_bit_cast(bf16x8, wv);
-                c = mfma_bf16(a0, b, c);
-                c = mfma_bf16(a1, b, c);
-                c = mfma_bf16(a2, b, c);
-            }
-            float l = 0.f;
+                // every operand in its own registers before the first product (otherwise the compiler
+                // reloads a part into a register an earlier product still reads, one LDS trip per product)
 #pragma unroll
-            for (int k = 0; k < NWE; k++) l += lpart[k];
-            if (lg == 0) att[h * hd + 16 * dt + li] = c[0] / l;
+                for (int u = 0; u < 2; u++) asm volatile("" : "+v"(a[u][0]), "+v"(a[u][1]), "+v"(a[u][2]), "+v"(b[u]));
+                c0 = mfma_bf16(a[0][0], b[0], c0);
+                c1 = mfma_bf16(a[0][1], b[0], c1);
+                c2 = mfma_bf16(a[0][2], b[0], c2);
+                if (k + 1 < steps) {
+                    c0 = mfma_bf16(a[1][0], b[1], c0);
+                    c1 = mfma_bf16(a[1][1], b[1], c1);
+                    c2 = mfma_bf16(a[1][2], b[1], c2);
+                }
+            }
+            // the wavefronts' sums of p: lane k < NWE reads wavefront k's (lanes 16 and up repeat them)
+            const float l = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(lanes_sum<16>(lpart[li]))));
+            if (lg == 0) att[h * hd + 16 * dt + li] = ((c0[0] + c1[0]) + c2[0]) / l;
         }
         __syncthreads();
     }
@@ -1335,6 +1346,9 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // heads this group writes, the cache
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
     const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
+    // the matrix-core attention (LDS window, hd a multiple of 32, q parts fit beside vred's 2 NWE sums)
+    const bool mfma_att = M.kv_lds && hd % 32 == 0 && 6 * nqd <= 4 * NWE * hd;
+    __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
     rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner, bool lead) {
         if (i < nqd + nkd) {
             const int local = i < nqd ? i : i - nqd, head = (int)(((float)local + 0.5f) * inv_hd);
@@ -1342,8 +1356,10 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
             y = (i & 1) ? partner * c.y + y * c.x : y * c.x - partner * c.y;
         }
         if (lead) {
-            if (i < nqd) qh[i] = y;
-            else {
+            if (i < nqd) {
+                qh[i] = y;
+                if (mfma_att) split3(y, qp[i], qp[nqd + i], qp[2 * nqd + i]);
+            } else {
                 const int r = i - nqd, kv = r < nkd ? 0 : 1, jj = r - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
                 const uint16_t hb = f32_bf16(y);
                 cur[kv * nkd + jj] = hb;
@@ -1355,7 +1371,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     });
     if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (M.kv_lds && hd % 32 == 0) attend_mfma(M, G, pos, qh, kvb, work, vred, att);
+    if (mfma_att) attend_mfma(M, G, pos, qp, kvb, work, vred, att);
     else if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
     else attend_group<false, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
 
