@@ -774,6 +774,11 @@ __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float 
     if (wave * 64 < G.n4) {
         P.nw = ldg16f(nw, own);
         P.base = ld16f<COH>(base, f);
+        if (rope_row) {                               // hd / 2 <= n4: the angles' threads are owners too
+            const int i = tid < (hd >> 1) ? tid : (hd >> 1) - 1;
+            const u32x2 c = gp<u32x2>(rope_row)[i];
+            P.cs = make_float2(__uint_as_float(c.x), __uint_as_float(c.y));
+        }
     }
     if (wave * 64 < G.groups * G.n4) {
 #pragma unroll
@@ -783,11 +788,6 @@ __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float 
                 P.p[j] = ld16f<COH>(parts, (size_t)pj * (dim >> 2) + f);
             }
         }
-    }
-    if (rope_row) {
-        const int i = tid < (hd >> 1) ? tid : (hd >> 1) - 1;
-        const u32x2 c = gp<u32x2>(rope_row)[i];
-        P.cs = make_float2(__uint_as_float(c.x), __uint_as_float(c.y));
     }
     if (use_embed) P.emb = lt_elem4(embed, tok, 4 * own);   // layer 0: x = dequant(embed[tok]) (engine.c:236)
     asm volatile("" ::: "memory");                            // these loads are issued before the weights
