@@ -70,12 +70,12 @@ typedef struct {
 typedef struct {
     int                pos0, nsteps, head_from;
     int                head_tpw, n_head, body_xcc;
-    unsigned          *sync;           // L3M_SYNC_WORDS: flags, tickets, argmax keys; zero at launch
+    unsigned          *sync;           // L3M_SYNC_WORDS words: flags, tickets, argmax keys; zero at launch
     unsigned long long spin_limit;     // longest wait, in ticks of the 100 MHz clock
 } l3m_run;
-#define L3M_SYNC_WORDS(n_head) (256 + 2 * (n_head))   // flag words, then one 64-bit key per head workgroup
+#define L3M_MAX_HEAD_WGS 256                         // the key area holds this many keys, whatever n_head is
+#define L3M_SYNC_WORDS (256 + 2 * L3M_MAX_HEAD_WGS)  // flag words, then one 64-bit key per head workgroup
 #define L3M_SYNC_ABORT 192                           // the word a timed-out wait sets
-#define L3M_MAX_HEAD_WGS 1024
 
 // ------------------------------------------------------------------ runtime
 int         l3m_dev_init(void);                 // 0 when a gfx9 HIP device is usable

@@ -1564,7 +1564,7 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
 // Every wait is bounded: past R.spin_limit ticks of the 100 MHz clock the waiter raises the abort flag
 // and every workgroup leaves at its next wait, so the grid always drains.
 enum { SY_ATTN = 0, SY_FFN = 64, SY_XF = 128, SY_ABORT = L3M_SYNC_ABORT, SY_TICKET = 224, SY_HEAD_TICKET = 240, SY_SLOTS = 256 };
-static_assert(L3M_SYNC_WORDS(0) == SY_SLOTS, "keys follow the flag words");
+static_assert(L3M_SYNC_WORDS == SY_SLOTS + 2 * L3M_MAX_HEAD_WGS && L3M_MAX_HEAD_WGS == 256, "keys follow the flag words");
 
 __device__ __forceinline__ unsigned xcc_id() {
     unsigned x;
@@ -1652,7 +1652,10 @@ __device__ __forceinline__ uint64_t lanes_max_u64(uint64_t v) {
 }
 
 // The token chosen by step s's head: wavefront 0 polls the n_head keys until all carry the step's tag and
-// reduces them. Returns the token, or -1 when the run is being abandoned.
+// reduces them. Returns the token, or -1 when the run is being abandoned. Each lane loads keys
+// lane + 64 r, r < 4, of the 256-key area every time, and keys from n_head on are masked by selects: a load
+// under a lane condition is followed by a wait for every load in flight, which would put the four loads
+// one cross-XCD round trip apart instead of overlapping them.
 __device__ int wait_token(const uint64_t *slots, int n_head, int s, unsigned *abort_flag, unsigned long long limit, int *lds) {
     const int tid = tidx();
     if (tid < 64) {
@@ -1663,14 +1666,15 @@ __device__ int wait_token(const uint64_t *slots, int n_head, int s, unsigned *ab
         for (unsigned spin = 0;; spin++) {
             bool all = true;
             best = 0;
+            uint64_t v[4];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {             // n_head <= 1024
-                const int i = tid + 64 * r;
-                if (i < n_head) {
-                    const uint64_t v = __hip_atomic_load(gp<uint64_t>(slots + i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    all = all && (unsigned)(v >> 49) == tag;
-                    best = max_u64(best, v & KEY_BITS);
-                }
+            for (int r = 0; r < 4; r++)
+                v[r] = __hip_atomic_load(gp<uint64_t>(slots + tid + 64 * r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const bool in = tid + 64 * r < n_head;
+                all = all && (!in || (unsigned)(v[r] >> 49) == tag);
+                best = max_u64(best, in ? v[r] & KEY_BITS : 0ull);
             }
             if (__all(all)) break;
             if (!keep_waiting(spin, t0, abort_flag, limit)) { best = ~0ull; break; }
