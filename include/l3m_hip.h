@@ -136,6 +136,10 @@ double l3m_weight_bytes(const l3m_model *m);                       // weight byt
 // 1 when decode runs as one persistent cooperative kernel per chunk of steps (L3M_PERSIST=0 at load
 // selects the one-graph-per-step path), 0 otherwise.
 int    l3m_decode_persistent(const l3m_model *m);
+// The logits the last generate call computed at position pos (the prediction for pos + 1), into out
+// [vocab]: positions within the last 64 that call ran; -1 otherwise. An inspection hook (the sampled and
+// greedy tokens are checked against the logits they came from).
+int    l3m_logits_at(const l3m_model *m, int pos, float *out);
 
 // Synthetic .l3m models (seeded, host-independent bytes).
 typedef struct {

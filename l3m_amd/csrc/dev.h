@@ -62,7 +62,16 @@ typedef struct {
     uint16_t    *kc, *vc;        // [layer][n_kv][ctx][hd] bf16
     l3m_dmat     embed, head;    // head may alias embed (tied)
     const float *norm;
+    struct l3m_dsample *samp;    // temperature sampling: the generate call's temperature and random state
 } l3m_dmodel;
+// Device-resident sampling state, set by the host at the start of each generate call; the workgroup that
+// samples advances rng (xorshift64*, engine.c:98-101) once per sampled token.
+typedef struct l3m_dsample {
+    unsigned long long rng;
+    float              temp;         // > 0: sample at this temperature; otherwise greedy
+    unsigned           pad;
+} l3m_dsample;
+#define L3M_SAMPLE_MAX_VOCAB (64 * 1024)   // logits held in one workgroup's registers (64 per thread)
 
 // One launch of the persistent decode kernel: steps at positions pos0 .. pos0 + nsteps - 1; logits (and
 // the argmax token at pos + 1) for positions >= head_from. The body runs on the workgroups of XCD
@@ -72,6 +81,8 @@ typedef struct {
     int                head_tpw, n_head, body_xcc;
     unsigned          *sync;           // L3M_SYNC_WORDS words: flags, tickets, argmax keys; zero at launch
     unsigned long long spin_limit;     // longest wait, in ticks of the 100 MHz clock
+    float              temp;           // > 0: tokens are sampled at this temperature (samp holds the state)
+    unsigned           pad;
 } l3m_run;
 #define L3M_MAX_HEAD_WGS 256                         // the key area holds this many keys, whatever n_head is
 #define L3M_SYNC_WORDS (256 + 2 * L3M_MAX_HEAD_WGS)  // flag words, then one 64-bit key per head workgroup

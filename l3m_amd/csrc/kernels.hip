@@ -1439,7 +1439,7 @@ __device__ __forceinline__ l3m_dmat head_slice(const l3m_dmodel &M, int t0, int 
 // into slot pos % nslots, and this slice's (max, lowest index) in v, idx for every thread.
 template <int DT, bool PRE>
 __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &V, int t0, int tpw, int pos, HeadW<DT> &w,
-                                           uint8_t *smem, float &v, int &idx) {
+                                           uint8_t *smem, float &v, int &idx, bool coh_logits = false) {
     const int tid = tidx(), dim = M.dim, kp = kpad(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
     float *work = (float *)(smem + L.work), *scr = (float *)(smem + L.scr);
@@ -1469,7 +1469,12 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
     v = -INFINITY;
     idx = 0x7FFFFFFF;
     rows_sum4(V, work, V.rows, [&](int i, float yy, float, bool lead) {
-        if (lead) { gw(lg)[i] = yy; better(v, idx, yy, t0 * 16 + i); }
+        if (lead) {
+            // write-through when a workgroup on another XCD samples from them during this kernel
+            if (coh_logits) __hip_atomic_store(gw((unsigned *)lg + i), __float_as_uint(yy), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else gw(lg)[i] = yy;
+            better(v, idx, yy, t0 * 16 + i);
+        }
     });
     block_argmax(v, idx, scr, (int *)scr + 16);
 }
@@ -1484,6 +1489,96 @@ __device__ void reduce_partials(const float *val, const int *idx_in, int n, floa
         better(v, idx, pv, pi);
     }
     block_argmax(v, idx, scr, (int *)scr + 16);
+}
+
+// ------------------------------------------------------------------ temperature sampling
+
+// xorshift64* (engine.c:98-101): three shifts of the state, then the top 53 bits of its product with the
+// generator's multiplier as a double in [0, 1).
+__device__ __forceinline__ double rand01(unsigned long long &st) {
+    st ^= st >> 12;
+    st ^= st << 25;
+    st ^= st >> 27;
+    return (double)((st * 0x2545F4914F6CDD1DULL) >> 11) * 0x1p-53;
+}
+// The unnormalized probability of a logit (engine.c:284-287): expf((logit - gmax) / temp), and 0 when the
+// exponent is below -16.
+__device__ __forceinline__ float sample_weight(float logit, float gmax, float temp) {
+    const float d = (logit - gmax) / temp;
+    return d < -16.0f ? 0.0f : expf(d);
+}
+
+constexpr int SAMPLE_F4 = L3M_SAMPLE_MAX_VOCAB / NTE / 4;   // float4 of logits per thread at most
+static_assert(SAMPLE_F4 * 4 * NTE == L3M_SAMPLE_MAX_VOCAB, "the vocabulary bound is whole float4 per thread");
+
+// One workgroup samples a token from the V logits at lg (V % 4 == 0, V <= L3M_SAMPLE_MAX_VOCAB), given
+// their maximum gmax and the draw u: p_i = sample_weight(lg[i]), z = the double sum of all p_i, and the
+// token is the first i whose running double sum exceeds u * z, or V - 1 when none does (engine.c:364-379,
+// the reference path; its multi-rank path, engine.c:303-319, differs from it only in how the double sums
+// round). Thread t owns float4 [t per4, (t + 1) per4): it sums its range in order, a block scan gives each
+// range the sum of the ranges before it, and every thread walks its own range at once; the lowest
+// crossing wins. lg is read with device-coherent loads (other workgroups wrote it). dscr: NWE doubles,
+// iscr: NWE ints of LDS. Every thread gets the token.
+__device__ int sample_block(const float *lg, int V, float gmax, float temp, double u, double *dscr, int *iscr) {
+    const int tid = tidx(), lane = tid & 63, wave = wave_id();
+    const int V4 = V >> 2, per4 = (V4 + NTE - 1) / NTE, f0 = tid * per4;
+    float p[4 * SAMPLE_F4];
+#pragma unroll
+    for (int k = 0; k < SAMPLE_F4; k++) {             // unconditional (clamped) loads, all in flight at once
+        const int f = f0 + k < V4 ? f0 + k : V4 - 1;
+        const float4 v = ld16f<true>(lg, f);
+        p[4 * k] = v.x; p[4 * k + 1] = v.y; p[4 * k + 2] = v.z; p[4 * k + 3] = v.w;
+    }
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < SAMPLE_F4; k++) {
+        if (k < per4) {                               // uniform
+            const bool in = f0 + k < V4;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                p[4 * k + e] = in ? sample_weight(p[4 * k + e], gmax, temp) : 0.0f;
+                sum += (double)p[4 * k + e];
+            }
+        }
+    }
+    // the ranges before this thread's: an inclusive scan in the wavefront, then the wavefronts' totals in
+    // order (z is accumulated in that same order by every thread, so `before` is exactly its prefix)
+    double incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    double excl = __shfl_up(incl, 1, 64);
+    if (lane == 0) excl = 0.0;
+    if (lane == 63) dscr[wave] = incl;
+    __syncthreads();
+    double before = 0.0, z = 0.0;
+    for (int w = 0; w < NWE; w++) {
+        const double t = dscr[w];
+        if (w == wave) before = z;
+        z += t;
+    }
+    const double target = u * z;
+    double c = before + excl;
+    int cand = 0x7FFFFFFF;
+#pragma unroll
+    for (int k = 0; k < SAMPLE_F4; k++) {
+        if (k < per4) {
+            const bool in = f0 + k < V4;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                c += (double)p[4 * k + e];
+                if (in && c > target && cand == 0x7FFFFFFF) cand = 4 * (f0 + k) + e;
+            }
+        }
+    }
+    cand = lanes_mini<64>(cand);
+    if (lane == 0) iscr[wave] = cand;
+    __syncthreads();
+    const int tok = lanes_mini<NWE>(iscr[tid & (NWE - 1)]);
+    __syncthreads();                                  // dscr and iscr are free again
+    return tok == 0x7FFFFFFF ? V - 1 : tok;
 }
 
 // ------------------------------------------------------------------ the graph path: one kernel per block
@@ -1530,6 +1625,13 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
     if (!last) return;
     __threadfence();
     reduce_partials(M.part_val, M.part_idx, gridDim.x, scr, v, idx);
+    const float temp = M.samp->temp;
+    if (temp > 0 && idx != 0x7FFFFFFF) {             // temperature sampling over this step's logits
+        unsigned long long st = M.samp->rng;
+        const double u = rand01(st);
+        idx = sample_block(M.logits + (size_t)(pos % M.nslots) * M.vocab, M.vocab, v, temp, u, (double *)scr, (int *)scr + 2 * NWE);
+        if (tidx() == 0) M.samp->rng = st;
+    }
     if (tidx() == 0) {
         if (advance) {
             M.tokens[pos + 1] = idx == 0x7FFFFFFF ? 0 : idx;
@@ -1563,7 +1665,8 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
 //
 // Every wait is bounded: past R.spin_limit ticks of the 100 MHz clock the waiter raises the abort flag
 // and every workgroup leaves at its next wait, so the grid always drains.
-enum { SY_ATTN = 0, SY_FFN = 64, SY_XF = 128, SY_ABORT = L3M_SYNC_ABORT, SY_TICKET = 224, SY_HEAD_TICKET = 240, SY_SLOTS = 256 };
+enum { SY_ATTN = 0, SY_FFN = 64, SY_XF = 128, SY_ABORT = L3M_SYNC_ABORT, SY_TOKEN = 208, SY_TICKET = 224, SY_HEAD_TICKET = 240,
+       SY_SLOTS = 256 };
 static_assert(L3M_SYNC_WORDS == SY_SLOTS + 2 * L3M_MAX_HEAD_WGS && L3M_MAX_HEAD_WGS == 256, "keys follow the flag words");
 
 __device__ __forceinline__ unsigned xcc_id() {
@@ -1651,40 +1754,71 @@ __device__ __forceinline__ uint64_t lanes_max_u64(uint64_t v) {
     return max_u64(join(__float_as_int(h0), __float_as_int(l0)), join(__float_as_int(h1), __float_as_int(l1)));
 }
 
-// The token chosen by step s's head: wavefront 0 polls the n_head keys until all carry the step's tag and
-// reduces them. Returns the token, or -1 when the run is being abandoned. Each lane loads keys
-// lane + 64 r, r < 4, of the 256-key area every time, and keys from n_head on are masked by selects: a load
-// under a lane condition is followed by a wait for every load in flight, which would put the four loads
-// one cross-XCD round trip apart instead of overlapping them.
+// Wavefront 0 polls the n_head keys of step s until all carry the step's tag; returns their maximum (the
+// winning key) in wavefront 0, or ~0 when the run is being abandoned. Each lane loads keys lane + 64 r,
+// r < 4, of the 256-key area every time, and keys from n_head on are masked by selects: a load under a
+// lane condition is followed by a wait for every load in flight, which would put the four loads one
+// cross-XCD round trip apart instead of overlapping them.
+__device__ __forceinline__ uint64_t poll_keys(const uint64_t *slots, int n_head, int s, unsigned *abort_flag, unsigned long long limit) {
+    const int tid = tidx();
+    const unsigned tag = step_tag(s);
+    uint64_t best = 0;
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    for (unsigned spin = 0;; spin++) {
+        bool all = true;
+        best = 0;
+        uint64_t v[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            v[r] = __hip_atomic_load(gp<uint64_t>(slots + tid + 64 * r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const bool in = tid + 64 * r < n_head;
+            all = all && (!in || (unsigned)(v[r] >> 49) == tag);
+            best = max_u64(best, in ? v[r] & KEY_BITS : 0ull);
+        }
+        if (__all(all)) break;
+        if (!keep_waiting(spin, t0, abort_flag, limit)) return ~0ull;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return lanes_max_u64(best);
+}
+__device__ __forceinline__ int key_token(uint64_t key) { return (key >> 17) == 0 ? 0 : 0x1FFFF - (int)(key & 0x1FFFF); }
+// The value a key holds (argmax_key's order-preserving code, undone; a -0 maximum comes back as +0).
+__device__ __forceinline__ float key_value(uint64_t key) {
+    const uint32_t u = (uint32_t)(key >> 17);
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+// The token chosen by step s's head (the winning key's index), into every thread; -1 when the run is
+// being abandoned.
 __device__ int wait_token(const uint64_t *slots, int n_head, int s, unsigned *abort_flag, unsigned long long limit, int *lds) {
     const int tid = tidx();
     if (tid < 64) {
+        const uint64_t best = poll_keys(slots, n_head, s, abort_flag, limit);
+        if (tid == 0) *lds = best == ~0ull ? -1 : key_token(best);
+    }
+    __syncthreads();
+    const int tok = *lds;
+    __syncthreads();
+    return tok;
+}
+
+// The token word: step_tag(s) << 17 | token, written by the workgroup that sampled step s.
+__device__ __forceinline__ unsigned token_word(int s, int tok) { return step_tag(s) << 17 | (unsigned)tok; }
+// The token sampled at step s, from the token word, into every thread; -1 when the run is being abandoned.
+__device__ int wait_token_word(const unsigned *word, int s, unsigned *abort_flag, unsigned long long limit, int *lds) {
+    if (tidx() == 0) {
         const unsigned tag = step_tag(s);
         int tok = -1;
-        uint64_t best = 0;
         const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
         for (unsigned spin = 0;; spin++) {
-            bool all = true;
-            best = 0;
-            uint64_t v[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                v[r] = __hip_atomic_load(gp<uint64_t>(slots + tid + 64 * r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const bool in = tid + 64 * r < n_head;
-                all = all && (!in || (unsigned)(v[r] >> 49) == tag);
-                best = max_u64(best, in ? v[r] & KEY_BITS : 0ull);
-            }
-            if (__all(all)) break;
-            if (!keep_waiting(spin, t0, abort_flag, limit)) { best = ~0ull; break; }
+            const unsigned w = ld_flag(word);
+            if (w >> 17 == tag) { tok = (int)(w & 0x1FFFF); break; }
+            if (!keep_waiting(spin, t0, abort_flag, limit)) break;
             __builtin_amdgcn_s_sleep(1);
         }
-        if (best != ~0ull) {
-            best = lanes_max_u64(best);
-            tok = (best >> 17) == 0 ? 0 : 0x1FFFF - (int)(best & 0x1FFFF);
-        }
-        if (tid == 0) *lds = tok;
+        *lds = tok;
     }
     __syncthreads();
     const int tok = *lds;
@@ -1758,7 +1892,8 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
         if (l == 0 && s > 0 && pos - 1 >= R.head_from) {
             // this step's token is the previous step's argmax (which also orders this step after every
             // read of the previous step's FFN partials)
-            tok = wait_token((const uint64_t *)(sync + SY_SLOTS), R.n_head, s - 1, abort_flag, R.spin_limit, &ok_lds);
+            tok = R.temp > 0 ? wait_token_word(sync + SY_TOKEN, s - 1, abort_flag, R.spin_limit, &ok_lds)
+                                   : wait_token((const uint64_t *)(sync + SY_SLOTS), R.n_head, s - 1, abort_flag, R.spin_limit, &ok_lds);
             if (tok < 0) return false;
             if (g == 0 && tidx() == 0) gw(M.tokens)[pos] = tok;
         } else {
@@ -1817,10 +1952,33 @@ __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, 
     HeadW<DT> wt;
     if (has_tiles) head_issue<DT>(wt, V);
     if (!wait_flags<4>(R.sync + SY_XF, M.n_chunks, (unsigned)s + 1, R.sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
-    if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx);
+    const float temp = R.temp;
+    if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx, temp > 0);
     if (tidx() == 0)
         __hip_atomic_store(gw((uint64_t *)(R.sync + SY_SLOTS) + h), argmax_key(v, idx, step_tag(s)), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+    if (h == 0 && temp > 0) {
+        // Temperature sampling: head workgroup 0 takes every key (so every logit of the step is in memory:
+        // each workgroup's logit stores completed before its key), then the whole row of logits, and
+        // publishes the token in the token word. Its weight registers are free by now.
+        double *dscr = (double *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).scr);
+        int *iscr = (int *)(dscr + NWE);
+        if (tidx() < 64) {
+            const uint64_t key = poll_keys((const uint64_t *)(R.sync + SY_SLOTS), R.n_head, s, R.sync + SY_ABORT, R.spin_limit);
+            if (tidx() == 0) { iscr[0] = (int)(uint32_t)key; iscr[1] = (int)(uint32_t)(key >> 32); }
+        }
+        __syncthreads();
+        const uint64_t key = (uint64_t)(uint32_t)iscr[1] << 32 | (uint32_t)iscr[0];
+        __syncthreads();
+        if (key == ~0ull) return false;
+        unsigned long long st = __hip_atomic_load(gp<unsigned long long>(&M.samp->rng), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const double u = rand01(st);
+        const int tok = sample_block(M.logits + (size_t)(pos % M.nslots) * M.vocab, M.vocab, key_value(key), temp, u, dscr, iscr);
+        if (tidx() == 0) {
+            __hip_atomic_store(gw(&M.samp->rng), st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(gw(R.sync + SY_TOKEN), token_word(s, tok), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     return true;
 }
 
@@ -1863,7 +2021,9 @@ __global__ void __launch_bounds__(NTE) k_decode(const l3m_dmodel *__restrict__ M
     // the last step's token has no next step in this launch to take it: group 0 writes it
     const int last = R.pos0 + R.nsteps - 1;
     if (role == 0 && R.nsteps > 0 && last >= R.head_from) {
-        const int tok = wait_token((const uint64_t *)(R.sync + SY_SLOTS), R.n_head, R.nsteps - 1, R.sync + SY_ABORT, R.spin_limit, &role_lds);
+        const int tok = R.temp > 0
+                            ? wait_token_word(R.sync + SY_TOKEN, R.nsteps - 1, R.sync + SY_ABORT, R.spin_limit, &role_lds)
+                            : wait_token((const uint64_t *)(R.sync + SY_SLOTS), R.n_head, R.nsteps - 1, R.sync + SY_ABORT, R.spin_limit, &role_lds);
         if (tok >= 0 && tidx() == 0) gw(Mp->tokens)[last + 1] = tok;
     }
 }

@@ -52,6 +52,10 @@ class Oracle:
             "or_logits": (_f, [C.c_void_p]),
             "or_forward": (None, [C.c_void_p, C.c_int32, C.c_int, C.c_int]),
             "or_generate": (C.c_int, [C.c_void_p, _i32, C.c_int, C.c_int, _i32]),
+            "or_rand01": (C.c_double, [C.POINTER(C.c_uint64)]),
+            "or_seed_state": (C.c_uint64, [C.c_uint64]),
+            "or_sample": (C.c_int, [_f, C.c_int, C.c_float, C.POINTER(C.c_uint64)]),
+            "or_generate_sampled": (C.c_int, [C.c_void_p, _i32, C.c_int, C.c_int, C.c_float, C.c_uint64, _i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -107,6 +111,23 @@ class Oracle:
         self.lib.or_attend(_p(out, _f), _p(q, _f), _p(k, _u16), _p(v, _u16), pos, hd, stride)
         return out
 
+    # --- temperature sampling (engine.c:98-101, 284-287, 364-379, 555)
+    def seed_state(self, seed):
+        return self.lib.or_seed_state(seed % (1 << 64))
+
+    def rand01(self, state):
+        """(the draw, the next state) of xorshift64* from state."""
+        st = C.c_uint64(state)
+        u = self.lib.or_rand01(C.byref(st))
+        return u, st.value
+
+    def sample(self, logits, temp, state):
+        """(the token, the next state): the reference path's pick from logits at temperature temp."""
+        x = np.ascontiguousarray(logits, np.float32)
+        st = C.c_uint64(state)
+        tok = self.lib.or_sample(_p(x, _f), len(x), temp, C.byref(st))
+        return tok, st.value
+
     # --- model
     def load(self, path, ctx=0, ref=False):
         h = self.lib.or_load(os.fsencode(str(path)), ctx, int(ref))
@@ -125,10 +146,13 @@ class OracleModel:
             self.o.lib.or_free(self.h)
             self.h = None
 
-    def generate(self, prompt, max_new):
+    def generate(self, prompt, max_new, temperature=0.0, seed=0):
         p = np.ascontiguousarray(prompt, np.int32)
         out = np.zeros(max(max_new, 1), np.int32)
-        n = self.o.lib.or_generate(self.h, _p(p, _i32), len(p), max_new, _p(out, _i32))
+        if temperature > 0:
+            n = self.o.lib.or_generate_sampled(self.h, _p(p, _i32), len(p), max_new, temperature, seed % (1 << 64), _p(out, _i32))
+        else:
+            n = self.o.lib.or_generate(self.h, _p(p, _i32), len(p), max_new, _p(out, _i32))
         return out[:n].tolist()
 
     def logits(self):
@@ -238,11 +262,11 @@ class RefModel:
     def describe(self):
         return self.r.lib.l3m_describe(self.h).decode()
 
-    def generate(self, prompt, max_new):
+    def generate(self, prompt, max_new, temperature=0.0, seed=0):
         out = []
         cb = TOKEN_CALLBACK(lambda t, u: out.append(t) or 1)
         p = np.ascontiguousarray(prompt, np.int32)
-        n = self.r.lib.l3m_generate(self.h, _p(p, _i32), len(p), max_new, 0.0, 0, cb, None)
+        n = self.r.lib.l3m_generate(self.h, _p(p, _i32), len(p), max_new, temperature, seed % (1 << 64), cb, None)
         assert n == len(out)
         return out
 

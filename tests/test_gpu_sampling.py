@@ -1,0 +1,77 @@
+"""Temperature sampling on the GPU (engine.c:98-101, 284-319, 555), through the l3m.h API.
+
+- Every sampled token equals the oracle's pick (the reference path's order, pinned against fpedd/l3m in
+  test_cpu_sampling.py) from the logits the GPU computed at that position, with the generator advanced
+  once per token from the generate call's seed: on the persistent kernel and on the one-graph-per-step
+  path, for quantized and bf16 models. (The GPU's expf is not glibc's: a pick could differ only where
+  u * z falls within a few float ulps of a boundary of the running sum.)
+- The first sampled token over many seeds follows softmax(logits / T) (chi-square, as the reference's
+  test_sampling_distribution).
+- Greedy decoding is unchanged by a sampled call before it, and the same seed gives the same tokens.
+"""
+import numpy as np
+import pytest
+
+import l3m_amd as A
+
+pytestmark = pytest.mark.gpu
+CFG = A.Config("samp", dim=128, n_layers=2, n_heads=4, n_kv_heads=2, ffn_dim=256, vocab=512, ctx=128, dtype="q4_0")
+
+
+def check_against_oracle(m, oracle, ids, temp, seed, n):
+    toks = m.generate(ids, n, temperature=temp, seed=seed)
+    st = oracle.seed_state(seed)
+    for k, tok in enumerate(toks):
+        want, st = oracle.sample(m.logits_at(len(ids) - 1 + k), temp, st)
+        assert tok == want, f"seed {seed}, token {k}"
+    if len(toks) < n:                                 # stopped: the next pick was EOS or BOS
+        want, st = oracle.sample(m.logits_at(len(ids) - 1 + len(toks)), temp, st)
+        assert want in (m.eos, m.bos)
+    return toks
+
+
+@pytest.mark.parametrize("persist", ["1", "0"])
+@pytest.mark.parametrize("dtype", ["q4_0", "q8_0", "bf16"])
+def test_sampled_tokens_match_oracle(models, oracle, monkeypatch, dtype, persist):
+    print(f"case {dtype} persist={persist}", flush=True)
+    monkeypatch.setenv("L3M_PERSIST", persist)
+    path = models.get(CFG, dtype, seed=6, std=0.05)
+    m = A.Model(path)
+    assert m.persistent == (persist == "1")
+    ids = A.prompt(6, CFG.vocab, 5)
+    seen = set()
+    for temp in (1.0, 0.6):
+        for seed in range(4):
+            seen.add(tuple(check_against_oracle(m, oracle, ids, temp, seed, 48)))
+    assert len(seen) > 4
+
+
+def test_sampling_distribution(models):
+    path = models.get(CFG, "q8_0", seed=8, std=0.2)
+    m = A.Model(path)
+    ids, temp, n = [3, 9], 0.8, 3000
+    m.generate(ids, 0)
+    lg = m.logits.astype(np.float64)
+    p = np.exp((lg - lg.max()) / temp)
+    p /= p.sum()
+    p[m.eos] += p[m.bos]                              # both end generation
+    p[m.bos] = 0
+    counts = np.zeros(m.vocab)
+    for seed in range(n):
+        out = m.generate(ids, 1, temperature=temp, seed=seed)
+        counts[out[0] if out else m.eos] += 1
+    big = p * n >= 5
+    obs = np.append(counts[big], counts[~big].sum())
+    exp = np.append(p[big], p[~big].sum()) * n
+    df = len(obs) - 1
+    assert ((obs - exp) ** 2 / exp).sum() < df + 5 * np.sqrt(2 * df)
+
+
+def test_seed_repeats_and_greedy_is_unchanged(models):
+    path = models.get(CFG, "q4_0", seed=6, std=0.05)
+    m = A.Model(path)
+    ids = A.prompt(7, CFG.vocab, 4)
+    greedy = m.generate(ids, 40)
+    a = m.generate(ids, 40, temperature=0.9, seed=5)
+    assert m.generate(ids, 40, temperature=0.9, seed=5) == a
+    assert m.generate(ids, 40) == greedy              # the sampled calls leave no state behind
