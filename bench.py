@@ -160,6 +160,15 @@ def cpu_baseline(path, prompt, seconds):
             "sample": f"{n} greedy tokens in {dt:.1f} s, same model file and prompt, restarts at the full context; {desc}"}
 
 
+def sampled_rate(A, m, prompt, n_tokens, temperature=1.0):
+    """Tokens/s of the same decode loop with temperature sampling on the device (l3m_bench_decode_t);
+    a side figure (the metric is greedy decode)."""
+    lib, arr = A.lib(), (C.c_int32 * len(prompt))(*prompt)
+    lib.l3m_bench_decode_t(m._handle(), arr, len(arr), 32, temperature, 0)
+    ns = lib.l3m_bench_decode_t(m._handle(), arr, len(arr), n_tokens, temperature, 1)
+    return {"temperature": temperature, "value": round(1e9 / ns, 1) if ns > 0 else None, "unit": "tok/s"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,6 +178,7 @@ def main():
     ap.add_argument("--dtype", default=None)
     ap.add_argument("--matvec", default="bf16,q8_0,q4_0,mxfp4", help="dtypes for the matvec microbench ('' to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="reference CPU sample length (0 to skip)")
+    ap.add_argument("--sample-temp", type=float, default=1.0, help="temperature of the sampled-decode side figure (0 to skip)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the plain copy kernel once over this many MiB (counter calibration under rocprofv3)")
     a = ap.parse_args()
@@ -213,6 +223,9 @@ def main():
         for r in kt:
             log(f"  {r['kernel']:10s} {r['us']:8.2f} us  {r['GBs']:8.1f} GB/s  x{r['launches_per_token']} = {r['us_per_token']:7.1f} us/token")
         wbytes = A.lib().l3m_weight_bytes(m._handle())
+        sampled = sampled_rate(A, m, prompt, a.steps, a.sample_temp) if a.sample_temp > 0 else None
+        if sampled:
+            log(f"bench: sampled at T={sampled['temperature']}: {sampled['value']} tok/s")
         m.close()
         dom = decode or max(kt, key=lambda r: r["us_per_token"])
         cpu = cpu_baseline(path, prompt, a.cpu_seconds) if a.cpu_seconds > 0 else None
@@ -241,6 +254,7 @@ def main():
         "weight_bytes_per_token": wbytes,
         "weight_GBs_per_token": round(wbytes * value * 1e-9, 1) if wbytes else None,
         "matvec": matvec,
+        "sampled_decode": sampled,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -121,6 +121,8 @@ void   l3m_rope_table(float *table, int ctx, int hd, float theta);   // host: [c
 // Benches. l3m_bench_decode: greedy tokens from prompt (restarting at a full context, main.c:251), ns per
 // generated token. Timers use hipEvents on the library stream; microseconds per launch, <0 on error.
 double l3m_bench_decode(l3m_model *m, const int32_t *prompt, int n_prompt, int n_tokens);
+// The same with temperature sampling on the device (seed + i for the i-th run of the context).
+double l3m_bench_decode_t(l3m_model *m, const int32_t *prompt, int n_prompt, int n_tokens, float temperature, uint64_t seed);
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);
 // One kernel of the decode step at position pos: kind 0 attention block, 1 FFN block, 2 head.
 double l3m_bench_kernel(l3m_model *m, int kind, int layer, int pos, int iters);
