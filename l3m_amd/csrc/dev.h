@@ -64,13 +64,6 @@ typedef struct {
     const float *norm;
     struct l3m_dsample *samp;    // temperature sampling: the generate call's temperature and random state
 } l3m_dmodel;
-// Device-resident sampling state, set by the host at the start of each generate call; the workgroup that
-// samples advances rng (xorshift64*, engine.c:98-101) once per sampled token.
-typedef struct l3m_dsample {
-    unsigned long long rng;
-    float              temp;         // > 0: sample at this temperature; otherwise greedy
-    unsigned           pad;
-} l3m_dsample;
 #define L3M_SAMPLE_MAX_VOCAB (64 * 1024)   // logits held in one workgroup's registers (64 per thread)
 
 // One launch of the persistent decode kernel: steps at positions pos0 .. pos0 + nsteps - 1; logits (and
@@ -85,7 +78,17 @@ typedef struct {
     unsigned           pad;
 } l3m_run;
 #define L3M_MAX_HEAD_WGS 256                         // the key area holds this many keys, whatever n_head is
-#define L3M_SYNC_WORDS (256 + 2 * L3M_MAX_HEAD_WGS)  // flag words, then one 64-bit key per head workgroup
+#define L3M_SYNC_WORDS (256 + 4 * L3M_MAX_HEAD_WGS)  // flag words, one 64-bit key per head workgroup, then
+                                                     // one 64-bit slice total per head workgroup (sampling)
+// Device-resident sampling state, set by the host at the start of each generate call. Every workgroup
+// that takes part in sampling keeps its own copy of the xorshift64* state (engine.c:98-101) and advances
+// it once per sampled token, so all copies stay equal: rng[h] for head workgroup h of the persistent
+// kernel, rng[0] for the graph path's last head workgroup.
+typedef struct l3m_dsample {
+    float              temp;         // > 0: sample at this temperature; otherwise greedy
+    unsigned           pad;
+    unsigned long long rng[L3M_MAX_HEAD_WGS];
+} l3m_dsample;
 #define L3M_SYNC_ABORT 192                           // the word a timed-out wait sets
 
 // ------------------------------------------------------------------ runtime

@@ -986,13 +986,14 @@ __device__ __forceinline__ LdsB lds_of(const l3m_dchunk &C) {
     L.act = C.lds[0]; L.work = C.lds[1]; L.gu = C.lds[2]; L.act2 = C.lds[3]; L.scr = C.lds[4]; L.total = 0;
     return L;
 }
-struct LdsH { size_t act, work, scr, total; };
+struct LdsH { size_t act, work, scr, lgv, total; };
 __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg) {
     LdsH L;
     size_t o = 0;
     L.act = o;  o += align16(act_size(dt, dim));
     L.work = o; o += work_bytes(res_bytes((size_t)tiles_per_wg * nb), 0);
     L.scr = o;  o += 4 * 64;
+    L.lgv = o;  o += align16(4 * 16 * (size_t)tiles_per_wg);   // the slice's logits, kept for sampling
     L.total = o;
     return L;
 }
@@ -1439,7 +1440,7 @@ __device__ __forceinline__ l3m_dmat head_slice(const l3m_dmodel &M, int t0, int 
 // into slot pos % nslots, and this slice's (max, lowest index) in v, idx for every thread.
 template <int DT, bool PRE>
 __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &V, int t0, int tpw, int pos, HeadW<DT> &w,
-                                           uint8_t *smem, float &v, int &idx, bool coh_logits = false) {
+                                           uint8_t *smem, float &v, int &idx, float *keep = nullptr) {
     const int tid = tidx(), dim = M.dim, kp = kpad(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
     float *work = (float *)(smem + L.work), *scr = (float *)(smem + L.scr);
@@ -1470,9 +1471,8 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
     idx = 0x7FFFFFFF;
     rows_sum4(V, work, V.rows, [&](int i, float yy, float, bool lead) {
         if (lead) {
-            // write-through when a workgroup on another XCD samples from them during this kernel
-            if (coh_logits) __hip_atomic_store(gw((unsigned *)lg + i), __float_as_uint(yy), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else gw(lg)[i] = yy;
+            gw(lg)[i] = yy;
+            if (keep) keep[i] = yy;                   // kept in LDS for sampling
             better(v, idx, yy, t0 * 16 + i);
         }
     });
@@ -1494,12 +1494,12 @@ __device__ void reduce_partials(const float *val, const int *idx_in, int n, floa
 // ------------------------------------------------------------------ temperature sampling
 
 // xorshift64* (engine.c:98-101): three shifts of the state, then the top 53 bits of its product with the
-// generator's multiplier as a double in [0, 1).
-__device__ __forceinline__ double rand01(unsigned long long &st) {
+// generator's multiplier. The reference's draw u is this integer times 2^-53.
+__device__ __forceinline__ unsigned long long draw53(unsigned long long &st) {
     st ^= st >> 12;
     st ^= st << 25;
     st ^= st >> 27;
-    return (double)((st * 0x2545F4914F6CDD1DULL) >> 11) * 0x1p-53;
+    return (st * 0x2545F4914F6CDD1DULL) >> 11;
 }
 // The unnormalized probability of a logit (engine.c:284-287): expf((logit - gmax) / temp), and 0 when the
 // exponent is below -16.
@@ -1507,77 +1507,104 @@ __device__ __forceinline__ float sample_weight(float logit, float gmax, float te
     const float d = (logit - gmax) / temp;
     return d < -16.0f ? 0.0f : expf(d);
 }
+// A weight as the integer p * 2^47, exactly: a weight is 0 or a float in [e^-16, 1], and e^-16 > 2^-24, so
+// its last mantissa bit is worth at least 2^-47. Totals of up to 2^16 weights stay below 2^64, so the
+// running sums and totals below are exact integers: the sampler adds in any order and still picks the
+// token the exact running sums pick. (The reference's double sums round; they can pick differently only
+// where u * z falls within their rounding of a boundary.) Anything else (NaN) counts as 0.
+__device__ __forceinline__ unsigned long long fixp(float p) {
+    if (!(p > 0.0f)) return 0;
+    const uint32_t b = __float_as_uint(p), e = b >> 23;
+    return (unsigned long long)((b & 0x7FFFFFu) | 0x800000u) << (e - 103);
+}
+// Whether a running sum c has passed the target u * z, u = k * 2^-53: c * 2^53 > k * z, in 128 bits.
+__device__ __forceinline__ bool crosses(unsigned long long c, unsigned long long k, unsigned long long z) {
+    return (unsigned __int128)c << 53 > (unsigned __int128)k * z;
+}
+// Inclusive prefix sums over the wavefront's lanes in lane order; excl gets the lanes before.
+__device__ __forceinline__ unsigned long long lanes_scan_u64(unsigned long long v, unsigned long long &excl) {
+    const int lane = tidx() & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    excl = __shfl_up(v, 1, 64);
+    if (lane == 0) excl = 0;
+    return v;
+}
+// Block prefix sums in thread order: this thread's exclusive prefix, and the total into every thread.
+// uscr: NWE words of LDS, free again when it returns.
+__device__ __forceinline__ unsigned long long block_scan_u64(unsigned long long v, unsigned long long &total, unsigned long long *uscr) {
+    const int wave = wave_id();
+    unsigned long long excl;
+    const unsigned long long incl = lanes_scan_u64(v, excl);
+    if ((tidx() & 63) == 63) uscr[wave] = incl;
+    __syncthreads();
+    unsigned long long before = 0, z = 0;
+    for (int w = 0; w < NWE; w++) {
+        if (w == wave) before = z;
+        z += uscr[w];
+    }
+    __syncthreads();
+    total = z;
+    return before + excl;
+}
+// The lowest of the threads' candidates (0x7FFFFFFF: none) into every thread. iscr: NWE ints of LDS.
+__device__ __forceinline__ int block_min_int(int v, int *iscr) {
+    v = lanes_mini<64>(v);
+    if ((tidx() & 63) == 0) iscr[wave_id()] = v;
+    __syncthreads();
+    v = lanes_mini<NWE>(iscr[tidx() & (NWE - 1)]);
+    __syncthreads();
+    return v;
+}
 
 constexpr int SAMPLE_F4 = L3M_SAMPLE_MAX_VOCAB / NTE / 4;   // float4 of logits per thread at most
 static_assert(SAMPLE_F4 * 4 * NTE == L3M_SAMPLE_MAX_VOCAB, "the vocabulary bound is whole float4 per thread");
 
 // One workgroup samples a token from the V logits at lg (V % 4 == 0, V <= L3M_SAMPLE_MAX_VOCAB), given
-// their maximum gmax and the draw u: p_i = sample_weight(lg[i]), z = the double sum of all p_i, and the
-// token is the first i whose running double sum exceeds u * z, or V - 1 when none does (engine.c:364-379,
-// the reference path; its multi-rank path, engine.c:303-319, differs from it only in how the double sums
-// round). Thread t owns float4 [t per4, (t + 1) per4): it sums its range in order, a block scan gives each
-// range the sum of the ranges before it, and every thread walks its own range at once; the lowest
-// crossing wins. lg is read with device-coherent loads (other workgroups wrote it). dscr: NWE doubles,
-// iscr: NWE ints of LDS. Every thread gets the token.
-__device__ int sample_block(const float *lg, int V, float gmax, float temp, double u, double *dscr, int *iscr) {
-    const int tid = tidx(), lane = tid & 63, wave = wave_id();
+// their maximum gmax and the draw k (engine.c:364-379): the first i whose running sum of weights passes
+// k * 2^-53 times their total, or V - 1 when none does. Thread t owns float4 [t per4, (t + 1) per4); a
+// block scan gives each range the sum of those before it and every thread walks its own range at once;
+// the lowest crossing wins. lg is read with device-coherent loads (other workgroups wrote it). uscr: NWE
+// words, iscr: NWE ints of LDS. Every thread gets the token.
+__device__ int sample_block(const float *lg, int V, float gmax, float temp, unsigned long long k, unsigned long long *uscr, int *iscr) {
+    const int tid = tidx();
     const int V4 = V >> 2, per4 = (V4 + NTE - 1) / NTE, f0 = tid * per4;
     float p[4 * SAMPLE_F4];
 #pragma unroll
-    for (int k = 0; k < SAMPLE_F4; k++) {             // unconditional (clamped) loads, all in flight at once
-        const int f = f0 + k < V4 ? f0 + k : V4 - 1;
+    for (int j = 0; j < SAMPLE_F4; j++) {             // unconditional (clamped) loads, all in flight at once
+        const int f = f0 + j < V4 ? f0 + j : V4 - 1;
         const float4 v = ld16f<true>(lg, f);
-        p[4 * k] = v.x; p[4 * k + 1] = v.y; p[4 * k + 2] = v.z; p[4 * k + 3] = v.w;
+        p[4 * j] = v.x; p[4 * j + 1] = v.y; p[4 * j + 2] = v.z; p[4 * j + 3] = v.w;
     }
-    double sum = 0.0;
+    unsigned long long sum = 0;
 #pragma unroll
-    for (int k = 0; k < SAMPLE_F4; k++) {
-        if (k < per4) {                               // uniform
-            const bool in = f0 + k < V4;
+    for (int j = 0; j < SAMPLE_F4; j++) {
+        if (j < per4) {                               // uniform
+            const bool in = f0 + j < V4;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                p[4 * k + e] = in ? sample_weight(p[4 * k + e], gmax, temp) : 0.0f;
-                sum += (double)p[4 * k + e];
+                p[4 * j + e] = in ? sample_weight(p[4 * j + e], gmax, temp) : 0.0f;
+                sum += fixp(p[4 * j + e]);
             }
         }
     }
-    // the ranges before this thread's: an inclusive scan in the wavefront, then the wavefronts' totals in
-    // order (z is accumulated in that same order by every thread, so `before` is exactly its prefix)
-    double incl = sum;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double t = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += t;
-    }
-    double excl = __shfl_up(incl, 1, 64);
-    if (lane == 0) excl = 0.0;
-    if (lane == 63) dscr[wave] = incl;
-    __syncthreads();
-    double before = 0.0, z = 0.0;
-    for (int w = 0; w < NWE; w++) {
-        const double t = dscr[w];
-        if (w == wave) before = z;
-        z += t;
-    }
-    const double target = u * z;
-    double c = before + excl;
+    unsigned long long z;
+    unsigned long long c = block_scan_u64(sum, z, uscr);
     int cand = 0x7FFFFFFF;
 #pragma unroll
-    for (int k = 0; k < SAMPLE_F4; k++) {
-        if (k < per4) {
-            const bool in = f0 + k < V4;
+    for (int j = 0; j < SAMPLE_F4; j++) {
+        if (j < per4) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                c += (double)p[4 * k + e];
-                if (in && c > target && cand == 0x7FFFFFFF) cand = 4 * (f0 + k) + e;
+                c += fixp(p[4 * j + e]);
+                if (f0 + j < V4 && cand == 0x7FFFFFFF && crosses(c, k, z)) cand = 4 * (f0 + j) + e;
             }
         }
     }
-    cand = lanes_mini<64>(cand);
-    if (lane == 0) iscr[wave] = cand;
-    __syncthreads();
-    const int tok = lanes_mini<NWE>(iscr[tid & (NWE - 1)]);
-    __syncthreads();                                  // dscr and iscr are free again
+    const int tok = block_min_int(cand, iscr);
     return tok == 0x7FFFFFFF ? V - 1 : tok;
 }
 
@@ -1627,10 +1654,11 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
     reduce_partials(M.part_val, M.part_idx, gridDim.x, scr, v, idx);
     const float temp = M.samp->temp;
     if (temp > 0 && idx != 0x7FFFFFFF) {             // temperature sampling over this step's logits
-        unsigned long long st = M.samp->rng;
-        const double u = rand01(st);
-        idx = sample_block(M.logits + (size_t)(pos % M.nslots) * M.vocab, M.vocab, v, temp, u, (double *)scr, (int *)scr + 2 * NWE);
-        if (tidx() == 0) M.samp->rng = st;
+        unsigned long long st = M.samp->rng[0];
+        const unsigned long long k = draw53(st);
+        idx = sample_block(M.logits + (size_t)(pos % M.nslots) * M.vocab, M.vocab, v, temp, k, (unsigned long long *)scr,
+                           (int *)scr + 2 * NWE);
+        if (tidx() == 0) M.samp->rng[0] = st;
     }
     if (tidx() == 0) {
         if (advance) {
@@ -1667,7 +1695,8 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
 // and every workgroup leaves at its next wait, so the grid always drains.
 enum { SY_ATTN = 0, SY_FFN = 64, SY_XF = 128, SY_ABORT = L3M_SYNC_ABORT, SY_TOKEN = 208, SY_TICKET = 224, SY_HEAD_TICKET = 240,
        SY_SLOTS = 256 };
-static_assert(L3M_SYNC_WORDS == SY_SLOTS + 2 * L3M_MAX_HEAD_WGS && L3M_MAX_HEAD_WGS == 256, "keys follow the flag words");
+constexpr int SY_SUMS = SY_SLOTS + 2 * L3M_MAX_HEAD_WGS;   // slice totals (sampling) follow the keys
+static_assert(L3M_SYNC_WORDS == SY_SUMS + 2 * L3M_MAX_HEAD_WGS && L3M_MAX_HEAD_WGS == 256, "keys and totals follow the flag words");
 
 __device__ __forceinline__ unsigned xcc_id() {
     unsigned x;
@@ -1936,6 +1965,104 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
     return true;
 }
 
+// Temperature sampling of step s over the head workgroups, in the reference's multi-rank form
+// (engine.c:290-319; the rules of engine.c:284-287 and 364-379). Head workgroup h, whose slice holds
+// rows [r0, r0 + nrow) with their logits in LDS (lgv), after it stored its key:
+//  1. waits for every key and takes the step's maximum from the winning one;
+//  2. stores its slice's weight total (exact, fixp) tagged with the step in its slot;
+//  3. waits for every slot, draws k from its own copy of the generator, and finds the slice where the
+//     running total passes k * 2^-53 times the grand total;
+//  4. if that slice is its own, walks it and publishes the token in the token word.
+// Every workgroup draws once per sampled step, so the copies of the generator stay equal. Returns false
+// when the run is being abandoned.
+__device__ __forceinline__ unsigned sum_tag(int s) { return (unsigned)(s % 63) + 1; }   // 6 bits: totals < 2^58
+__device__ bool sample_step(const l3m_dmodel &M, const l3m_run &R, int h, int s, int nrow, int r0, uint8_t *smem) {
+    const int tid = tidx(), lane = tid & 63;
+    const LdsH LH = lds_h(M.head.dtype, M.dim, M.head.nb, R.head_tpw);
+    const float *lgv = (const float *)(smem + LH.lgv);
+    unsigned long long *uscr = (unsigned long long *)(smem + LH.scr);
+    int *iscr = (int *)(uscr + NWE);
+    const float temp = R.temp;
+    // 1. the step's maximum
+    if (tid < 64) {
+        const uint64_t key = poll_keys((const uint64_t *)(R.sync + SY_SLOTS), R.n_head, s, R.sync + SY_ABORT, R.spin_limit);
+        if (tid == 0) uscr[0] = key;
+    }
+    __syncthreads();
+    const uint64_t key = uscr[0];
+    __syncthreads();
+    if (key == ~0ull) return false;
+    const float gmax = key_value(key);
+    // 2. this slice's total (one row per thread: nrow <= 16 * 64 <= NTE)
+    const unsigned long long w = tid < nrow ? fixp(sample_weight(lgv[tid], gmax, temp)) : 0;
+    unsigned long long total;
+    const unsigned long long before = block_scan_u64(w, total, uscr);
+    unsigned long long *sums = (unsigned long long *)(R.sync + SY_SUMS);
+    if (tid == 0) __hip_atomic_store(gw(sums + h), (unsigned long long)sum_tag(s) << 58 | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // 3. every slice's total, the draw, the owner slice
+    if (tid < 64) {
+        const unsigned tag = sum_tag(s);
+        unsigned long long v[4];
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        bool ok = true;
+        for (unsigned spin = 0;; spin++) {
+            bool all = true;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                v[r] = __hip_atomic_load(gp<unsigned long long>(sums + lane + 64 * r), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int r = 0; r < 4; r++) all = all && (lane + 64 * r >= R.n_head || (unsigned)(v[r] >> 58) == tag);
+            if (__all(all)) break;
+            if (!keep_waiting(spin, t0, R.sync + SY_ABORT, R.spin_limit)) { ok = false; break; }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        // slice j = lane + 64 r, in order: its running total through it, and the grand total
+        unsigned long long incl[4], carry = 0;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const unsigned long long sj = lane + 64 * r < R.n_head ? v[r] & ((1ull << 58) - 1) : 0;
+            unsigned long long ex;
+            incl[r] = carry + lanes_scan_u64(sj, ex);
+            carry += __shfl(incl[r] - carry, 63, 64);
+        }
+        const unsigned long long z = carry;
+        unsigned long long st = __hip_atomic_load(gp<unsigned long long>(&M.samp->rng[h]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long k = draw53(st);
+        int owner = 0x7FFFFFFF;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (lane + 64 * r < R.n_head && owner == 0x7FFFFFFF && crosses(incl[r], k, z)) owner = lane + 64 * r;
+        owner = lanes_mini<64>(owner);
+        if (lane == 0) {
+            __hip_atomic_store(gw(&M.samp->rng[h]), st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            iscr[0] = ok ? owner : -1;
+            uscr[1] = k;
+            uscr[2] = z;
+        }
+        // the running total before the owner slice, for the owner
+        unsigned long long base = 0;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const unsigned long long sj = lane + 64 * r < R.n_head ? v[r] & ((1ull << 58) - 1) : 0;
+            if (lane + 64 * r == owner) base = incl[r] - sj;
+        }
+        if (lane + 64 * 0 == owner || lane + 64 * 1 == owner || lane + 64 * 2 == owner || lane + 64 * 3 == owner) uscr[3] = base;
+    }
+    __syncthreads();
+    const int owner = iscr[0];
+    const unsigned long long k = uscr[1], z = uscr[2], base = uscr[3];
+    __syncthreads();
+    if (owner < 0) return false;
+    // 4. the owner walks its slice; with no owner (a zero grand total) head 0 answers the last index
+    if (owner == h || (owner == 0x7FFFFFFF && h == 0)) {
+        const int cand = owner == h && tid < nrow && crosses(base + before + w, k, z) ? tid : 0x7FFFFFFF;
+        const int first = block_min_int(cand, iscr);
+        const int tok = first == 0x7FFFFFFF ? (owner == h ? r0 + nrow - 1 : M.vocab - 1) : r0 + first;
+        if (tid == 0) __hip_atomic_store(gw(R.sync + SY_TOKEN), token_word(s, tok), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return true;
+}
+
 // Head workgroup h: tiles [h * head_tpw, (h + 1) * head_tpw) of step s, once the final residual is out.
 template <int DT>
 __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, int h, int s) {
@@ -1953,32 +2080,12 @@ __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, 
     if (has_tiles) head_issue<DT>(wt, V);
     if (!wait_flags<4>(R.sync + SY_XF, M.n_chunks, (unsigned)s + 1, R.sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
     const float temp = R.temp;
-    if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx, temp > 0);
+    float *keep = temp > 0 ? (float *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).lgv) : nullptr;
+    if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx, keep);
     if (tidx() == 0)
         __hip_atomic_store(gw((uint64_t *)(R.sync + SY_SLOTS) + h), argmax_key(v, idx, step_tag(s)), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-    if (h == 0 && temp > 0) {
-        // Temperature sampling: head workgroup 0 takes every key (so every logit of the step is in memory:
-        // each workgroup's logit stores completed before its key), then the whole row of logits, and
-        // publishes the token in the token word. Its weight registers are free by now.
-        double *dscr = (double *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).scr);
-        int *iscr = (int *)(dscr + NWE);
-        if (tidx() < 64) {
-            const uint64_t key = poll_keys((const uint64_t *)(R.sync + SY_SLOTS), R.n_head, s, R.sync + SY_ABORT, R.spin_limit);
-            if (tidx() == 0) { iscr[0] = (int)(uint32_t)key; iscr[1] = (int)(uint32_t)(key >> 32); }
-        }
-        __syncthreads();
-        const uint64_t key = (uint64_t)(uint32_t)iscr[1] << 32 | (uint32_t)iscr[0];
-        __syncthreads();
-        if (key == ~0ull) return false;
-        unsigned long long st = __hip_atomic_load(gp<unsigned long long>(&M.samp->rng), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const double u = rand01(st);
-        const int tok = sample_block(M.logits + (size_t)(pos % M.nslots) * M.vocab, M.vocab, key_value(key), temp, u, dscr, iscr);
-        if (tidx() == 0) {
-            __hip_atomic_store(gw(&M.samp->rng), st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(gw(R.sync + SY_TOKEN), token_word(s, tok), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    if (temp > 0 && !sample_step(M, R, h, s, has_tiles ? V.rows : 0, t0 * 16, smem)) return false;
     return true;
 }
 
