@@ -169,6 +169,34 @@ def sampled_rate(A, m, prompt, n_tokens, temperature=1.0):
     return {"temperature": temperature, "value": round(1e9 / ns, 1) if ns > 0 else None, "unit": "tok/s"}
 
 
+def prefill_figure(A, d, reps=5):
+    """Time to the first logits of the C5 workload (SmolLM2-135M-shaped q8_0, its 64-token seeded prompt):
+    the batched prefill against token-by-token decode steps (L3M_PREFILL=0), median of reps; a side figure."""
+    cfg = A.CONFIGS["smollm2"]
+    path = A.write_model(Path(d) / "smollm2-q8_0.l3m", cfg, dtype="q8_0", seed=1)
+    ids = A.prompt(1, cfg.vocab, cfg.n_prompt)
+    out = {"config": "smollm2-q8_0", "prompt": len(ids)}
+    for key, env in (("ms_prefill", None), ("ms_token_by_token", "0")):
+        if env is None:
+            os.environ.pop("L3M_PREFILL", None)
+        else:
+            os.environ["L3M_PREFILL"] = env
+        m = A.Model(path)
+        m.generate(ids, 0)
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            m.generate(ids, 0)
+            A.lib().l3m_dev_sync()
+            times.append((time.perf_counter() - t0) * 1e3)
+        out[key] = round(sorted(times)[reps // 2], 3)
+        if env is None:
+            out["prefilled_positions"] = m.prefilled
+        m.close()
+    os.environ.pop("L3M_PREFILL", None)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -179,6 +207,7 @@ def main():
     ap.add_argument("--matvec", default="bf16,q8_0,q4_0,mxfp4", help="dtypes for the matvec microbench ('' to skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="reference CPU sample length (0 to skip)")
     ap.add_argument("--sample-temp", type=float, default=1.0, help="temperature of the sampled-decode side figure (0 to skip)")
+    ap.add_argument("--prefill", type=int, default=1, help="time the SmolLM2 64-token prefill side figure (0 to skip)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the plain copy kernel once over this many MiB (counter calibration under rocprofv3)")
     a = ap.parse_args()
@@ -229,6 +258,10 @@ def main():
         m.close()
         dom = decode or max(kt, key=lambda r: r["us_per_token"])
         cpu = cpu_baseline(path, prompt, a.cpu_seconds) if a.cpu_seconds > 0 else None
+        prefill = prefill_figure(A, d) if a.prefill else None
+        if prefill:
+            log(f"bench: SmolLM2 q8_0 64-token prompt to first logits: {prefill['ms_prefill']} ms batched, "
+                f"{prefill['ms_token_by_token']} ms token by token")
         if cpu:
             log(f"bench: reference CPU {cpu['value']} tok/s on {cpu['cores']} cores")
     matvec = matvec_bench(A, [s for s in a.matvec.split(",") if s]) if a.matvec else None
@@ -255,6 +288,7 @@ def main():
         "weight_GBs_per_token": round(wbytes * value * 1e-9, 1) if wbytes else None,
         "matvec": matvec,
         "sampled_decode": sampled,
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -142,6 +142,9 @@ int    l3m_decode_persistent(const l3m_model *m);
 // [vocab]: positions within the last 64 that call ran; -1 otherwise. An inspection hook (the sampled and
 // greedy tokens are checked against the logits they came from).
 int    l3m_logits_at(const l3m_model *m, int pos, float *out);
+// Prompt positions the last generate call ran as one batched prefill (0: token by token). Prompts of at
+// least L3M_PREFILL_MIN (default 8) tokens on q8_0 and q4_0 bodies are prefilled unless L3M_PREFILL=0.
+int    l3m_prefill_positions(const l3m_model *m);
 
 // Synthetic .l3m models (seeded, host-independent bytes).
 typedef struct {

@@ -130,6 +130,27 @@ int      l3m_step_slots(int dtype, int which);   // weight slots per lane (matri
 int      l3m_step_a_dtype(int dtype);            // storage dtype of a step kernel's matrix A for a body of dtype
 int l3m_step_enqueue(const l3m_dmodel *m, const l3m_dlayer *layers, int with_head, void *stream);
 
+// Batched prompt prefill: the full matrices of each layer as q8_0 lane-tile planes (q4_0 widened), and
+// the activation buffers of up to ctx tokens.
+typedef struct {
+    l3m_dmat     qkv;            // (n_heads + 2 n_kv) hd rows (q, then k, then v) x dim
+    l3m_dmat     wo;             // dim x n_heads hd
+    l3m_dmat     gu;             // 2 ffn rows (gate, then up) x dim
+    l3m_dmat     down;           // dim x ffn
+    const float *attn_norm, *ffn_norm;
+} l3m_pflayer;
+typedef struct {
+    float   *x;                  // [ctx][dim] residual stream
+    uint8_t *act;                // [ctx][astride] int8 prep of each token's matrix input
+    float   *qkv;                // [ctx][(n_heads + 2 n_kv) hd]
+    float   *att;                // [ctx][n_heads hd]
+    float   *gu;                 // [ctx][2 ffn]
+    int      astride;
+} l3m_pfbuf;
+// K/V rows of positions 0..P-1 of every layer from the token ids on the device (m->tokens); the last
+// layer's FFN is skipped (nothing reads it). -1 on a launch error.
+int l3m_prefill(const l3m_dmodel *m, const l3m_pflayer *layers, const l3m_pfbuf *b, int P, void *stream);
+
 // The persistent decode kernel (one cooperative launch for R->nsteps steps; layers_dev in device memory).
 int l3m_dev_cus(void);
 // The XCD each block of a cooperative grid of `grid` 1024-thread workgroups with lds bytes lands on

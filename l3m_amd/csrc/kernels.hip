@@ -2140,6 +2140,168 @@ __global__ void __launch_bounds__(NTE) k_where(int *out) {
     if (tidx() == 0) out[blockIdx.x] = (int)xcc_id();
 }
 
+// ------------------------------------------------------------------ batched prompt prefill
+// The prompt positions before the last one, all at once: per layer, the same
+// operations as the decode step (engine.c:230-275) on P tokens, with the matrices as int8 GEMMs on the
+// matrix cores. The decode path then runs from the last prompt position on, over the K/V rows these
+// kernels wrote. Weights are q8_0 lane-tile planes of the full matrices (q4_0 widened exactly); the
+// activations of token t are its own int8 prep (act_size bytes at t * astride), as the decode step
+// prepares them.
+
+// x[t] = the embedding row of tokens[t] (engine.c:236), t < P; one workgroup per token.
+__global__ void __launch_bounds__(NTE) k_pf_embed(l3m_dmat embed, const int32_t *tokens, int dim, float *x) {
+    const int t = blockIdx.x, f = tidx();
+    if (4 * f < dim) ((float4 *)(x + (size_t)t * dim))[f] = lt_elem4(embed, tokens[t], 4 * f);
+}
+
+// act[t] = the int8 prep of RMSNorm(x[t]) * w (engine.c:241, 261); one workgroup per token.
+__global__ void __launch_bounds__(NTE) k_pf_norm_prep(const float *x, const float *w, int dim, float eps, uint8_t *act, int astride) {
+    __shared__ float scr[32];
+    const int t = blockIdx.x, f = tidx(), own = 4 * f < dim ? f : 0;
+    const float4 xv = 4 * f < dim ? ((const float4 *)(x + (size_t)t * dim))[own] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 nw = ((const float4 *)w)[own];
+    Red red{scr, 0};
+    norm_prep<L3M_Q8_0>(xv, nw, dim, kpad(dim), eps, act + (size_t)t * astride, red);
+}
+
+// act[t] = the int8 prep of y[t][0..k) (the attention output before Wo); one workgroup per token.
+__global__ void __launch_bounds__(NTE) k_pf_prep(const float *y, int ystride, int k, uint8_t *act, int astride) {
+    const int t = blockIdx.x, f = tidx();
+    const float4 v = 4 * f < k ? ((const float4 *)(y + (size_t)t * ystride))[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    prep_owned<L3M_Q8_0>(v, act + (size_t)t * astride, kpad(k));
+}
+
+// act[t] = the int8 prep of up * silu(gate) (ops.c:49-51) from gu[t] = [gate 0..ffn) | up 0..ffn)].
+__global__ void __launch_bounds__(NTE) k_pf_silu_prep(const float *gu, int ffn, uint8_t *act, int astride) {
+    const int t = blockIdx.x, f = tidx();
+    float4 h = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * f < ffn) {
+        const float4 g = ((const float4 *)(gu + (size_t)t * 2 * ffn))[f], u = ((const float4 *)(gu + (size_t)t * 2 * ffn + ffn))[f];
+        h = make_float4(silu_mul(u.x, g.x), silu_mul(u.y, g.y), silu_mul(u.z, g.z), silu_mul(u.w, g.w));
+    }
+    prep_owned<L3M_Q8_0>(h, act + (size_t)t * astride, kpad(ffn));
+}
+
+// y[t][r] = sum over blocks b of d_w[r][b] * s_t[b] * (the int8 dot of row r and token t over block b):
+// the q8_0 gemv of every token at once (kernels_scalar.c:30-45), with the integer dots on
+// v_mfma_i32_16x16x32_i8 (one 32-input block per product). A workgroup takes one 16-row tile and 64
+// tokens, one wavefront per 16 tokens: lane l holds weights of row l % 16 and activations of token
+// l % 16, 8 bytes each at byte 8 (l / 16) of the block, and gets rows 4 (l / 16) + i of that token. Eight
+// blocks are loaded before their products (clamped indices, masked), so the loads overlap. add: y += the
+// result (the residual adds, engine.c:259, 275), else y = it.
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+constexpr int PF_BATCH = 8;
+__global__ void __launch_bounds__(256) k_pf_gemm(l3m_dmat W, const uint8_t *act, int astride, int P, float *y, int ystride, int add) {
+    const int lane = tidx() & 63, tile = blockIdx.x, tg = blockIdx.y * 4 + wave_id();
+    if (tg * 16 >= P) return;                                   // whole wavefronts past the tokens
+    const int nb = W.nb, kp = 32 * nb, quarter = lane >> 4, col = lane & 15;
+    const int tok = tg * 16 + col < P ? tg * 16 + col : P - 1;
+    const uint8_t *wq = (const uint8_t *)W.q + (size_t)tile * nb * 512 + col * 32 + quarter * 8;
+    const uint16_t *ws = (const uint16_t *)W.s + (size_t)tile * nb * 16 + quarter * 4;
+    const uint8_t *aq = act + (size_t)tok * astride + quarter * 8;
+    const float *as = (const float *)(act + (size_t)tok * astride + kp);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < nb; b0 += PF_BATCH) {
+        long a8[PF_BATCH], x8[PF_BATCH];
+        u32x2 sw[PF_BATCH];
+        float sa[PF_BATCH];
+#pragma unroll
+        for (int i = 0; i < PF_BATCH; i++) {
+            const int b = b0 + i < nb ? b0 + i : nb - 1;
+            a8[i] = *gp<long>(wq + (size_t)b * 512);
+            x8[i] = *gp<long>(aq + (size_t)b * 32);
+            sw[i] = *gp<u32x2>(ws + (size_t)b * 16);
+            sa[i] = *gp<float>(as + b);
+        }
+#pragma unroll
+        for (int i = 0; i < PF_BATCH; i++) {
+            const v4i32 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a8[i], x8[i], v4i32{0, 0, 0, 0}, 0, 0, 0);
+            const float m = b0 + i < nb ? sa[i] : 0.f;
+            acc[0] += (float)c[0] * (f16_f32(sw[i].x & 0xFFFF) * m);
+            acc[1] += (float)c[1] * (f16_f32(sw[i].x >> 16) * m);
+            acc[2] += (float)c[2] * (f16_f32(sw[i].y & 0xFFFF) * m);
+            acc[3] += (float)c[3] * (f16_f32(sw[i].y >> 16) * m);
+        }
+    }
+    const int t = tg * 16 + col;
+    if (t < P) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = tile * 16 + 4 * quarter + i;
+            if (r < W.rows) {
+                float *o = y + (size_t)t * ystride + r;
+                *o = add ? *o + acc[i] : acc[i];
+            }
+        }
+    }
+}
+
+// RoPE on the q and k rows of every token (ops.c:29-40, angles of position t from the host table), then
+// the k and v rows rounded to bf16 into the cache (engine.c:247-248); q stays in qkv for the attention.
+__global__ void __launch_bounds__(256) k_pf_rope_kv(float *qkv, int P, int n_heads, int n_kv, int hd, int ctx, int layer,
+                                                    const float *rope, uint16_t *kc, uint16_t *vc) {
+    const int t = blockIdx.x, nq = n_heads * hd, nk = n_kv * hd, width = nq + 2 * nk;
+    float *row = qkv + (size_t)t * width;
+    const float2 *cs = (const float2 *)(rope + (size_t)t * hd);
+    for (int i = tidx(); i < (nq + nk) / 2; i += blockDim.x) {   // pairs (2i, 2i+1) of q, then of k
+        const int e = 2 * i, j = (e < nq ? e : e - nq) % hd;
+        const float2 c = cs[j >> 1];
+        const float a = row[e], b = row[e + 1];
+        row[e] = a * c.x - b * c.y;
+        row[e + 1] = a * c.y + b * c.x;
+    }
+    __syncthreads();
+    for (int i = tidx(); i < 2 * nk; i += blockDim.x) {
+        const int kv = i < nk ? 0 : 1, r = i - kv * nk, h = r / hd, j = r - h * hd;
+        (kv ? vc : kc)[(((size_t)layer * n_kv + h) * ctx + t) * hd + j] = f32_bf16(row[nq + i]);
+    }
+}
+
+// Attention of token t, head h over positions 0..t (ops.c:42-73): one wavefront per (t, h), positions in
+// chunks of 64 (a lane per position) with a running maximum and sum; then each lane sums its output
+// dims over the chunk's weights. q from qkv (after RoPE), K and V from the cache as bf16.
+__global__ void __launch_bounds__(64) k_pf_attend(const float *qkv, int P, int n_heads, int n_kv, int hd, int ctx, int layer,
+                                                  float scale, const uint16_t *kc, const uint16_t *vc, float *att) {
+    __shared__ float qs[256], ps[64];
+    const int t = blockIdx.x, h = blockIdx.y, lane = tidx(), hpk = n_heads / n_kv, kv = h / hpk;
+    const int width = n_heads * hd + 2 * n_kv * hd;
+    for (int d = lane; d < hd; d += 64) qs[d] = qkv[(size_t)t * width + h * hd + d];
+    __syncthreads();
+    const uint16_t *K = kc + ((size_t)layer * n_kv + kv) * ctx * hd, *V = vc + ((size_t)layer * n_kv + kv) * ctx * hd;
+    float m = -INFINITY, l = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};   // output dims lane, lane + 64, ... (hd <= 256)
+    for (int p0 = 0; p0 <= t; p0 += 64) {
+        const int p = p0 + lane;
+        float sc = -INFINITY;
+        if (p <= t) {
+            float dot = 0.f;
+            for (int d = 0; d < hd; d++) dot += qs[d] * bf16_f32(K[(size_t)p * hd + d]);
+            sc = dot * scale;
+        }
+        const float cm = lanes_max<64>(sc), nm = fmaxf(m, cm);
+        const float w = p <= t ? expf(sc - nm) : 0.f, rescale = expf(m - nm);
+        l = l * rescale + lanes_sum<64>(w);
+        ps[lane] = w;
+        __syncthreads();
+        const int n = t - p0 + 1 < 64 ? t - p0 + 1 : 64;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int d = lane + 64 * i;
+            if (d < hd) {
+                float acc = o[i] * rescale;
+                for (int j = 0; j < n; j++) acc += ps[j] * bf16_f32(V[(size_t)(p0 + j) * hd + d]);
+                o[i] = acc;
+            }
+        }
+        m = nm;
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int d = lane + 64 * i;
+        if (d < hd) att[(size_t)t * n_heads * hd + h * hd + d] = o[i] / l;
+    }
+}
+
 // ----------------------------------------------------------------------------------------- runtime
 
 char g_err[512];
@@ -2401,6 +2563,35 @@ int l3m_step_a_dtype(int dtype) {
 int l3m_step_slots(int dtype, int which) {
     if (which) return dtype == L3M_F32 ? nslot_b<L3M_F32>() : dtype == L3M_BF16 ? nslot_b<L3M_BF16>() : dtype == L3M_Q8_0 ? nslot_b<L3M_Q8_0>() : nslot_b<L3M_Q4_0>();
     return dtype == L3M_F32 ? nslot_a<L3M_F32>() : dtype == L3M_BF16 ? nslot_a<L3M_BF16>() : dtype == L3M_Q8_0 ? nslot_a<L3M_Q8_0>() : nslot_a<L3M_Q4_0>();
+}
+
+int l3m_prefill(const l3m_dmodel *M, const l3m_pflayer *L, const l3m_pfbuf *B, int P, void *stream) {
+    if (P < 1) return 0;
+    if (P > M->ctx || M->dim > 4 * NTE || M->ffn > 4 * NTE || M->n_heads * M->hd > 4 * NTE || M->hd > 256 || M->hd % 2)
+        return fail_msg("prefill: shape out of range");
+    hipStream_t st = as_stream(stream);
+    const int dim = M->dim, hd = M->hd, nq = M->n_heads * hd, width = nq + 2 * M->n_kv * hd;
+    auto gemm = [&](const l3m_dmat &W, float *y, int ystride, int add) {
+        hipLaunchKernelGGL(k_pf_gemm, dim3(W.tiles, (P + 63) / 64), dim3(256), 0, st, W, (const uint8_t *)B->act, B->astride, P, y, ystride, add);
+    };
+    hipLaunchKernelGGL(k_pf_embed, dim3(P), dim3(NTE), 0, st, M->embed, (const int32_t *)M->tokens, dim, B->x);
+    for (int l = 0; l < M->n_layers; l++) {
+        const l3m_pflayer &W = L[l];
+        hipLaunchKernelGGL(k_pf_norm_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->x, W.attn_norm, dim, M->eps, B->act, B->astride);
+        gemm(W.qkv, B->qkv, width, 0);
+        hipLaunchKernelGGL(k_pf_rope_kv, dim3(P), dim3(256), 0, st, B->qkv, P, M->n_heads, M->n_kv, hd, M->ctx, l, M->rope, M->kc, M->vc);
+        hipLaunchKernelGGL(k_pf_attend, dim3(P, M->n_heads), dim3(64), 0, st, (const float *)B->qkv, P, M->n_heads, M->n_kv, hd, M->ctx, l,
+                           M->att_scale, (const uint16_t *)M->kc, (const uint16_t *)M->vc, B->att);
+        if (l == M->n_layers - 1) break;              // the last layer's residual feeds only the head
+        hipLaunchKernelGGL(k_pf_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->att, nq, nq, B->act, B->astride);
+        gemm(W.wo, B->x, dim, 1);
+        hipLaunchKernelGGL(k_pf_norm_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->x, W.ffn_norm, dim, M->eps, B->act, B->astride);
+        gemm(W.gu, B->gu, 2 * M->ffn, 0);
+        hipLaunchKernelGGL(k_pf_silu_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->gu, M->ffn, B->act, B->astride);
+        gemm(W.down, B->x, dim, 1);
+    }
+    CKL("prefill");
+    return 0;
 }
 
 int l3m_step_enqueue(const l3m_dmodel *M, const l3m_dlayer *layers, int with_head, void *stream) {
