@@ -197,6 +197,28 @@ def prefill_figure(A, d, reps=5):
     return out
 
 
+def probes(A):
+    """The residency and exchange probes: rows of printable results."""
+    lib, out = A.lib(), {"stream": [], "exchange": [], "graph_node_us": None}
+    v = C.c_double()
+    for xcds in (1, 8):
+        for mib in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024):
+            total = mib << 20
+            per = total // (32 * xcds)
+            if per < 4096 or per % 16:
+                continue
+            passes = max(1, (256 << 20) // total)
+            if lib.l3m_probe_stream(per, xcds, 32, passes, C.byref(v)) == 0:
+                out["stream"].append({"xcds": xcds, "workgroups": 32 * xcds, "working_set_mib": mib, "GBs": round(v.value, 1)})
+    for same in (1, 0):
+        for n in (2, 4, 8, 16, 28, 32):
+            if lib.l3m_probe_exchange(n, same, 768, 2000, C.byref(v)) == 0:
+                out["exchange"].append({"workgroups": n, "same_xcd": bool(same), "dim": 768, "us_per_round": round(v.value, 3)})
+    if lib.l3m_probe_graph_node(256, 20, C.byref(v)) == 0:
+        out["graph_node_us"] = round(v.value, 3)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -208,6 +230,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="reference CPU sample length (0 to skip)")
     ap.add_argument("--sample-temp", type=float, default=1.0, help="temperature of the sampled-decode side figure (0 to skip)")
     ap.add_argument("--prefill", type=int, default=1, help="time the SmolLM2 64-token prefill side figure (0 to skip)")
+    ap.add_argument("--probes", action="store_true", help="run only the residency and exchange probes, one JSON line")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the plain copy kernel once over this many MiB (counter calibration under rocprofv3)")
     a = ap.parse_args()
@@ -217,6 +240,9 @@ def main():
         sys.exit(2)
 
     import l3m_amd as A
+    if a.probes:
+        print(json.dumps({"probes": probes(A)}), flush=True)
+        return
     cfg = A.CONFIGS[a.config]
     dtype = a.dtype or cfg.dtype
     with tempfile.TemporaryDirectory() as d:

@@ -146,6 +146,15 @@ int    l3m_logits_at(const l3m_model *m, int pos, float *out);
 // least L3M_PREFILL_MIN (default 8) tokens on q8_0 and q4_0 bodies are prefilled unless L3M_PREFILL=0.
 int    l3m_prefill_positions(const l3m_model *m);
 
+// Probes, the GPU analogues of the reference's bench/residency.c:31-97 and bench/exchange.c:22-44 (no
+// counterpart in its library): bandwidth of workgroups streaming their own shards (per_xcd workgroups on
+// each of the first xcds XCDs, bytes_per_wg each, warm, passes per launch), in GB/s; microseconds per
+// exchange round of n workgroups (each writes its slice of a dim-float vector, flags, waits for all flags,
+// reads the vector; on one XCD or across XCDs); microseconds per node of a hipGraph of empty kernels.
+int    l3m_probe_stream(size_t bytes_per_wg, int xcds, int per_xcd, int passes, double *gbs);
+int    l3m_probe_exchange(int n, int same_xcd, int dim, int rounds, double *us_per_round);
+int    l3m_probe_graph_node(int nodes, int reps, double *us_per_node);
+
 // Synthetic .l3m models (seeded, host-independent bytes).
 typedef struct {
     const char *arch;

@@ -2302,6 +2302,93 @@ __global__ void __launch_bounds__(64) k_pf_attend(const float *qkv, int P, int n
     }
 }
 
+// ------------------------------------------------------------------ residency and exchange probes
+// The GPU analogues of the reference's bench/residency.c (every core streams its own shard, at each
+// working-set size) and bench/exchange.c (ns per barrier and exchange over a set of cores), which back the
+// layout and hand-over choices of the decode kernel. Launched with one workgroup per CU; the workgroups on
+// the chosen XCDs take tickets per XCD and work, the others leave at once.
+
+// Shard streaming: workgroup (x, t) of the first `xcds` XCDs (t < per_xcd tickets) reads its n16 16-byte
+// words `passes` times. sink keeps the loads alive.
+__global__ void __launch_bounds__(NTE) k_probe_stream(const u32x4 *buf, size_t n16, int passes, int xcds, int per_xcd,
+                                                      unsigned *tickets, unsigned *sink) {
+    __shared__ int shard;
+    if (tidx() == 0) {
+        const unsigned x = xcc_id();
+        int sh = -1;
+        if ((int)x < xcds) {
+            const unsigned t = __hip_atomic_fetch_add(gw(tickets + x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((int)t < per_xcd) sh = (int)x * per_xcd + (int)t;
+        }
+        shard = sh;
+    }
+    __syncthreads();
+    if (shard < 0) return;
+    const u32x4 *p = buf + (size_t)shard * n16;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (int pass = 0; pass < passes; pass++)
+        for (size_t i = tidx(); i < n16; i += NTE) acc ^= gp<u32x4>(p)[i];
+    const unsigned v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (v == 0x9E3779B9u) gw(sink)[0] = v;            // practically never: keeps the loads
+}
+
+// Exchange rounds among n workgroups (on XCD 0 when same_xcd, else dealt round-robin over the XCDs):
+// round i, each writes its slice of a dim-float vector (two copies by parity), stores flag = i + 1 after its
+// stores are in L2 (device-scope stores when the group spans XCDs), waits for every flag, then reads the
+// whole vector. Workgroup 0 times `rounds` rounds with the 100 MHz clock. Every wait is bounded:
+// past `limit` ticks the abort word is raised and all leave.
+__global__ void __launch_bounds__(NTE) k_probe_exchange(float *vec, int dim, int n, int same_xcd, int rounds, unsigned *flags,
+                                                        unsigned *tickets, unsigned long long *out, unsigned long long limit) {
+    __shared__ int role, ok;
+    if (tidx() == 0) {
+        const unsigned x = xcc_id();
+        int r = -1;
+        if (same_xcd) {
+            if (x == 0) {
+                const unsigned t = __hip_atomic_fetch_add(gw(tickets), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((int)t < n) r = (int)t;
+            }
+        } else {
+            const unsigned t = __hip_atomic_fetch_add(gw(tickets + 1 + x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((int)(t * 8 + x) < n) r = (int)(t * 8 + x);   // member t*8 + x: round-robin over the 8 XCDs
+        }
+        role = r;
+        ok = 1;
+    }
+    __syncthreads();
+    const int me = role;
+    if (me < 0) return;
+    unsigned *abort_flag = flags + 64;
+    const int lo = dim * me / n, hi = dim * (me + 1) / n;
+    float acc = 0.f;
+    unsigned long long t0 = 0;
+    for (int i = 0; i < rounds; i++) {
+        if (i == 1 && me == 0 && tidx() == 0) t0 = __builtin_amdgcn_s_memrealtime();   // round 0 warms up
+        float *v = vec + (size_t)(i & 1) * dim;
+        for (int j = lo + tidx(); j < hi; j += NTE) {
+            if (same_xcd) gw(v)[j] = (float)(i + j);
+            else __hip_atomic_store(gw((unsigned *)v + j), __float_as_uint((float)(i + j)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tidx() == 0) __hip_atomic_store(gw(flags + me), (unsigned)i + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tidx() < 64) {
+            const unsigned long long w0 = __builtin_amdgcn_s_memrealtime();
+            for (unsigned spin = 0;; spin++) {
+                const unsigned f = (int)tidx() < n ? ld_flag(flags + tidx()) : (unsigned)i + 1;
+                if (__all(f >= (unsigned)i + 1)) break;
+                if (!keep_waiting(spin, w0, abort_flag, limit)) { ok = 0; break; }
+            }
+        }
+        __syncthreads();
+        if (!ok) return;
+        for (int j = tidx(); j < dim; j += NTE) acc += __uint_as_float(__hip_atomic_load(gp<unsigned>((unsigned *)v + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    if (me == 0 && tidx() == 0) { out[0] = __builtin_amdgcn_s_memrealtime() - t0; out[1] = (unsigned long long)__float_as_uint(acc); }
+}
+
+__global__ void k_probe_empty() {}
+
 // ----------------------------------------------------------------------------------------- runtime
 
 char g_err[512];
@@ -2753,6 +2840,107 @@ void l3m_graphs_free(l3m_graphs *g) {
         if (g->g[w]) (void)hipGraphDestroy(g->g[w]);
     }
     free(g);
+}
+
+// ------------------------------------------------------------------ probes (host)
+
+int l3m_probe_stream(size_t bytes_per_wg, int xcds, int per_xcd, int passes, double *gbs) {
+    if (l3m_dev_init()) return -1;
+    if (bytes_per_wg < 16 || bytes_per_wg % 16 || xcds < 1 || xcds > 8 || per_xcd < 1 || per_xcd > 32 || passes < 1)
+        return fail_msg("probe_stream: bad arguments");
+    const size_t n16 = bytes_per_wg / 16, total = bytes_per_wg * (size_t)xcds * per_xcd;
+    void *buf = nullptr;
+    unsigned *aux = nullptr;
+    CK(hipMalloc(&buf, total));
+    if (hipMalloc(&aux, 64 * 4) != hipSuccess) { (void)hipFree(buf); return fail_msg("probe_stream: out of memory"); }
+    hipError_t e = hipMemsetAsync(buf, 0x5A, total, g_stream);
+    hipEvent_t a = nullptr, b = nullptr;
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    const int grid = l3m_dev_cus();
+    float ms = 0.f;
+    for (int rep = 0; rep < 2 && e == hipSuccess; rep++) {   // the first launch warms the caches
+        e = hipMemsetAsync(aux, 0, 64 * 4, g_stream);
+        if (e == hipSuccess && rep) e = hipEventRecord(a, g_stream);
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(k_probe_stream, dim3(grid), dim3(NTE), 0, g_stream, (const u32x4 *)buf, n16, passes, xcds, per_xcd, aux, aux + 32);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess && rep) e = hipEventRecord(b, g_stream);
+    }
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    unsigned got[8] = {0};
+    if (e == hipSuccess) e = hipMemcpy(got, aux, sizeof got, hipMemcpyDeviceToHost);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    (void)hipFree(buf); (void)hipFree(aux);
+    if (e != hipSuccess) return fail("probe_stream", e);
+    for (int x = 0; x < xcds; x++)
+        if ((int)got[x] < per_xcd) return fail_msg("probe_stream: an XCD has fewer CUs than requested");
+    *gbs = (double)total * passes / (ms * 1e6);
+    return 0;
+}
+
+int l3m_probe_exchange(int n, int same_xcd, int dim, int rounds, double *us_per_round) {
+    if (l3m_dev_init()) return -1;
+    if (n < 1 || n > 32 || dim < n || dim > (1 << 20) || rounds < 2) return fail_msg("probe_exchange: bad arguments");
+    float *vec = nullptr;
+    unsigned *aux = nullptr;
+    unsigned long long *out = nullptr;
+    CK(hipMalloc(&vec, 2 * (size_t)dim * 4));
+    if (hipMalloc(&aux, 256 * 4) != hipSuccess || hipMalloc(&out, 16) != hipSuccess) {
+        (void)hipFree(vec); (void)hipFree(aux); return fail_msg("probe_exchange: out of memory");
+    }
+    hipError_t e = hipMemsetAsync(aux, 0, 256 * 4, g_stream);
+    if (e == hipSuccess) e = hipMemsetAsync(out, 0, 16, g_stream);
+    unsigned *flags = aux, *tickets = aux + 128;
+    unsigned long long limit = 100000000ull, host_out[2] = {0, 0};
+    int grid = l3m_dev_cus();
+    void *args[] = {&vec, &dim, &n, &same_xcd, &rounds, &flags, &tickets, &out, &limit};
+    if (e == hipSuccess) e = hipLaunchCooperativeKernel((const void *)k_probe_exchange, dim3(grid), dim3(NTE), args, 0, g_stream);
+    unsigned abort_word = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(host_out, out, 16, hipMemcpyDeviceToHost, g_stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(&abort_word, flags + 64, 4, hipMemcpyDeviceToHost, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    (void)hipFree(vec); (void)hipFree(aux); (void)hipFree(out);
+    if (e != hipSuccess) return fail("probe_exchange", e);
+    if (abort_word || !host_out[0]) return fail_msg("probe_exchange: a wait timed out (not enough workgroups on the XCDs asked for)");
+    *us_per_round = (double)host_out[0] * 0.01 / (rounds - 1);
+    return 0;
+}
+
+int l3m_probe_graph_node(int nodes, int reps, double *us_per_node) {
+    if (l3m_dev_init()) return -1;
+    if (nodes < 1 || nodes > 4096 || reps < 1) return fail_msg("probe_graph_node: bad arguments");
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipStream_t cs = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    float ms = 0.f;
+    hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+        for (int i = 0; i < nodes; i++) hipLaunchKernelGGL(k_probe_empty, dim3(1), dim3(64), 0, cs);
+        e = hipStreamEndCapture(cs, &g);
+    }
+    if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    if (e == hipSuccess) e = hipGraphLaunch(ge, g_stream);                 // warm
+    if (e == hipSuccess) e = hipEventRecord(a, g_stream);
+    for (int r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ge, g_stream);
+    if (e == hipSuccess) e = hipEventRecord(b, g_stream);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
+    if (cs) (void)hipStreamDestroy(cs);
+    if (e != hipSuccess) return fail("probe_graph_node", e);
+    *us_per_node = 1e3 * ms / ((double)reps * nodes);
+    return 0;
 }
 
 }  // extern "C"
