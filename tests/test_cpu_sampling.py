@@ -82,3 +82,20 @@ def test_sampled_generation_matches_reference(models, oracle, reference, temp):
         assert ref_fast.generate(ids, 32, temperature=temp, seed=seed) == want
         seen.add(tuple(want))
     assert len(seen) > 1                              # the seed matters
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "q8_0", "q4_0"])
+def test_gpt2_variant_matches_reference(models, oracle, reference, dtype):
+    """The oracle's GPT-2 variant (LayerNorm with biases, learned positions, matrix biases, GELU MLP;
+    engine.c:236-275, ops.c:20-27, 53-56) against fpedd/l3m built from source: its reference path bit for
+    bit, its fast path to its own float rounding."""
+    cfg = A.Config("g2", dim=64, n_layers=2, n_heads=4, n_kv_heads=4, ffn_dim=256, vocab=256, ctx=64, dtype=dtype)
+    path = models.get(cfg, dtype, seed=3, std=0.08, arch="gpt2")
+    ids = A.prompt(3, cfg.vocab, 5)
+    r, o = reference.load(path, reference=True), oracle.load(path, ref=True)
+    assert r.generate(ids, 12) == o.generate(ids, 12)
+    assert np.array_equal(r.logits(), o.logits())
+    rf, of = reference.load(path, cpus=[0]), oracle.load(path)
+    assert rf.generate(ids, 12) == of.generate(ids, 12)
+    lr, lo = rf.logits(), of.logits()
+    assert np.abs(lr - lo).max() <= 1e-5 * np.abs(lr).max()
