@@ -20,7 +20,7 @@ typedef struct {
     unsigned write_kv;           // bit i: this group writes kv head kv0 + i into the cache
     int      att_wl;             // log2 of the most wavefronts one query head takes in the attention
     unsigned lds[10];            // LDS byte offsets of the attention block's regions (l3m_group_layout)
-    int      pad_[2];
+    const float *bqkv;           // GPT-2 variant: the biases of the qkv rows, in their order; else NULL
 } l3m_dgroup;
 
 // One chunk of a layer's FFN block: ffn rows [f0, f0 + nf), nf a multiple of 32.
@@ -30,12 +30,14 @@ typedef struct {
     int      f0, nf;
     unsigned lds[5];             // LDS byte offsets of the FFN block's regions (l3m_chunk_layout)
     int      pad_;
+    const float *bup;            // GPT-2 variant: b_up of rows f0.. (gate_up then holds the up rows only)
 } l3m_dchunk;
 
 typedef struct {
     const l3m_dgroup *groups;    // device arrays [n_groups], [n_chunks]
     const l3m_dchunk *chunks;
     const float      *attn_norm, *ffn_norm;
+    const float      *attn_norm_b, *ffn_norm_b, *bo, *bdown;   // GPT-2 variant; else NULL
 } l3m_dlayer;
 
 typedef struct {
@@ -63,6 +65,9 @@ typedef struct {
     l3m_dmat     embed, head;    // head may alias embed (tied)
     const float *norm;
     struct l3m_dsample *samp;    // temperature sampling: the generate call's temperature and random state
+    const float *norm_b;         // GPT-2 variant (gpt2 != 0): the final LayerNorm's bias,
+    const float *pos_embed;      // the learned position rows [ctx][dim]
+    int          gpt2, pad_g2;
 } l3m_dmodel;
 #define L3M_SAMPLE_MAX_VOCAB (64 * 1024)   // logits held in one workgroup's registers (64 per thread)
 

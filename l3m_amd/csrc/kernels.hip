@@ -929,6 +929,40 @@ __device__ __forceinline__ void norm_prep(float4 x, float4 nw, int k, int kp, fl
     __syncthreads();
 }
 
+// LayerNorm (ops.c:20-27: the mean, then the mean square deviation, s = 1/sqrt(var / n + eps),
+// y = (x - mean) * s * w + b) of the owned x, then its prep: the GPT-2 variant's norm. Two workgroup sums
+// (same slots and order of additions as norm_prep's), only past the first does x's mean exist.
+template <int DT>
+__device__ __forceinline__ void ln_prep(float4 x, const float *w, const float *b, int k, int kp, float eps, uint8_t *act, Red &red) {
+    const int wave = wave_id(), f = tidx();
+    const bool owner = wave * 256 < kp;
+    auto block_total = [&](float v) {
+        float *slot = red.scr + 16 * (red.k++ & 1);
+        const float part = owner ? lanes_sum<64>(v) : 0.f;
+        if ((f & 63) == 0) slot[wave] = part;
+        __syncthreads();
+        const float4 *sv = (const float4 *)slot;
+        const float4 a = sv[0], c = sv[1], d = sv[2], e = sv[3];
+        return (((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w))) + (((d.x + d.y) + (d.z + d.w)) + ((e.x + e.y) + (e.z + e.w)));
+    };
+    const float mean = block_total(x.x + x.y + x.z + x.w) / (float)k;
+    const bool in = 4 * f < k;
+    const float4 dv = in ? make_float4(x.x - mean, x.y - mean, x.z - mean, x.w - mean) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float var = block_total(dv.x * dv.x + dv.y * dv.y + dv.z * dv.z + dv.w * dv.w);
+    if (owner) {
+        const float s = 1.0f / sqrtf(var / (float)k + eps);
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (in) {
+            const float4 wv = ((const float4 *)w)[f], bv = ((const float4 *)b)[f];
+            y = make_float4(dv.x * s * wv.x + bv.x, dv.y * s * wv.y + bv.y, dv.z * s * wv.z + bv.z, dv.w * s * wv.w + bv.w);
+        }
+        prep_body<DT>(y, act, kp);
+    }
+    __syncthreads();
+}
+// GELU, tanh form (ops.c:53-56).
+__device__ __forceinline__ float gelu_tanh(float x) { return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x))); }
+
 // LDS regions of the step kernels (byte offsets, 16-aligned) from the layer geometry. `work` holds the
 // prologue's group sums, then the per-pair matvec results.
 // Matvec results take 64 bytes per (tile, block) pair; a wavefront writes whole groups of 4 pairs
@@ -1318,7 +1352,7 @@ __device__ __forceinline__ void attn_kv_window(const l3m_dmodel &M, const l3m_dg
 // The attention block of head group gi (engine.c:236-258) at `layer`, position pos: x = xb + the FFN
 // partials (layer 0: the embedding row of tokens[pos]), RMSNorm, prep, the group's q/k/v rows, RoPE,
 // bf16 K/V into the cache, attention, prep, the group's Wo columns -> po[gi]. Group 0 keeps x in xa.
-template <int DT, bool PRE>
+template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dgroup &G, int layer, int pos,
                                            int tok, int gi, AttnW<DT> &w, uint8_t *smem) {
     const int tid = tidx(), dim = M.dim, hd = M.hd, kp = kpad(dim);
@@ -1333,12 +1367,19 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     const ProGeom PG = pro_geom(M, 0);
     pro_load<PRE>(P, M.xb, M.pd, PG, Lw.attn_norm, M.embed, layer == 0, tok, M.rope + (size_t)pos * hd, hd);
     if constexpr (!PRE) attn_issue<DT>(w, G);
-    const float4 x = pro_finish<PRE>(P, M.pd, PG, layer == 0, (float4 *)work, gi == 0 ? M.xa : nullptr, cs, hd);
+    float4 x = pro_finish<PRE>(P, M.pd, PG, layer == 0, (float4 *)work, G2 && layer == 0 ? nullptr : gi == 0 ? M.xa : nullptr, cs, hd);
+    if constexpr (G2) {
+        if (layer == 0) {                             // the learned position row (engine.c:237), then kept
+            if (tid < (dim >> 2)) x = add4(x, ((const float4 *)(M.pos_embed + (size_t)pos * dim))[tid]);
+            if (gi == 0 && tid < (dim >> 2)) ((float4 *)M.xa)[tid] = x;
+        }
+    }
     // K, V rows 0..pos-1 (no dependence on this step). Issued after the prologue is consumed: a copy of
     // data-dependent length ahead of it would make the compiler wait for every load in flight there.
     // The persistent path issues it before it waits for the block's inputs (attn_kv_window).
     if (!PRE && M.kv_lds) kv_window_dma<false>(kvb, M, layer, G.kv0, G.nkv, pos);
-    norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
+    if constexpr (G2) ln_prep<DT>(x, Lw.attn_norm, Lw.attn_norm_b, dim, kp, M.eps, act, red);
+    else norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
 
     mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, act, kp, work);
     __syncthreads();
@@ -1351,7 +1392,8 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     const bool mfma_att = M.kv_lds && hd % 32 == 0 && 6 * nqd <= 4 * NWE * hd;
     __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
     rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner, bool lead) {
-        if (i < nqd + nkd) {
+        if constexpr (G2) y += G.bqkv[i];            // the GPT-2 variant's q, k, v biases; no RoPE
+        if (!G2 && i < nqd + nkd) {
             const int local = i < nqd ? i : i - nqd, head = (int)(((float)local + 0.5f) * inv_hd);
             const float2 c = ((const float2 *)cs)[(local - head * hd) >> 1];
             y = (i & 1) ? partner * c.y + y * c.x : y * c.x - partner * c.y;
@@ -1382,12 +1424,15 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     mv<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
     __syncthreads();
     float *po = M.po + (size_t)gi * dim;
-    rows_sum4(G.wo, work, dim, [&](int i, float y, float, bool lead) { if (lead) gw(po)[i] = y; });
+    rows_sum4(G.wo, work, dim, [&](int i, float y, float, bool lead) {
+        if constexpr (G2) y += gi == 0 ? Lw.bo[i] : 0.f;   // bo once, with group 0's partial
+        if (lead) gw(po)[i] = y;
+    });
 }
 
 // The FFN block of chunk ci (engine.c:259-275): x = xa + the attention partials, RMSNorm, prep, the
 // chunk's gate and up rows, SiLU(gate) * up, prep, its Wdown columns -> pd[ci]. Chunk 0 keeps x in xb.
-template <int DT, bool PRE>
+template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dchunk &C, int ci, FfnW<DT> &w,
                                           uint8_t *smem) {
     const int tid = tidx(), dim = M.dim, kp = kpad(dim);
@@ -1401,10 +1446,14 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     pro_load<PRE>(P, M.xa, M.po, PG, Lw.ffn_norm, M.embed, false, 0, nullptr, 0);     // x += proj (engine.c:259)
     if constexpr (!PRE) ffn_issue<DT>(w, C);
     const float4 x = pro_finish<PRE>(P, M.po, PG, false, (float4 *)work, ci == 0 ? M.xb : nullptr, nullptr, 0);
-    norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
+    if constexpr (G2) ln_prep<DT>(x, Lw.ffn_norm, Lw.ffn_norm_b, dim, kp, M.eps, act, red);
+    else norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
     mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
     __syncthreads();
-    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float, bool lead) { if (lead) gu[i] = y; });
+    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float, bool lead) {
+        if constexpr (G2) y += i < C.nf ? C.bup[i] : 0.f;   // the up rows only, with b_up
+        if (lead) gu[i] = y;
+    });
     __syncthreads();
     // h = up * silu(gate) (ops.c:49-51) for the owned 4 rows (gate tile t and up tile t interleave), prepared
     const int kf = kpad(C.nf);
@@ -1414,7 +1463,8 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int i = 4 * tid + e, gi = (2 * (i >> 4)) * 16 + (i & 15);
-            hh[e] = silu_mul(gu[gi + 16], gu[gi]);
+            if constexpr (G2) hh[e] = i < C.nf ? gelu_tanh(gu[i]) : 0.f;   // GELU(up) (engine.c:263-264)
+            else hh[e] = silu_mul(gu[gi + 16], gu[gi]);
         }
         hv = make_float4(hh[0], hh[1], hh[2], hh[3]);
     }
@@ -1422,7 +1472,10 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     mv<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, act2, kf, work);
     __syncthreads();
     float *pd = M.pd + (size_t)ci * dim;
-    rows_sum4(C.down, work, dim, [&](int i, float y, float, bool lead) { if (lead) gw(pd)[i] = y; });
+    rows_sum4(C.down, work, dim, [&](int i, float y, float, bool lead) {
+        if constexpr (G2) y += ci == 0 ? Lw.bdown[i] : 0.f;   // b_down once, with chunk 0's partial
+        if (lead) gw(pd)[i] = y;
+    });
 }
 
 // Tiles [t0, t0 + tpw) of the head as a matrix of their own (the last slice may be short).
@@ -1438,7 +1491,7 @@ __device__ __forceinline__ l3m_dmat head_slice(const l3m_dmodel &M, int t0, int 
 
 // Final norm and the head rows of slice V (tiles from t0) at position pos (engine.c:277-301): logits
 // into slot pos % nslots, and this slice's (max, lowest index) in v, idx for every thread.
-template <int DT, bool PRE>
+template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &V, int t0, int tpw, int pos, HeadW<DT> &w,
                                            uint8_t *smem, float &v, int &idx, float *keep = nullptr) {
     const int tid = tidx(), dim = M.dim, kp = kpad(dim);
@@ -1462,7 +1515,8 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
         x = pro_finish<false>(P, M.pd, PG, false, (float4 *)work, nullptr, nullptr, 0);
         nw = P.nw;
     }
-    norm_prep<DT>(x, nw, dim, kp, M.eps, act, red);
+    if constexpr (G2) ln_prep<DT>(x, M.norm, M.norm_b, dim, kp, M.eps, act, red);
+    else norm_prep<DT>(x, nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work);
     __syncthreads();
     // each row's logit from the lane that sums it: stored, and kept if it beats the lane's earlier rows
@@ -1610,28 +1664,28 @@ __device__ int sample_block(const float *lg, int V, float gmax, float temp, unsi
 
 // ------------------------------------------------------------------ the graph path: one kernel per block
 
-template <int DT>
+template <int DT, bool G2 = false>
 __global__ void __launch_bounds__(NTE) k_attn_block(l3m_dmodel M, l3m_dlayer Lw, int layer) {
     extern __shared__ __align__(16) uint8_t smem[];
     const l3m_dgroup G = Lw.groups[blockIdx.x];
     AttnW<DT> w;
     const int pos = *M.pos;
-    attn_block<DT, false>(M, Lw, G, layer, pos, layer ? 0 : M.tokens[pos], blockIdx.x, w, smem);
+    attn_block<DT, false, G2>(M, Lw, G, layer, pos, layer ? 0 : M.tokens[pos], blockIdx.x, w, smem);
 }
 
 // The last layer of a step without the head advances the position (nothing in this kernel reads it).
-template <int DT>
+template <int DT, bool G2 = false>
 __global__ void __launch_bounds__(NTE) k_ffn_block(l3m_dmodel M, l3m_dlayer Lw, int advance) {
     extern __shared__ __align__(16) uint8_t smem[];
     const l3m_dchunk C = Lw.chunks[blockIdx.x];
     FfnW<DT> w;
-    ffn_block<DT, false>(M, Lw, C, blockIdx.x, w, smem);
+    ffn_block<DT, false, G2>(M, Lw, C, blockIdx.x, w, smem);
     if (advance && blockIdx.x == 0 && tidx() == 0) *M.pos += 1;
 }
 
 // Each workgroup reduces its slice; the last one to finish reduces the partials, writes tokens[pos + 1],
 // resets the counter and (advance) moves pos on.
-template <int DT>
+template <int DT, bool G2 = false>
 __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tpw = M.head_tiles_per_wg, t0 = blockIdx.x * tpw, pos = *M.pos;
@@ -1639,7 +1693,7 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
     HeadW<DT> w;
     float v;
     int idx;
-    head_block<DT, false>(M, V, t0, tpw, pos, w, smem, v, idx);
+    head_block<DT, false, G2>(M, V, t0, tpw, pos, w, smem, v, idx);
     float *scr = (float *)(smem + lds_h(DT, M.dim, M.head.nb, tpw).scr);
     __shared__ int last;
     if (tidx() == 0) {
@@ -2439,17 +2493,21 @@ template <int DT> void launch_gemv(const l3m_dmat &m, const void *act, int k, fl
 template <class K> void lds_opt_in(K kernel, unsigned bytes) {
     if (bytes > 65536) (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
+// The GPT-2 variant (M.gpt2) runs its own instantiations of the step kernels.
 template <int DT> void launch_attn(const l3m_dmodel &M, const l3m_dlayer &L, int layer, hipStream_t st) {
-    lds_opt_in(k_attn_block<DT>, M.lds_a);
-    hipLaunchKernelGGL(k_attn_block<DT>, dim3(M.n_groups), dim3(NTE), M.lds_a, st, M, L, layer);
+    auto k = M.gpt2 ? k_attn_block<DT, true> : k_attn_block<DT, false>;
+    lds_opt_in(k, M.lds_a);
+    hipLaunchKernelGGL(k, dim3(M.n_groups), dim3(NTE), M.lds_a, st, M, L, layer);
 }
 template <int DT> void launch_ffn(const l3m_dmodel &M, const l3m_dlayer &L, int advance, hipStream_t st) {
-    lds_opt_in(k_ffn_block<DT>, M.lds_b);
-    hipLaunchKernelGGL(k_ffn_block<DT>, dim3(M.n_chunks), dim3(NTE), M.lds_b, st, M, L, advance);
+    auto k = M.gpt2 ? k_ffn_block<DT, true> : k_ffn_block<DT, false>;
+    lds_opt_in(k, M.lds_b);
+    hipLaunchKernelGGL(k, dim3(M.n_chunks), dim3(NTE), M.lds_b, st, M, L, advance);
 }
 template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t st) {
-    lds_opt_in(k_head_block<DT>, M.lds_h);
-    hipLaunchKernelGGL(k_head_block<DT>, dim3(M.head_grid), dim3(NTE), M.lds_h, st, M, advance);
+    auto k = M.gpt2 ? k_head_block<DT, true> : k_head_block<DT, false>;
+    lds_opt_in(k, M.lds_h);
+    hipLaunchKernelGGL(k, dim3(M.head_grid), dim3(NTE), M.lds_h, st, M, advance);
 }
 // The persistent kernel needs every workgroup resident at once: a cooperative launch, which the runtime
 // refuses (instead of starting it) when the grid does not fit.

@@ -1,0 +1,59 @@
+"""The GPT-2 variant on the GPU (LayerNorm with biases, learned positions, biases on every matrix, GELU
+MLP without gate; model.h:19-26, engine.c:236-275), through the l3m.h API, against the oracle (pinned
+bit-exact against the reference's --ref path in test_cpu_sampling.py). It runs on the one-graph-per-step
+path; the bar is the engine's: equal argmax, KL < 0.01 nats, max-abs within SPREAD of max|logit| after
+the prompt, and the greedy tokens of the oracle until its first near-tie.
+"""
+import numpy as np
+import pytest
+
+import l3m_amd as A
+
+pytestmark = pytest.mark.gpu
+CFG = A.Config("g2gpu", dim=128, n_layers=2, n_heads=4, n_kv_heads=4, ffn_dim=512, vocab=512, ctx=64, dtype="q8_0")
+SPREAD = {"f32": 1e-4, "bf16": 1e-3, "q8_0": 0.02, "q4_0": 0.02}
+
+
+def kl(lr, lf):
+    lr, lf = np.float64(lr), np.float64(lf)
+    pr = np.exp(lr - lr.max()); pr /= pr.sum()
+    lpr = lr - lr.max() - np.log(np.exp(lr - lr.max()).sum())
+    lpf = lf - lf.max() - np.log(np.exp(lf - lf.max()).sum())
+    return float((pr * (lpr - lpf)).sum())
+
+
+def margin(logits):
+    top = np.sort(logits)[-2:]
+    return (top[1] - top[0]) / np.abs(logits).max()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "q8_0", "q4_0", "f32"])
+def test_gpt2_matches_oracle(models, oracle, dtype):
+    print(f"case gpt2 {dtype}", flush=True)
+    path = models.get(CFG, dtype, seed=5, std=0.06, norm_jitter=0.1, arch="gpt2")
+    ids = A.prompt(5, CFG.vocab, 12)
+    m, om = A.Model(path), oracle.load(path)
+    assert not m.persistent
+    m.generate(ids, 0)
+    assert m.prefilled == 0
+    om.generate(ids, 0)
+    lg, lo = m.logits, om.logits()
+    assert int(np.argmax(lg)) == int(np.argmax(lo)) and kl(lo, lg) < 0.01
+    assert np.abs(lg - lo).max() <= SPREAD[dtype] * np.abs(lo).max()
+    got, want = m.generate(ids, 16), om.generate(ids, 16)
+    # equal up to the first step whose top-2 margin in the oracle is a near-tie (0.5% of max|logit|)
+    seq = list(ids)
+    for k, (a, b) in enumerate(zip(got, want)):
+        om.generate(seq, 0)
+        if margin(om.logits()) < 0.005:
+            break
+        assert a == b, f"step {k}"
+        seq.append(b)
+
+
+def test_gpt2_reference_path(models, oracle):
+    path = models.get(CFG, "q4_0", seed=5, std=0.06, norm_jitter=0.1, arch="gpt2")
+    ids = A.prompt(6, CFG.vocab, 6)
+    gref, oref = A.Model(path, reference=True), oracle.load(path, ref=True)
+    assert gref.generate(ids, 16) == oref.generate(ids, 16)
+    assert np.abs(gref.logits - oref.logits()).max() <= 1e-4 * np.abs(oref.logits()).max()
