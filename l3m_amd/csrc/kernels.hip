@@ -278,57 +278,49 @@ __device__ __forceinline__ float block_fma(float acc, const uint4 *w, uint32_t s
     }
 }
 
-// This lane's partial dot for row (lane & 15) of `tile`, over blocks b0 + sub, b0 + sub + 4, ... < b1.
+// One batch of a lane's blocks: U blocks of its row, 4 blocks apart (the quarter-wavefronts interleave).
+template <int DT> struct LaneBatch {
+    static constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
+    static constexpr int U = DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 4 : 8;
+    uint4 w[U][NV];
+    uint32_t sc[U];
+};
 template <int DT>
-__device__ __forceinline__ float lane_dot(const l3m_dmat &m, int tile, int b0, int b1, const uint8_t *act, int kp, int lane) {
-    constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
-    constexpr int U = DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 4 : 8;
-    const int c = lane & 15, sub = lane >> 4;
-    const size_t base = (size_t)tile * m.nb * RT + c;
-    const uint8_t *__restrict__ qp = m.q + base * QBY;
-    const uint8_t *__restrict__ sp = SBY ? m.s + base * SBY : nullptr;
+__device__ __forceinline__ void lane_load(const l3m_dmat &m, int tile, int b, int b1, int lane, LaneBatch<DT> &x) {
+    using L = LaneBatch<DT>;
+    const size_t base = (size_t)tile * m.nb * RT + (lane & 15);
+    const uint8_t *__restrict__ qp = m.q + base * L::QBY;
+    const uint8_t *__restrict__ sp = L::SBY ? m.s + base * L::SBY : nullptr;
+    // every load is issued (past b1 the index stays on block b1 - 1, b0 < b1): loads under a branch
+    // would make the compiler wait for all of them where the branches join
+#pragma unroll
+    for (int u = 0; u < L::U; u++) {
+        const int bb = min(b + 4 * u, b1 - 1);
+        const uint4 *src = (const uint4 *)(qp + (size_t)bb * RT * L::QBY);
+#pragma unroll
+        for (int v = 0; v < L::NV; v++) x.w[u][v] = src[v];
+        x.sc[u] = 0;
+        if constexpr (L::SBY == 2) x.sc[u] = *(const uint16_t *)(sp + (size_t)bb * RT * 2);
+        if constexpr (L::SBY == 1) x.sc[u] = sp[(size_t)bb * RT];
+    }
+}
+// This lane's partial dot for row (lane & 15) of `tile`, over blocks b0 + sub, b0 + sub + 4, ... < b1.
+// x: its first batch, already requested by the caller.
+template <int DT>
+__device__ __forceinline__ float lane_dot(const l3m_dmat &m, int tile, int b0, int b1, const uint8_t *act, int kp, int lane,
+                                          LaneBatch<DT> x) {
+    constexpr int U = LaneBatch<DT>::U;
     float acc = 0.f;
-    for (int b = b0 + sub; b < b1; b += 4 * U) {
-        uint4 w[U][NV];
-        uint32_t sc[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int bb = b + 4 * u;
-            sc[u] = 0;
-            if (bb < b1) {
-                const uint4 *src = (const uint4 *)(qp + (size_t)bb * RT * QBY);
-#pragma unroll
-                for (int v = 0; v < NV; v++) w[u][v] = src[v];
-                if constexpr (SBY == 2) sc[u] = *(const uint16_t *)(sp + (size_t)bb * RT * 2);
-                if constexpr (SBY == 1) sc[u] = sp[(size_t)bb * RT];
-            }
-        }
+    int b = b0 + (lane >> 4);
+    for (;;) {
 #pragma unroll
         for (int u = 0; u < U; u++)
-            if (b + 4 * u < b1) acc = block_fma<DT>(acc, w[u], sc[u], act, kp, b + 4 * u);
+            if (b + 4 * u < b1) acc = block_fma<DT>(acc, x.w[u], x.sc[u], act, kp, b + 4 * u);
+        b += 4 * U;
+        if (b >= b1) break;
+        lane_load<DT>(m, tile, b, b1, lane, x);
     }
     return acc;
-}
-
-// The workgroup's 4/S tiles starting at tile0, each split over S wavefronts along the inputs.
-// yv[t*16 + r] = output row r of tile tile0 + t. red: 64 floats of LDS.
-template <int DT>
-__device__ void wg_matvec(const l3m_dmat &m, int tile0, int S, const uint8_t *act, int kp, float *red, float *yv) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, tpw = 4 / S;
-    const int t = wave / S, split = wave % S, tile = tile0 + t;
-    const int b0 = split * m.nb / S, b1 = (split + 1) * m.nb / S;
-    float acc = tile < m.tiles ? lane_dot<DT>(m, tile, b0, b1, act, kp, lane) : 0.f;
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
-    if (lane < 16) red[wave * 16 + lane] = acc;
-    __syncthreads();
-    if (tid < tpw * 16) {
-        const int tt = tid >> 4, r = tid & 15;
-        float y = red[(tt * S) * 16 + r];
-        for (int s = 1; s < S; s++) y += red[(tt * S + s) * 16 + r];
-        yv[tid] = y;
-    }
-    __syncthreads();
 }
 
 // LDS carve-up shared by the matvec kernels.
@@ -348,6 +340,8 @@ __device__ Smem carve(uint8_t *base, int dt, int k) {
     s.iscr = (int *)(s.scr + 8);
     return s;
 }
+// 16-byte words of the activation each k_gemv thread holds in registers while its first weights load
+constexpr int GEMV_ACT_REGS = 4;
 inline size_t smem_bytes(int dt, int k) { return align16(act_size(dt, k)) + 4 * (size_t)kpad(k) + 4 * (64 + 64 + 16); }
 constexpr size_t LDS_MAX = 65536;   // dynamic LDS per workgroup without opting in to more
 
@@ -374,19 +368,51 @@ __global__ void __launch_bounds__(NT) k_prep(const float *__restrict__ x, int k,
     for (size_t i = threadIdx.x; i < n; i += NT) out[i] = s.act[i];
 }
 
-template <int DT>
+// STAGED: the activation is 16-byte aligned and at most GEMV_ACT_REGS * NT 16-byte words (gemv_staged).
+template <int DT, bool STAGED>
 __global__ void __launch_bounds__(NT) k_gemv(l3m_dmat m, const uint8_t *__restrict__ act_g, int k, float *__restrict__ y, int S) {
     extern __shared__ __align__(16) uint8_t smem[];
     Smem s = carve(smem, DT, k);
-    const int kp = kpad(k);
-    const size_t n4 = act_size(DT, k) / 4;   // 40 bytes per 32 inputs when quantized: whole words, not whole uint4
-    for (size_t i = threadIdx.x; i < n4; i += NT) ((uint32_t *)s.act)[i] = ((const uint32_t *)act_g)[i];
+    const int kp = kpad(k), tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the workgroup's 4/S tiles from tile0, each split over S wavefronts along the inputs
+    const int tpw = 4 / S, tile0 = blockIdx.x * tpw, tile = tile0 + wave / S, split = wave % S;
+    const int b0 = split * m.nb / S, b1 = (split + 1) * m.nb / S;
+    const bool live = tile < m.tiles;
+    const int ltile = min(tile, m.tiles - 1);   // a wavefront past the last tile loads the last one and discards it
+    const size_t bytes = act_size(DT, k);   // 40 bytes per 32 inputs when quantized: whole words, not whole uint4
+    const int n16 = (int)(bytes / 16), ntail = (int)(bytes % 16) / 4;
+    LaneBatch<DT> x;
+    // b0 < b1 holds: pick_split gives every split at least one block. Every load below is issued
+    // unconditionally: a load under a branch makes the compiler wait for all loads where the branches join.
+    if constexpr (STAGED) {
+        // The activation's loads go out first and the wavefront's first batch of weights right behind
+        // them. Loads complete in order, so the activation reaches LDS while the weights are on the way.
+        u32x4 a[GEMV_ACT_REGS];
+        uint32_t at;
+#pragma unroll
+        for (int r = 0; r < GEMV_ACT_REGS; r++) a[r] = ((const u32x4 *)act_g)[min(tid + r * NT, n16 - 1)];   // clamped
+        at = ((const uint32_t *)act_g)[4 * n16 - 1 + min(tid + 1, ntail)];   // tail word tid, or a word in range
+        lane_load<DT>(m, ltile, b0 + (lane >> 4), b1, lane, x);
+        // clamped slots are written by several threads, with the same value
+#pragma unroll
+        for (int r = 0; r < GEMV_ACT_REGS; r++) ((u32x4 *)s.act)[min(tid + r * NT, n16 - 1)] = a[r];
+        ((uint32_t *)s.act)[4 * n16 - 1 + min(tid + 1, ntail)] = at;
+    } else {
+        for (size_t i = tid; i < bytes / 4; i += NT) ((uint32_t *)s.act)[i] = ((const uint32_t *)act_g)[i];
+        lane_load<DT>(m, ltile, b0 + (lane >> 4), b1, lane, x);
+    }
     __syncthreads();
-    const int tpw = 4 / S, tile0 = blockIdx.x * tpw;
-    wg_matvec<DT>(m, tile0, S, s.act, kp, s.red, s.yv);
-    if (threadIdx.x < tpw * 16) {
-        const int r = (tile0 + (threadIdx.x >> 4)) * RT + (threadIdx.x & 15);
-        if (r < m.rows) y[r] = s.yv[threadIdx.x];
+    float acc = lane_dot<DT>(m, ltile, b0, b1, s.act, kp, lane, x);
+    if (!live) acc = 0.f;
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (lane < 16) s.red[wave * 16 + lane] = acc;
+    __syncthreads();
+    if (tid < tpw * 16) {
+        const int tt = tid >> 4, r = tid & 15, row = (tile0 + tt) * RT + r;
+        float v = s.red[(tt * S) * 16 + r];
+        for (int sp = 1; sp < S; sp++) v += s.red[(tt * S + sp) * 16 + r];
+        if (row < m.rows) y[row] = v;
     }
 }
 
@@ -2487,7 +2513,10 @@ template <int DT> void launch_prep(const float *x, int k, void *act, hipStream_t
 }
 template <int DT> void launch_gemv(const l3m_dmat &m, const void *act, int k, float *y, int S, hipStream_t st) {
     const int grid = (m.tiles + 4 / S - 1) / (4 / S);
-    hipLaunchKernelGGL(k_gemv<DT>, dim3(grid), dim3(NT), smem_bytes(DT, k), st, m, (const uint8_t *)act, k, y, S);
+    const size_t n16 = act_size(DT, k) / 16;
+    const bool staged = n16 > 0 && n16 <= (size_t)GEMV_ACT_REGS * NT && ((uintptr_t)act & 15) == 0;
+    if (staged) hipLaunchKernelGGL((k_gemv<DT, true>), dim3(grid), dim3(NT), smem_bytes(DT, k), st, m, (const uint8_t *)act, k, y, S);
+    else hipLaunchKernelGGL((k_gemv<DT, false>), dim3(grid), dim3(NT), smem_bytes(DT, k), st, m, (const uint8_t *)act, k, y, S);
 }
 // Kernels that take more than 64 KiB of dynamic LDS declare it once.
 template <class K> void lds_opt_in(K kernel, unsigned bytes) {
