@@ -1,27 +1,35 @@
 #!/usr/bin/env python3
-"""Batch-1 decode benchmark of the gfx950 backend (BASELINE.json metric: decode tok/s + matvec weight GB/s
-vs roofline, per dtype).
+"""Batch-1 decode benchmark of the gfx950 backend (BASELINE.json metric: decode tok/s + matvec weight GB/s vs
+roofline, per dtype).
 
-A step is one greedy decode token of the stories110M-shaped q4_0 Llama (dim 768, 12
-layers, 12 heads, ffn 2048, vocab 32000, ctx 128, tied q4_0 head, random-init N(0, 0.02)), fed a 4-token
-seeded prompt and restarted when the context fills (the reference's bench loop, main.c:247-251).
-Weights are resident in HBM before the timed region. One JSON line on stdout:
-  value / ms_per_step  generated tokens per second over exactly --steps tokens
-  roofline             the decode kernel (k_decode, one persistent launch per run of up to 64 steps): the
-                       algorithmic bytes of the steps it ran (body weights every step, head weights on steps
-                       with logits, K/V rows read and written) over its average launch duration (hipEvents
-                       around each launch on the library stream), against 8 TB/s HBM3E; traffic = the HBM
-                       bytes per launch that rocprofv3 counted for the same command (profiles/)
-  step_kernels         the one-graph-per-step path's three kernels, each timed alone at ctx/2
-  matvec               per-dtype matvec GB/s at the microbench shapes, warm
-                       (cache-resident) and cold (rotating over > 512 MiB of copies)
-  cpu_baseline         fpedd/l3m itself (built from its sources into oracle/_ref), AVX2/AVX-512 path,
-                       on this host's cores, same model file and prompt
+Headline (value): greedy decode of the stories110M-shaped q4_0 Llama (dim 768, 12 layers,
+12 heads, ffn 2048, vocab 32000, ctx 128, tied q4_0 head, random-init N(0, 0.02)) from a one-token prompt
+(token 0, as the reference's `l3m bench` feeds BOS or 0, main.c:244), restarted when the context fills
+(main.c:247-251). A step is one generated token; exactly --steps are timed, after --warmup. Weights are
+resident in HBM before the timed region. One JSON line on stdout:
+  value / ms_per_step  generated tokens per second over the timed tokens (wall clock around the run)
+  roofline             the decode kernel (k_decode, one persistent launch per run of up to 64 forward
+                       passes): the algorithmic bytes of the passes it ran (body weights every pass, head
+                       weights on passes with logits, K/V rows read and written) over its launch durations
+                       (hipEvents around each launch on the library stream), against 8 TB/s HBM3E;
+                       traffic = HBM bytes per launch from the committed rocprofv3 counter profile
+  decode               one line per BASELINE decode configuration and dtype (C1 stories15M bf16, C3
+                       stories42M q8_0 at ctx 1024, C4 stories110M q4_0, C5 SmolLM2-135M q8_0 and mxfp4 with
+                       the 64-token prompt prefilled): 256 greedy tokens, restarting at a full context, median
+                       of 5 GPU runs; k_decode's roofline fraction; the reference's own engine on this host
+                       (median of 7 runs, cores and ISA stated); C5 also times the prompt to its first logits
+  matvec               per dtype at the microbench shapes: warm (one matrix re-read) and
+                       cold (round robin over > 512 MiB of copies) GB/s, each against 8 TB/s and against a
+                       streaming read of the same bytes in the same residency (the measured roofline), with
+                       the reference's own matvec table on one core and on all physical cores
+  cpu_baseline         the reference (oracle/_ref, built from its sources) on the headline workload: median
+                       of 7 runs of --steps tokens on this host's physical cores (at most 16)
 """
 import argparse
 import ctypes as C
 import json
 import os
+import statistics
 import sys
 import tempfile
 import time
@@ -33,65 +41,27 @@ sys.path.insert(0, str(ROOT))
 PEAK_HBM_GBS = 8000.0
 KINDS = ["attn_block", "ffn_block", "head"]
 MICRO_SHAPES = [(288, 768), (768, 288), (2048, 768), (4096, 4096), (14336, 4096)]
-PUBLISHED = {("stories110M", "q4_0"): 5800.0, ("stories15M", "bf16"): 15300.0, ("stories42M", "q8_0"): 10700.0}
+# README.md:52-56 of the reference (Ryzen 9 7950X, median of 7 runs of 256 tokens, real weights)
+PUBLISHED = {("stories110M", "q4_0"): 5800.0, ("stories15M", "bf16"): 15300.0, ("stories42M", "q8_0"): 10700.0,
+             ("smollm2", "q8_0"): 530.0}
+# (config, dtype, ctx, prompt kind): BASELINE configs 1, 3, 4 and 5
+DECODE_LINES = [("stories15M", "bf16", 0, "seeded"), ("stories42M", "q8_0", 1024, "seeded"), ("stories110M", "q4_0", 0, "bos"),
+                ("smollm2", "q8_0", 0, "seeded"), ("smollm2", "mxfp4", 0, "seeded")]
+N_TOKENS = 256
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_table(A, m, cfg):
-    lib = A.lib()
-    pos = cfg.ctx // 2
-    rows = []
-    for kind, name in enumerate(KINDS):
-        us = lib.l3m_bench_kernel(m._handle(), kind, 0, pos, 200)
-        if us < 0:
-            raise RuntimeError(f"timing {name} failed")
-        nbytes = lib.l3m_kernel_bytes(m._handle(), kind, pos)
-        per_tok = 1 if name == "head" else cfg.n_layers
-        rows.append({"kernel": name, "us": us, "bytes": nbytes, "GBs": nbytes / us * 1e-3, "launches_per_token": per_tok,
-                     "us_per_token": us * per_tok})
-    return rows
-
-
-def matvec_bench(A, dtypes, iters=50):
-    """Warm: one matrix re-read; cold: round robin over copies totalling > 512 MiB (beyond the 256 MB MALL)."""
-    import numpy as np
-    sys.path.insert(0, str(ROOT / "tests"))
-    from weights import rows as make_rows
-    lib, dev = A.lib(), A.Device()
-    out = {}
-    for name in dtypes:
-        dt = A.DTYPES[name]
-        res = {}
-        for n, k in MICRO_SHAPES:
-            w = make_rows(dt, n, k, seed=n + k)
-            q, s = dev.pack_rows(dt, w, k)
-            nbytes = len(q) + len(s)
-            copies = 1 + (512 << 20) // nbytes
-            mats = (A.DMat * copies)()
-            dq = dev.put(np.tile(q, copies))                      # each copy starts 256-byte aligned
-            ds = dev.put(np.tile(s, copies)) if len(s) else None
-            for i in range(copies):
-                mats[i] = A.DMat(dq + i * len(q), ds + i * len(s) if ds else None, n, (n + 15) // 16, (k + 31) // 32, dt)
-            x = np.random.default_rng(0).standard_normal(k).astype(np.float32)
-            act = dev.alloc(lib.l3m_act_bytes(dt, k))
-            lib.l3m_k_prep(dt, dev.put(x), k, act, None)
-            y = dev.alloc(n * 4)
-            warm = lib.l3m_time_gemv(mats, 1, act, k, y, iters)
-            cold = lib.l3m_time_gemv(mats, copies, act, k, y, max(iters, 2 * copies))
-            res[f"{n}x{k}"] = {"bytes": nbytes, "warm_us": round(warm, 3), "warm_GBs": round(nbytes / warm * 1e-3, 1),
-                               "cold_us": round(cold, 3), "cold_GBs": round(nbytes / cold * 1e-3, 1),
-                               "cold_frac_of_peak": round(nbytes / cold * 1e-3 / PEAK_HBM_GBS, 3)}
-            dev.free_all()
-        out[name] = res
-        log(f"matvec {name}: " + ", ".join(f"{s} {r['warm_GBs']:.0f}/{r['cold_GBs']:.0f} GB/s" for s, r in res.items()))
-    return out
+def prompt_of(A, cfg, kind):
+    return [0] if kind == "bos" else A.prompt(1, cfg.vocab, cfg.n_prompt)
 
 
 def decode_bytes(A, m, cfg, work):
-    """Algorithmic bytes of `work` = (steps, steps with the head, K/V rows read per kv head and layer)."""
+    """Algorithmic bytes of `work` = (forward passes, passes with the head, K/V rows read per kv head and
+    layer): the weight bytes of the file's blocks (rows x k x bytes per weight, as the reference's
+    bytes_token, engine.c:591) and the bf16 K/V rows read and written."""
     lib, h = A.lib(), m._handle()
     body = cfg.n_layers * (lib.l3m_kernel_bytes(h, 0, 0) + lib.l3m_kernel_bytes(h, 1, 0))
     head = lib.l3m_kernel_bytes(h, 2, 0)
@@ -100,11 +70,43 @@ def decode_bytes(A, m, cfg, work):
     return steps * body + head_steps * head + kv_rows * row + steps * row
 
 
+class DecodeTimer:
+    """k_decode's launches (hipEvents on the library stream) and the work they did, over a region."""
+
+    def __init__(self, A, m):
+        self.A, self.m, self.lib = A, m, A.lib()
+
+    def __enter__(self):
+        self.lib.l3m_dev_sync()
+        self.w0 = (C.c_double * 3)()
+        self.lib.l3m_decode_work(self.m._handle(), self.w0)
+        self.lib.l3m_decode_timer(1, None, None)
+        return self
+
+    def __exit__(self, *exc):
+        self.lib.l3m_dev_sync()
+        us, launches = C.c_double(), C.c_int()
+        self.lib.l3m_decode_timer(0, C.byref(us), C.byref(launches))
+        w1 = (C.c_double * 3)()
+        self.lib.l3m_decode_work(self.m._handle(), w1)
+        self.us, self.launches = us.value, launches.value
+        self.work = [w1[i] - self.w0[i] for i in range(3)]
+
+    def roofline(self, cfg):
+        if not (self.m.persistent and self.launches):
+            return None
+        nbytes = decode_bytes(self.A, self.m, cfg, self.work)
+        gbs = nbytes / (self.us * 1e3)
+        return {"kernel": "k_decode", "launches": self.launches, "steps": self.work[0], "head_steps": self.work[1],
+                "us": self.us / self.launches, "bytes": nbytes / self.launches, "GBs": gbs, "us_per_step": self.us / self.work[0]}
+
+
 def measured_traffic(cfg_name, dtype, kernel, steps_per_launch=None):
     """HBM bytes per launch of a kernel (read + written), from the committed counter profile of this
     configuration (profiles/decode_<config>_<dtype>_traffic.json: two rocprofv3 --pmc passes, FETCH_SIZE
-    and WRITE_SIZE, scaled by the plain copy kernel's readings). k_decode's entry is per step (its launches
-    run different step counts), scaled here by this run's steps per launch. None when no profile covers it."""
+    and WRITE_SIZE, scaled by the plain copy kernel's readings). k_decode's entry is per forward pass (its
+    launches run different numbers of passes), scaled here by this run's passes per launch. None when no
+    profile covers it."""
     p = ROOT / "profiles" / f"decode_{cfg_name}_{dtype}_traffic.json"
     if not p.exists():
         return None
@@ -114,16 +116,6 @@ def measured_traffic(cfg_name, dtype, kernel, steps_per_launch=None):
     if "read_bytes_per_step" in k:
         return None if steps_per_launch is None else round((k["read_bytes_per_step"] + k["write_bytes_per_step"]) * steps_per_launch)
     return k["read_bytes"] + k["write_bytes"]
-
-
-def copy_calibration(A, nbytes):
-    """One launch of the plain copy kernel over nbytes (read nbytes, write nbytes), for scaling counters."""
-    lib, dev = A.lib(), A.Device()
-    src, dst = dev.alloc(nbytes), dev.alloc(nbytes)
-    if lib.l3m_dev_copy(dst, src, nbytes, None) or lib.l3m_dev_sync():
-        raise RuntimeError("copy kernel failed")
-    dev.free_all()
-    log(f"copy: {nbytes} bytes")
 
 
 def host_cores():
@@ -141,23 +133,194 @@ def host_cores():
     return cpus[:16]
 
 
-def cpu_baseline(path, prompt, seconds):
-    """The reference's own engine (oracle/_ref, AVX2/AVX-512 per its CPUID dispatch) on this host."""
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def tokens_per_run(model, prompt, n, restart):
+    """Generate n tokens from prompt, restarting when the context fills (main.c:247-251); returns the count."""
+    done = 0
+    while done < n:
+        got = len(model.generate(prompt, n - done))
+        if got == 0:
+            break
+        done += got
+        if not restart:
+            break
+    return done
+
+
+def cpu_decode(path, prompt, n_tokens, ctx, runs=7):
+    """The reference's own engine (oracle/_ref, its CPUID-picked AVX2/AVX-512 table) on this host's physical
+    cores: one warm-up, then the median of `runs` runs of n_tokens greedy tokens (README.md:58-62)."""
     from oracle.oracle import Reference
     if not Reference.available():
         return None
     os.environ.pop("L3M_ISA", None)
     cpus = host_cores()
-    ref = Reference()
-    m = ref.load(path, cpus=cpus)
-    m.generate(prompt, 16)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        n += len(m.generate(prompt, 10 ** 6))
-    dt = time.perf_counter() - t0
+    m = Reference().load(path, ctx=ctx, cpus=cpus)
+    tokens_per_run(m, prompt, min(n_tokens, 32), True)
+    rates = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        n = tokens_per_run(m, prompt, n_tokens, True)
+        rates.append(n / (time.perf_counter() - t0))
     desc = m.describe()
-    return {"value": round(n / dt, 1), "unit": "tok/s", "cores": len(cpus), "kind": "reference",
-            "sample": f"{n} greedy tokens in {dt:.1f} s, same model file and prompt, restarts at the full context; {desc}"}
+    return {"value": round(statistics.median(rates), 1), "unit": "tok/s", "cores": len(cpus), "kind": "reference",
+            "sample": f"median of {runs} runs of {n_tokens} greedy tokens after one warm-up (min {min(rates):.0f}, max {max(rates):.0f}), "
+                      f"same model file and prompt, restarts at the full context; {desc}; {cpu_model()}"}
+
+
+def cpu_first_logits(path, prompt, ctx, runs=3):
+    """Milliseconds from the prompt to its first logits on the reference's engine (token by token)."""
+    from oracle.oracle import Reference
+    if not Reference.available():
+        return None
+    m = Reference().load(path, ctx=ctx, cpus=host_cores())
+    m.generate(prompt, 0)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        m.generate(prompt, 0)
+        times.append((time.perf_counter() - t0) * 1e3)
+    return round(statistics.median(times), 3)
+
+
+def gpu_first_logits(A, path, prompt, ctx, reps=5):
+    """Milliseconds to the first logits of the prompt on the GPU: batched prefill, and token by token
+    (L3M_PREFILL=0); median of reps."""
+    out = {}
+    for key, env in (("ms_prefill", None), ("ms_token_by_token", "0")):
+        if env is None:
+            os.environ.pop("L3M_PREFILL", None)
+        else:
+            os.environ["L3M_PREFILL"] = env
+        with A.Model(path, ctx=ctx) as m:
+            m.generate(prompt, 0)
+            times = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                m.generate(prompt, 0)
+                A.lib().l3m_dev_sync()
+                times.append((time.perf_counter() - t0) * 1e3)
+            out[key] = round(statistics.median(times), 3)
+            if env is None:
+                out["prefilled_positions"] = m.prefilled
+    os.environ.pop("L3M_PREFILL", None)
+    return out
+
+
+def decode_line(A, d, name, dtype, ctx, kind, cpu_runs, gpu_runs=5):
+    cfg = A.CONFIGS[name]
+    path = A.write_model(Path(d) / f"{name}-{dtype}.l3m", cfg, dtype=dtype, seed=1)
+    prompt = prompt_of(A, cfg, kind)
+    with A.Model(path, ctx=ctx) as m:
+        m.bench_decode(prompt, 32)
+        rates, dom = [], None
+        with DecodeTimer(A, m) as t:
+            for _ in range(gpu_runs):
+                rates.append(1.0 / m.bench_decode(prompt, N_TOKENS))
+        dom = t.roofline(cfg)
+        wbytes = A.lib().l3m_weight_bytes(m._handle())
+        mctx, persistent, att = m.ctx, m.persistent, m.attention_mode
+    value = statistics.median(rates)
+    line = {"config": name, "dtype": dtype, "ctx": mctx, "prompt_tokens": len(prompt), "tokens": N_TOKENS,
+            "value": round(value, 1), "unit": "tok/s", "us_per_token": round(1e6 / value, 2),
+            "gpu_runs": [round(r, 1) for r in rates], "persistent": persistent, "attention_mode": att,
+            "weight_bytes_per_token": wbytes, "weight_GBs": round(wbytes * value * 1e-9, 1)}
+    if dom:
+        line["roofline"] = {"bound": "hbm", "kernel": "k_decode", "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4), "us_per_step": round(dom["us_per_step"], 2)}
+    pub = PUBLISHED.get((name, dtype))
+    line["published"] = pub
+    line["vs_published"] = round(value / pub, 3) if pub else None
+    if len(prompt) > 8:
+        line["first_logits"] = gpu_first_logits(A, path, prompt, ctx)
+    if cpu_runs:
+        line["cpu_baseline"] = cpu_decode(path, prompt, N_TOKENS, ctx, cpu_runs)
+        if line["cpu_baseline"]:
+            line["vs_cpu"] = round(value / line["cpu_baseline"]["value"], 3)
+            if len(prompt) > 8:
+                line["first_logits"]["cpu_ms"] = cpu_first_logits(path, prompt, ctx)
+    log(f"decode {name} {dtype} ctx {mctx}: {line['value']} tok/s ({line['us_per_token']} us/token, "
+        f"k_decode {line.get('roofline', {}).get('us_per_step', '-')} us/pass, {line.get('roofline', {}).get('frac', '-')} of HBM peak); "
+        f"cpu {line.get('cpu_baseline', {}) and line['cpu_baseline']['value']} tok/s")
+    return line
+
+
+def cpu_matvec_lib():
+    p = ROOT / "oracle" / "_ref" / "libcpubench.so"
+    if not p.exists():
+        return None
+    lib = C.CDLL(str(p))
+    lib.cb_gemv_gbs.restype = C.c_double
+    lib.cb_gemv_gbs.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_double]
+    lib.cb_table.restype = C.c_int
+    return lib
+
+
+def matvec_bench(A, dtypes, iters=50, cpu_seconds=0.2):
+    """Warm: one matrix re-read; cold: round robin over copies totalling > 512 MiB (beyond the 256 MB
+    Infinity Cache). Beside each, the measured roofline (a streaming read of the same bytes, warm and cold)
+    and the reference's own matvec table (tests/test_kernels.c:151-176's method) on one core and on all."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "tests"))
+    from weights import rows as make_rows
+    lib, dev, cpu = A.lib(), A.Device(), cpu_matvec_lib() if cpu_seconds > 0 else None
+    cores = host_cores()
+    arr = (C.c_int * len(cores))(*cores)
+    out = {}
+    for name in dtypes:
+        dt = A.DTYPES[name]
+        res = {}
+        for n, k in MICRO_SHAPES:
+            w = make_rows(dt, n, k, seed=n + k)
+            x = np.random.default_rng(0).standard_normal(k).astype(np.float32)
+            q, s = dev.pack_rows(dt, w, k)
+            nbytes = len(q) + len(s)
+            copies = 1 + (512 << 20) // nbytes
+            mats = (A.DMat * copies)()
+            dq = dev.put(np.tile(q, copies))                      # each copy starts 256-byte aligned
+            ds = dev.put(np.tile(s, copies)) if len(s) else None
+            for i in range(copies):
+                mats[i] = A.DMat(dq + i * len(q), ds + i * len(s) if ds else None, n, (n + 15) // 16, (k + 31) // 32, dt)
+            act = dev.alloc(lib.l3m_act_bytes(dt, k))
+            lib.l3m_k_prep(dt, dev.put(x), k, act, None)
+            y = dev.alloc(n * 4)
+            warm = lib.l3m_time_gemv(mats, 1, act, k, y, iters)
+            cold = lib.l3m_time_gemv(mats, copies, act, k, y, max(iters, 2 * copies))
+            rb = (nbytes + 16 + 15) // 16 * 16                   # read roofline: the same bytes (+ its scratch word)
+            rcopies = 1 + (512 << 20) // rb
+            rbuf = dev.alloc(rb * rcopies)
+            bufs = (C.c_void_p * rcopies)(*[rbuf + i * rb for i in range(rcopies)])
+            rwarm = lib.l3m_time_read(bufs, 1, rb, iters)
+            rcold = lib.l3m_time_read(bufs, rcopies, rb, max(iters, 2 * rcopies))
+            r = {"bytes": nbytes, "warm_us": round(warm, 3), "warm_GBs": round(nbytes / warm * 1e-3, 1),
+                 "cold_us": round(cold, 3), "cold_GBs": round(nbytes / cold * 1e-3, 1),
+                 "cold_frac_of_peak": round(nbytes / cold * 1e-3 / PEAK_HBM_GBS, 3),
+                 "read_warm_GBs": round(nbytes / rwarm * 1e-3, 1), "read_cold_GBs": round(nbytes / rcold * 1e-3, 1),
+                 "warm_frac_of_read": round(rwarm / warm, 3), "cold_frac_of_read": round(rcold / cold, 3)}
+            if cpu:
+                wc = np.ascontiguousarray(w)
+                r["cpu_1core_GBs"] = round(cpu.cb_gemv_gbs(dt, n, k, wc.ctypes.data, x.ctypes.data, arr, 1, cpu_seconds), 1)
+                r["cpu_all_GBs"] = round(cpu.cb_gemv_gbs(dt, n, k, wc.ctypes.data, x.ctypes.data, arr, len(cores), cpu_seconds), 1)
+            res[f"{n}x{k}"] = r
+            dev.free_all()
+        out[name] = res
+        log(f"matvec {name} (GB/s warm/cold | read roofline warm/cold | cpu 1/{len(cores)} cores): " +
+            ", ".join(f"{s} {r['warm_GBs']:.0f}/{r['cold_GBs']:.0f} | {r['read_warm_GBs']:.0f}/{r['read_cold_GBs']:.0f} | "
+                      f"{r.get('cpu_1core_GBs', '-')}/{r.get('cpu_all_GBs', '-')}" for s, r in res.items()))
+    if cpu:
+        out["cpu"] = {"table": ["scalar", "avx2", "avx512"][cpu.cb_table()], "cores": len(cores), "model": cpu_model(),
+                      "method": f"the reference's own gemv table on its packed tiles, looped for {cpu_seconds} s, warm (resident), "
+                                "one core, then every core on a contiguous range of tiles"}
+    return out
 
 
 def sampled_rate(A, m, prompt, n_tokens, temperature=1.0):
@@ -169,36 +332,16 @@ def sampled_rate(A, m, prompt, n_tokens, temperature=1.0):
     return {"temperature": temperature, "value": round(1e9 / ns, 1) if ns > 0 else None, "unit": "tok/s"}
 
 
-def prefill_figure(A, d, reps=5):
-    """Time to the first logits of the C5 workload (SmolLM2-135M-shaped q8_0, its 64-token seeded prompt):
-    the batched prefill against token-by-token decode steps (L3M_PREFILL=0), median of reps; a side figure."""
-    cfg = A.CONFIGS["smollm2"]
-    path = A.write_model(Path(d) / "smollm2-q8_0.l3m", cfg, dtype="q8_0", seed=1)
-    ids = A.prompt(1, cfg.vocab, cfg.n_prompt)
-    out = {"config": "smollm2-q8_0", "prompt": len(ids)}
-    for key, env in (("ms_prefill", None), ("ms_token_by_token", "0")):
-        if env is None:
-            os.environ.pop("L3M_PREFILL", None)
-        else:
-            os.environ["L3M_PREFILL"] = env
-        m = A.Model(path)
-        m.generate(ids, 0)
-        times = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            m.generate(ids, 0)
-            A.lib().l3m_dev_sync()
-            times.append((time.perf_counter() - t0) * 1e3)
-        out[key] = round(sorted(times)[reps // 2], 3)
-        if env is None:
-            out["prefilled_positions"] = m.prefilled
-        m.close()
-    os.environ.pop("L3M_PREFILL", None)
-    return out
+def cold_rate(A, path, prompt, n_tokens):
+    """Tokens/s with the caches emptied of the weights before every forward pass (--cold, engine.c:330-338),
+    the eviction not counted: a side figure (README.md:46-47 reports 6-8x slower on the CPU)."""
+    with A.Model(path, cold=True) as m:
+        m.bench_decode(prompt, 8)
+        return {"value": round(1.0 / m.bench_decode(prompt, n_tokens), 1), "unit": "tok/s", "tokens": n_tokens}
 
 
 def probes(A):
-    """The residency and exchange probes: rows of printable results."""
+    """The residency and exchange probes (the GPU analogues of bench/residency.c and bench/exchange.c)."""
     lib, out = A.lib(), {"stream": [], "exchange": [], "graph_node_us": None}
     v = C.c_double()
     for xcds in (1, 8):
@@ -226,11 +369,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--config", default="stories110M")
     ap.add_argument("--dtype", default=None)
+    ap.add_argument("--decode", type=int, default=1, help="the per-config decode lines (0 to skip)")
     ap.add_argument("--matvec", default="bf16,q8_0,q4_0,mxfp4", help="dtypes for the matvec microbench ('' to skip)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="reference CPU sample length (0 to skip)")
+    ap.add_argument("--cpu-runs", type=int, default=7, help="runs of the reference CPU engine per decode line (0 to skip)")
+    ap.add_argument("--cpu-matvec-seconds", type=float, default=0.2, help="loop length of each CPU matvec figure (0 to skip)")
     ap.add_argument("--sample-temp", type=float, default=1.0, help="temperature of the sampled-decode side figure (0 to skip)")
-    ap.add_argument("--prefill", type=int, default=1, help="time the SmolLM2 64-token prefill side figure (0 to skip)")
+    ap.add_argument("--cold", type=int, default=1, help="the --cold side figure (0 to skip)")
     ap.add_argument("--probes", action="store_true", help="run only the residency and exchange probes, one JSON line")
+    ap.add_argument("--only-decode", action="store_true", help="the headline decode only (for profiling runs)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the plain copy kernel once over this many MiB (counter calibration under rocprofv3)")
     a = ap.parse_args()
@@ -245,76 +391,72 @@ def main():
         return
     cfg = A.CONFIGS[a.config]
     dtype = a.dtype or cfg.dtype
+    lib = A.lib()
     with tempfile.TemporaryDirectory() as d:
         path = A.write_model(Path(d) / f"{cfg.name}-{dtype}.l3m", cfg, dtype=dtype, seed=1)
-        prompt = A.prompt(1, cfg.vocab, cfg.n_prompt)
-        m = A.Model(path)
-        log(f"bench: {m.describe()} on {A.lib().l3m_dev_name().decode()}")
-        lib = A.lib()
-        m.bench_decode(prompt, max(a.warmup, 1))
-        lib.l3m_dev_sync()
-        w0 = (C.c_double * 3)()
-        lib.l3m_decode_work(m._handle(), w0)
-        lib.l3m_decode_timer(1, None, None)
-        t0 = time.perf_counter()
-        m.bench_decode(prompt, a.steps)
-        lib.l3m_dev_sync()
-        elapsed = time.perf_counter() - t0
-        us, launches = C.c_double(), C.c_int()
-        lib.l3m_decode_timer(0, C.byref(us), C.byref(launches))
-        w1 = (C.c_double * 3)()
-        lib.l3m_decode_work(m._handle(), w1)
-        value = a.steps / elapsed
-        log(f"bench: {a.steps} tokens in {elapsed * 1e3:.2f} ms = {value:.0f} tok/s")
+        prompt = [0]
+        with A.Model(path) as m:
+            log(f"bench: {m.describe()} on {lib.l3m_dev_name().decode()}")
+            m.bench_decode(prompt, max(a.warmup, 1))
+            with DecodeTimer(A, m) as t:
+                t0 = time.perf_counter()
+                m.bench_decode(prompt, a.steps)
+                lib.l3m_dev_sync()
+                elapsed = time.perf_counter() - t0
+            dom = t.roofline(cfg)
+            value = a.steps / elapsed
+            log(f"bench: {a.steps} tokens in {elapsed * 1e3:.2f} ms = {value:.0f} tok/s")
+            if dom:
+                log(f"bench: k_decode {dom['launches']} launches, {dom['steps']:.0f} passes, {dom['us']:.1f} us per launch, "
+                    f"{dom['us_per_step']:.1f} us per pass, {dom['GBs']:.1f} GB/s algorithmic")
+            wbytes = lib.l3m_weight_bytes(m._handle())
+            sampled = sampled_rate(A, m, prompt, a.steps, a.sample_temp) if a.sample_temp > 0 and not a.only_decode else None
+            if sampled:
+                log(f"bench: sampled at T={sampled['temperature']}: {sampled['value']} tok/s")
+        cold = cold_rate(A, path, prompt, min(a.steps, 64)) if a.cold and not a.only_decode else None
+        if cold:
+            log(f"bench: --cold {cold['value']} tok/s")
         decode = None
-        if m.persistent and launches.value:
-            work = [w1[i] - w0[i] for i in range(3)]
-            nbytes = decode_bytes(A, m, cfg, work)
-            decode = {"kernel": "k_decode", "launches": launches.value, "steps": work[0], "head_steps": work[1],
-                      "us": us.value / launches.value, "bytes": nbytes / launches.value, "GBs": nbytes / (us.value * 1e3)}
-            log(f"bench: k_decode {launches.value} launches, {work[0]:.0f} steps, {us.value / launches.value:.1f} us per launch, "
-                f"{decode['GBs']:.1f} GB/s algorithmic")
-        kt = kernel_table(A, m, cfg)
-        for r in kt:
-            log(f"  {r['kernel']:10s} {r['us']:8.2f} us  {r['GBs']:8.1f} GB/s  x{r['launches_per_token']} = {r['us_per_token']:7.1f} us/token")
-        wbytes = A.lib().l3m_weight_bytes(m._handle())
-        sampled = sampled_rate(A, m, prompt, a.steps, a.sample_temp) if a.sample_temp > 0 else None
-        if sampled:
-            log(f"bench: sampled at T={sampled['temperature']}: {sampled['value']} tok/s")
-        m.close()
-        dom = decode or max(kt, key=lambda r: r["us_per_token"])
-        cpu = cpu_baseline(path, prompt, a.cpu_seconds) if a.cpu_seconds > 0 else None
-        prefill = prefill_figure(A, d) if a.prefill else None
-        if prefill:
-            log(f"bench: SmolLM2 q8_0 64-token prompt to first logits: {prefill['ms_prefill']} ms batched, "
-                f"{prefill['ms_token_by_token']} ms token by token")
+        if a.decode and not a.only_decode:
+            decode = [decode_line(A, d, *line, cpu_runs=a.cpu_runs) for line in DECODE_LINES]
+        # the headline's CPU line: the reference on the same model and prompt, runs of 256 tokens (the
+        # per-config line of this workload when it ran)
+        same = [ln for ln in decode or [] if (ln["config"], ln["dtype"], ln["prompt_tokens"]) == (cfg.name, dtype, len(prompt))]
+        cpu = same[0].get("cpu_baseline") if same else None
+        if cpu is None and a.cpu_runs > 0 and not a.only_decode:
+            cpu = cpu_decode(path, prompt, max(a.steps, N_TOKENS), 0, a.cpu_runs)
         if cpu:
             log(f"bench: reference CPU {cpu['value']} tok/s on {cpu['cores']} cores")
-    matvec = matvec_bench(A, [s for s in a.matvec.split(",") if s]) if a.matvec else None
+    matvec = matvec_bench(A, [s for s in a.matvec.split(",") if s], cpu_seconds=a.cpu_matvec_seconds) if a.matvec and not a.only_decode else None
     if a.copy_mib:
-        copy_calibration(A, a.copy_mib << 20)
+        dev = A.Device()
+        src, dst = dev.alloc(a.copy_mib << 20), dev.alloc(a.copy_mib << 20)
+        if lib.l3m_dev_copy(dst, src, a.copy_mib << 20, None) or lib.l3m_dev_sync():
+            raise RuntimeError("copy kernel failed")
+        dev.free_all()
+        log(f"copy: {a.copy_mib} MiB")
     pub = PUBLISHED.get((cfg.name, dtype))
     line = {
         "metric": "batch-1 decode tok/s + matvec weight GB/s vs roofline, per dtype",
         "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(elapsed * 1e3 / a.steps, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": round(value / pub, 3) if pub else None, "dtype": dtype, "data": "synthetic",
-        "config": {"workload": f"{cfg.name}-shaped {dtype} Llama, batch-1 greedy decode of {a.steps} tokens from a "
-                               f"{cfg.n_prompt}-token seeded prompt, restart at ctx {cfg.ctx}",
+        "config": {"workload": f"{cfg.name}-shaped {dtype} Llama, batch-1 greedy decode of {a.steps} tokens from a one-token "
+                               f"prompt (the reference bench's), restart at ctx {cfg.ctx}",
                    "dim": cfg.dim, "layers": cfg.n_layers, "heads": cfg.n_heads, "kv_heads": cfg.n_kv_heads,
                    "ffn": cfg.ffn_dim, "vocab": cfg.vocab, "ctx": cfg.ctx, "weights": "random-init N(0,0.02), seed 1"},
-        "roofline": {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4),
-                     "traffic": measured_traffic(cfg.name, dtype, dom["kernel"],
-                                                 dom["steps"] / dom["launches"] if "launches" in dom else None),
-                     "bytes_per_launch": round(dom["bytes"]), "us_per_launch": round(dom["us"], 3),
-                     **({"launches": dom["launches"], "steps": dom["steps"]} if "launches" in dom else {})},
-        "step_kernels": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in kt],
+        "roofline": None if not dom else {
+            "bound": "hbm", "kernel": dom["kernel"], "achieved": round(dom["GBs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(dom["GBs"] / PEAK_HBM_GBS, 4),
+            "traffic": measured_traffic(cfg.name, dtype, dom["kernel"], dom["steps"] / dom["launches"]),
+            "bytes_per_launch": round(dom["bytes"]), "us_per_launch": round(dom["us"], 3), "us_per_pass": round(dom["us_per_step"], 3),
+            "launches": dom["launches"], "passes": dom["steps"]},
         "weight_bytes_per_token": wbytes,
         "weight_GBs_per_token": round(wbytes * value * 1e-9, 1) if wbytes else None,
+        "decode": decode,
         "matvec": matvec,
         "sampled_decode": sampled,
-        "prefill": prefill,
+        "cold_decode": cold,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -28,7 +28,8 @@ typedef struct {
     int        reference;
     int        force;
     int        verbose;
-    int        cold;       // 1 = evict L2 and the Infinity Cache before each token (engine.c:330-338)
+    int        cold;       // 1 = evict L2 and the Infinity Cache before each forward pass, one pass per launch;
+                           // the eviction is not token time (engine.c:330-338, 584)
 } l3m_opts;
 
 // Replaces l3m_perf (src/l3m.h:21-29); counters the GPU path cannot read are NAN.
@@ -116,6 +117,21 @@ int    l3m_k_rmsnorm(float *y, const float *x, const float *w, int n, float eps,
 int    l3m_k_rope(float *v, int n_heads, int hd, int pos, const float *table, void *stream);      // ops.c:29
 int    l3m_k_silu_mul(float *h, const float *g, int n, void *stream);                            // ops.c:49
 int    l3m_k_argmax(const float *x, int n, int32_t *out, void *stream);                          // engine.c:290-301
+// The decode step's own pieces, alone (parity hooks):
+// rows [row0, row0 + n) of m dequantized by the step's embedding lookup (l3m_dequant_row, pack.c:55-62)
+// into out[n][32 * m->nb];
+int    l3m_k_dequant(const l3m_dmat *m, int row0, int n, float *out, void *stream);
+// which attention a decode step runs for a head group of nq query heads (2 matrix cores over the K/V
+// window in LDS, 1 VALU over the window, 0 VALU reading the cache; kv_lds: the window fits in LDS);
+int    l3m_attention_mode(int kv_lds, int hd, int nq, int ctx);
+// one head group's attention in that mode, exactly as the decode step runs it (l3m_attend, ops.c:58-73, for
+// each query head; GQA head h reads kv head h / (nq / nkv)): q [nq][hd] f32, kc and vc [nkv][ctx][hd] bf16
+// holding rows 0..pos, out [nq][hd].
+int    l3m_k_attend_decode(int mode, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int nq, int nkv, int hd,
+                           int ctx, int pos, void *stream);
+// One streaming read of bytes (16-byte multiple) at buf: with bytes above the Infinity Cache's size it
+// evicts every cached weight (the --cold eviction, engine.c:330-338).
+int    l3m_dev_evict(const void *buf, size_t bytes, void *stream);
 void   l3m_rope_table(float *table, int ctx, int hd, float theta);   // host: [ctx][hd/2] (cos, sin), ops.c:31-32
 
 // Benches. l3m_bench_decode: greedy tokens from prompt (restarting at a full context, main.c:251), ns per
@@ -124,6 +140,9 @@ double l3m_bench_decode(l3m_model *m, const int32_t *prompt, int n_prompt, int n
 // The same with temperature sampling on the device (seed + i for the i-th run of the context).
 double l3m_bench_decode_t(l3m_model *m, const int32_t *prompt, int n_prompt, int n_tokens, float temperature, uint64_t seed);
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);
+// The measured roofline beside it: one streaming read of `bytes` (a 16-byte multiple; the last 16 bytes
+// are scratch) per launch, over bufs[i % n_bufs].
+double l3m_time_read(void *const *bufs, int n_bufs, size_t bytes, int iters);
 // One kernel of the decode step at position pos: kind 0 attention block, 1 FFN block, 2 head.
 double l3m_bench_kernel(l3m_model *m, int kind, int layer, int pos, int iters);
 // Timing of the persistent decode kernel's launches (hipEvents on the library stream around each launch):
@@ -145,6 +164,11 @@ int    l3m_logits_at(const l3m_model *m, int pos, float *out);
 // Prompt positions the last generate call ran as one batched prefill (0: token by token). Prompts of at
 // least L3M_PREFILL_MIN (default 8) tokens on q8_0 and q4_0 bodies are prefilled unless L3M_PREFILL=0.
 int    l3m_prefill_positions(const l3m_model *m);
+// The attention mode the decode step of m runs (l3m_attention_mode's codes).
+int    l3m_decode_attention(const l3m_model *m);
+// K and V rows [pos0, pos0 + n) of kv head kvh in layer `layer` of m's cache (bf16 as the step writes them,
+// engine.c:247-248), into k and v [n][hd]; -1 when out of range.
+int    l3m_kv_rows(const l3m_model *m, int layer, int kvh, int pos0, int n, uint16_t *k, uint16_t *v);
 
 // Probes, the GPU analogues of the reference's bench/residency.c:31-97 and bench/exchange.c:22-44 (no
 // counterpart in its library): bandwidth of workgroups streaming their own shards (per_xcd workgroups on

@@ -69,6 +69,9 @@ l3m_f32_to_f16 w f               | l3m_decode_persistent i p      | l3m_decode_t
 l3m_decode_work v p *d          | l3m_logits_at i p i *f         | l3m_bench_decode_t d p *I i i f q
 l3m_prefill_positions i p       | l3m_probe_stream i z i i i *d   | l3m_probe_exchange i i i i i *d
 l3m_probe_graph_node i i i *d
+l3m_k_dequant i M i i p p       | l3m_attention_mode i i i i i   | l3m_k_attend_decode i i p p p p i i i i i p
+l3m_dev_evict i p z p           | l3m_decode_attention i p       | l3m_kv_rows i p i i i i p p
+l3m_time_read d ** i z i
 """
 _SIG = {}
 for _entry in _SIGNATURES.replace("\n", "|").split("|"):
@@ -123,8 +126,8 @@ class _TokenSink:
 
 class Model:
     """A .l3m file loaded on the GPU with a KV cache of ctx positions (0: min(model, 512)). The arguments
-    are those of the reference's Python Model (python/l3m/__init__.py:53-68); cpus, force and cold are
-    accepted for compatibility and have no meaning on one GPU."""
+    are those of the reference's Python Model (python/l3m/__init__.py:53-68); cpus and force are accepted
+    for compatibility and have no meaning on one GPU; cold evicts the caches before each forward pass."""
     _m = None
 
     def __init__(self, path, cpus=None, ctx=0, reference=False, force=False, verbose=False, cold=False):
@@ -183,6 +186,18 @@ class Model:
     def logits(self):
         ptr = self._lib.l3m_logits(self._handle())
         return np.ctypeslib.as_array(ptr, shape=(self.vocab,)).copy()
+
+    @property
+    def attention_mode(self):
+        """The decode step's attention: 2 matrix cores over the LDS window, 1 VALU over it, 0 from the cache."""
+        return self._lib.l3m_decode_attention(self._handle())
+
+    def kv_rows(self, layer, kvh, pos0, n, hd):
+        """bf16 K and V rows [pos0, pos0 + n) of one kv head of one layer's cache, as uint16 [n, hd] each."""
+        k, v = np.zeros((n, hd), np.uint16), np.zeros((n, hd), np.uint16)
+        if self._lib.l3m_kv_rows(self._handle(), layer, kvh, pos0, n, _p(k), _p(v)) != 0:
+            raise ValueError("K/V rows out of range")
+        return k, v
 
     @property
     def prefilled(self):
@@ -252,7 +267,8 @@ CONFIGS = {
 
 def write_model(path, cfg, dtype=None, seed=1, std=0.02, norm_jitter=0.0, tied=True, head_dtype=None, arch="llama"):
     """Write the seeded synthetic model of cfg (a Config or a name) to path. arch "gpt2" writes the GPT-2
-    variant: LayerNorm with biases, learned positions, a GELU MLP without gate, biases on every matrix."""
+    variant: LayerNorm with biases, learned positions, a GELU MLP without gate, biases on every matrix;
+    "gptneo" the same without the q, k, v biases."""
     cfg = CONFIGS[cfg] if isinstance(cfg, str) else cfg
     dt = DTYPES[dtype or cfg.dtype]
     spec = GenSpec(arch=arch.encode(), dim=cfg.dim, n_layers=cfg.n_layers, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
@@ -378,6 +394,19 @@ class Device:
         dh = self.put(np.float32(h))
         self._check(self.lib.l3m_k_silu_mul(dh, self.put(np.float32(g)), len(h), None), "silu_mul")
         return self.get(dh, len(h), np.float32)
+
+    def dequant(self, m, row0, n):
+        """Rows [row0, row0 + n) of device matrix m through the decode step's dequantization: float32 [n, 32 nb]."""
+        out = self.alloc(n * m.nb * 32 * 4)
+        self._check(self.lib.l3m_k_dequant(C.byref(m), row0, n, out, None), "dequant")
+        return self.get(out, (n, m.nb * 32), np.float32)
+
+    def attend_decode(self, mode, q, kc, vc, nq, nkv, hd, ctx, pos):
+        """One head group's decode attention (mode 2 matrix cores, 1 LDS window, 0 cache): out [nq, hd]."""
+        do = self.alloc(nq * hd * 4)
+        self._check(self.lib.l3m_k_attend_decode(mode, do, self.put(np.float32(q)), self.put(np.uint16(kc)), self.put(np.uint16(vc)),
+                                                 nq, nkv, hd, ctx, pos, None), "attend_decode")
+        return self.get(do, (nq, hd), np.float32)
 
     def argmax(self, x):
         do = self.alloc(4)

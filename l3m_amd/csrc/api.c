@@ -15,6 +15,7 @@
 #define NSLOTS 64              // logits slots = the most steps enqueued between two host reads
 #define HEAD_WGS 256           // workgroups of the head kernel
 #define MAX_PARTS 64           // partial residual vectors a step kernel adds (head groups, FFN chunks)
+#define EVICT_BYTES (512u << 20)   // --cold: read before each forward pass, twice the 256 MiB Infinity Cache
 
 struct l3m_model {
     l3m_mapped   f;
@@ -42,6 +43,10 @@ struct l3m_model {
     int          prefilled;    // positions the last generate call prefilled
     int          logits_fresh;
     double       tokens, ns;
+    int          cold;         // evict the caches before each forward pass (engine.c:330-338)
+    void        *evict;        // EVICT_BYTES of device memory read to evict them
+    double       cold_ns;      // host time spent evicting since the last perf read (not token time)
+    double       cold_ns_all;  // the same since load
     double       weight_bytes, attn_bytes, ffn_bytes, head_bytes;
     char         desc[256];
 };
@@ -313,7 +318,7 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     // 32-blocks): unless L3M_PREFILL=0
     const char *pe_ = getenv("L3M_PREFILL"), *pm_ = getenv("L3M_PREFILL_MIN");
     const int qb_ = d->dim % 32 == 0 && (d->n_heads * d->hd) % 32 == 0 && d->ffn % 32 == 0;
-    if ((!pe_ || strcmp(pe_, "0")) && !m->reference && !gpt2 && qb_ &&
+    if ((!pe_ || strcmp(pe_, "0")) && !m->reference && !gpt2 && qb_ && l3m_prefill_fits(d->dim, d->ffn, d->n_heads * d->hd, d->hd) &&
         (m->dtype == L3M_Q8_0 || m->dtype == L3M_Q4_0 || (m->dtype == L3M_MXFP4 && mxfp4_body_widens(f, d->n_layers))))
         m->pf = calloc((size_t)d->n_layers, sizeof *m->pf);
     m->prefill_min = pm_ ? atoi(pm_) : 8;
@@ -484,9 +489,9 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
         if (lh > m->lds_decode) m->lds_decode = lh;
         if (m->lds_decode < lds_max / 2 + 16) m->lds_decode = lds_max / 2 + 16;
         const char *pe = getenv("L3M_PERSIST");
-        m->persist = (!pe || strcmp(pe, "0")) && !gpt2 && d->head.dtype == d->body_dtype && d->n_groups <= 64 && d->n_chunks <= 64 &&
-                     d->vocab <= 0x20000 && m->head_tpw <= 64 && m->lds_decode <= lds_max &&
-                     l3m_decode_fits(d->body_dtype, m->grid, m->lds_decode);
+        m->persist = (!pe || strcmp(pe, "0")) && !gpt2 && l3m_decode_pair(d->body_dtype, d->head.dtype) && d->n_groups <= 64 &&
+                     d->n_chunks <= 64 && d->vocab <= 0x20000 && m->head_tpw <= 64 && m->lds_decode <= lds_max &&
+                     l3m_decode_fits(d->body_dtype, d->head.dtype, m->grid, m->lds_decode);
         int *xcc = m->persist ? calloc((size_t)m->grid, sizeof *xcc) : NULL;
         if (xcc && !l3m_decode_placement(m->grid, m->lds_decode, xcc)) {
             int count[16] = {0};
@@ -521,6 +526,8 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
         !d->kc || !d->vc || !d->rope || !d->norm || !m->tok_host || !m->logits || !m->sync || !m->layers_dev || !m->run_dev ||
         !m->dm_dev || l3m_dev_upload(m->dm_dev, d, sizeof *d))
         return fail(m, "device allocation failed");
+    m->cold = o.cold != 0;
+    if (m->cold && !(m->evict = dalloc(m, EVICT_BYTES))) return fail(m, "--cold: no device memory for the eviction buffer");
     const char *g = getenv("L3M_GRAPH");
     if (!g || strcmp(g, "0")) {
         m->graphs = l3m_graphs_build(d, m->layers);
@@ -560,7 +567,7 @@ static int decode_launch(l3m_model *m, int first, int last, int head_from) {
     l3m_run r = {first, last - first + 1, head_from, m->head_tpw, m->n_head, m->body_xcc, m->sync, 100000000ull,   // waits end after 1 s
                  m->temp, 0};
     if (l3m_dev_upload(m->run_dev, &r, sizeof r)) return -1;
-    if (l3m_decode_launch(d->body_dtype, m->dm_dev, m->layers_dev, m->run_dev, m->grid, m->lds_decode, NULL)) return -1;
+    if (l3m_decode_launch(d->body_dtype, d->head.dtype, m->dm_dev, m->layers_dev, m->run_dev, m->grid, m->lds_decode, NULL)) return -1;
     if (l3m_dev_download(&abort_flag, m->sync + L3M_SYNC_ABORT, 4)) return -1;
     if (l3m_decode_timer(2, NULL, NULL)) return -1;
     for (int p = first; p <= last; p++) {
@@ -577,6 +584,18 @@ static int decode_launch(l3m_model *m, int first, int last, int head_from) {
 
 static int step(l3m_model *m, int with_head) {
     return m->graphs ? l3m_graphs_launch(m->graphs, with_head, NULL) : l3m_step_enqueue(&m->dm, m->layers, with_head, NULL);
+}
+
+// --cold (engine.c:330-338): the caches are emptied of the weights before a forward pass; the eviction is
+// not token time. The queue is drained first, so the time counted is the eviction's alone.
+static int evict(l3m_model *m) {
+    if (l3m_dev_sync()) return -1;
+    const double t0 = now_ns();
+    if (l3m_dev_evict(m->evict, EVICT_BYTES, NULL) || l3m_dev_sync()) return -1;
+    const double dt = now_ns() - t0;
+    m->cold_ns += dt;
+    m->cold_ns_all += dt;
+    return 0;
 }
 
 // Run forward passes for positions 0..last (prompt, then greedy or sampled tokens); calls back per the
@@ -597,13 +616,16 @@ static int run(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, f
     int next = 0;
     m->prefilled = 0;
     if (m->pf && n_prompt - 1 >= m->prefill_min && n_prompt - 1 >= 1) {
-        if (l3m_prefill(d, m->pf, &m->pfb, n_prompt - 1, NULL)) return -1;
+        if ((m->cold && evict(m)) || l3m_prefill(d, m->pf, &m->pfb, n_prompt - 1, NULL)) return -1;
         next = m->prefilled = n_prompt - 1;
     }
     if (l3m_dev_upload(d->pos, &next, 4)) return -1;
     for (; next <= last && stop < 0;) {
         int end = next + NSLOTS - 1 < last ? next + NSLOTS - 1 : last;
-        if (m->persist) {
+        if (m->cold) {                                 // one forward pass per launch, each after an eviction
+            for (int p = next; p <= end; p++)
+                if (evict(m) || (m->persist ? decode_launch(m, p, p, n_prompt - 1) : step(m, p >= n_prompt - 1))) return -1;
+        } else if (m->persist) {
             if (decode_launch(m, next, end, n_prompt - 1)) return -1;
         } else {
             for (int p = next; p <= end; p++)
@@ -633,11 +655,6 @@ int l3m_generate(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new,
     if (n_prompt < 1 || n_prompt >= m->dm.ctx) return 0;
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= m->dm.vocab) { fprintf(stderr, "l3m: token %d out of range\n", prompt[i]); return -1; }
-    if (temperature > 0 && (m->dm.vocab % 4 || m->dm.vocab > L3M_SAMPLE_MAX_VOCAB)) {
-        fprintf(stderr, "l3m: temperature sampling on the GPU needs a vocabulary that is a multiple of 4 and at most %d\n",
-                L3M_SAMPLE_MAX_VOCAB);
-        return -1;
-    }
     double t0 = now_ns();
     int n = run(m, prompt, n_prompt, max_new < 0 ? 0 : max_new, temperature, seed, on_token, user);
     m->ns += now_ns() - t0;
@@ -665,12 +682,14 @@ int l3m_encode(const l3m_model *m, const char *text, int add_bos, int32_t *out, 
 }
 const char *l3m_decode(const l3m_model *m, int32_t tok, int *len) { return (const char *)l3m_vocab_decode(&m->f.tok, tok, len); }
 
-// Counters since the last read (src/l3m.h:21-29): time per generated token from the host clock around
-// each generate call; weight bytes streamed per token; the CPU-side counters have no GPU meaning (NAN).
+// Counters since the last read (src/l3m.h:21-29): time per forward pass from the host clock around each
+// generate call, less the --cold evictions (engine.c:584); weight bytes streamed per token; the CPU-side
+// counters (L2 bytes, L3 misses, DRAM bytes, energy, LLC occupancy) have no GPU meaning here (NAN); the host
+// never waits on ranks, so ns_wait is 0 and ns_compute is the whole token.
 int l3m_perf_read(l3m_model *m, l3m_perf *out) {
-    const double n = m->tokens, spent = m->ns;
-    m->tokens = m->ns = 0;
-    *out = (l3m_perf){.l3_miss = NAN, .dram_bytes = NAN, .energy_j = NAN, .llc_occupancy = NAN};
+    const double n = m->tokens, spent = m->ns - m->cold_ns;
+    m->tokens = m->ns = m->cold_ns = 0;
+    *out = (l3m_perf){.l2_bytes = NAN, .l3_miss = NAN, .dram_bytes = NAN, .energy_j = NAN, .llc_occupancy = NAN};
     if (!(n > 0)) return -1;
     out->tokens = n;
     out->ns_token = out->ns_compute = spent / n;
@@ -707,8 +726,7 @@ void l3m_print_hw(FILE *out) {
 
 double l3m_bench_decode_t(l3m_model *m, const int32_t *prompt, int n_prompt, int n_tokens, float temperature, uint64_t seed) {
     if (n_prompt < 1 || n_prompt >= m->dm.ctx) return -1;
-    if (temperature > 0 && (m->dm.vocab % 4 || m->dm.vocab > L3M_SAMPLE_MAX_VOCAB)) return -1;
-    double t0 = now_ns();
+    const double t0 = now_ns(), c0 = m->cold_ns_all;
     int done = 0;
     for (int tries = 0; done < n_tokens; tries++) {   // main.c:251: restart when the context is full
         int want = n_tokens - done, room = m->dm.ctx - n_prompt;
@@ -716,7 +734,7 @@ double l3m_bench_decode_t(l3m_model *m, const int32_t *prompt, int n_prompt, int
         if (n < 0 || (n == 0 && (!(temperature > 0) || tries > 64))) return -1;   // a sampled EOS may end a run early
         done += n;
     }
-    return (now_ns() - t0) / done;
+    return (now_ns() - t0 - (m->cold_ns_all - c0)) / done;   // --cold: evictions are not token time
 }
 
 double l3m_bench_decode(l3m_model *m, const int32_t *prompt, int n_prompt, int n_tokens) {
@@ -740,6 +758,17 @@ double l3m_weight_bytes(const l3m_model *m) { return m->weight_bytes; }
 int l3m_decode_persistent(const l3m_model *m) { return m->persist; }
 
 int l3m_prefill_positions(const l3m_model *m) { return m->prefilled; }
+
+int l3m_decode_attention(const l3m_model *m) {
+    return l3m_attention_mode(m->dm.kv_lds, m->dm.hd, m->dm.n_heads / m->dm.n_groups, m->dm.ctx);
+}
+
+int l3m_kv_rows(const l3m_model *m, int layer, int kvh, int pos0, int n, uint16_t *k, uint16_t *v) {
+    const l3m_dmodel *d = &m->dm;
+    if (layer < 0 || layer >= d->n_layers || kvh < 0 || kvh >= d->n_kv || pos0 < 0 || n < 1 || pos0 + n > d->ctx) return -1;
+    const size_t at = (((size_t)layer * d->n_kv + kvh) * d->ctx + pos0) * d->hd, bytes = (size_t)n * d->hd * 2;
+    return l3m_dev_download(k, d->kc + at, bytes) || l3m_dev_download(v, d->vc + at, bytes) ? -1 : 0;
+}
 
 int l3m_logits_at(const l3m_model *m, int pos, float *out) {
     if (m->logits_pos < 0 || pos > m->logits_pos || pos <= m->logits_pos - NSLOTS || pos < 0) return -1;

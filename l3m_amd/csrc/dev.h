@@ -69,7 +69,6 @@ typedef struct {
     const float *pos_embed;      // the learned position rows [ctx][dim]
     int          gpt2, pad_g2;
 } l3m_dmodel;
-#define L3M_SAMPLE_MAX_VOCAB (64 * 1024)   // logits held in one workgroup's registers (64 per thread)
 
 // One launch of the persistent decode kernel: steps at positions pos0 .. pos0 + nsteps - 1; logits (and
 // the argmax token at pos + 1) for positions >= head_from. The body runs on the workgroups of XCD
@@ -155,16 +154,19 @@ typedef struct {
 // K/V rows of positions 0..P-1 of every layer from the token ids on the device (m->tokens); the last
 // layer's FFN is skipped (nothing reads it). -1 on a launch error.
 int l3m_prefill(const l3m_dmodel *m, const l3m_pflayer *layers, const l3m_pfbuf *b, int P, void *stream);
+// 1 when l3m_prefill takes a model of these sizes (nqd = n_heads * hd); the loader enables prefill only then.
+int l3m_prefill_fits(int dim, int ffn, int nqd, int hd);
 
 // The persistent decode kernel (one cooperative launch for R->nsteps steps; layers_dev in device memory).
 int l3m_dev_cus(void);
 // The XCD each block of a cooperative grid of `grid` 1024-thread workgroups with lds bytes lands on
 // (xcc[grid]); 0, or -1 on a device error.
 int l3m_decode_placement(int grid, unsigned lds, int *xcc);
-int l3m_decode_fits(int dtype, int grid, unsigned lds);     // 1 if grid workgroups with lds bytes can all be resident
+int l3m_decode_pair(int dtype, int head_dtype);              // 1 if the kernel is built for this (body, head) pair
+int l3m_decode_fits(int dtype, int head_dtype, int grid, unsigned lds);   // 1 if grid workgroups with lds bytes can all be resident
 // m_dev, layers_dev, r_dev: device-memory copies (the kernel reads its parameters from there)
-int l3m_decode_launch(int dtype, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev, int grid, unsigned lds,
-                      void *stream);
+int l3m_decode_launch(int dtype, int head_dtype, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev, int grid,
+                      unsigned lds, void *stream);
 
 // Timing (microseconds per launch, hipEvents on the library stream, after one untimed launch).
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);

@@ -12,6 +12,7 @@
 // ---------------------------------------------------------------- mapped file (reference file.h:17-22)
 typedef struct {
     int             n, bos, eos, max_len;
+    int             merges;       // some piece is longer than one byte: the byte-level encoder refuses
     const uint8_t **bytes;
     const uint16_t *len;
 } l3m_vocab_table;

@@ -11,6 +11,7 @@
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include "dev.h"
 #include "format.h"
@@ -355,6 +356,16 @@ extern "C" __global__ void __launch_bounds__(NT) k_dummy() {}
 // (FETCH_SIZE, WRITE_SIZE) against which the step kernels' traffic is read.
 __global__ void __launch_bounds__(NT) k_copy(u32x4 *__restrict__ dst, const u32x4 *__restrict__ src, size_t n16) {
     for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n16; i += (size_t)gridDim.x * NT) dst[i] = src[i];
+}
+
+// One streaming read of n16 16-byte words: the --cold eviction (engine.c:330-338). Read through L2 and the
+// Infinity Cache, a buffer larger than the Infinity Cache leaves none of the weights in either. sink keeps
+// the loads.
+__global__ void __launch_bounds__(NT) k_evict(const u32x4 *__restrict__ buf, size_t n16, unsigned *sink) {
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n16; i += (size_t)gridDim.x * NT) acc ^= gp<u32x4>(buf)[i];
+    const unsigned v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (v == 0x9E3779B9u) gw(sink)[0] = v;            // practically never: keeps the loads
 }
 
 template <int DT>
@@ -1003,6 +1014,14 @@ __host__ __device__ inline size_t work_bytes(size_t a, size_t b) {
 // consecutive rows' same 16 bytes on 16 different 4-bank groups, so reads down a column (the MFMA
 // operand layout) are free of bank conflicts.
 __host__ __device__ inline int kv_row(int hd) { return hd + 8; }
+// Which attention the decode step runs for a head group of nq query heads: 2 on the matrix cores
+// (attend_mfma: the K/V window in LDS, hd a multiple of 32, the q parts beside the wavefront sums in vred,
+// the scores and p parts within the 16 KiB minimum of the work region), 1 the VALU split softmax over the
+// LDS window, 0 the VALU split softmax reading K and V from the cache.
+__host__ __device__ inline int att_mode(int kv_lds, int hd, int nq, int ctx) {
+    if (!kv_lds) return 0;
+    return hd % 32 == 0 && 6 * nq * hd <= 4 * NWE * hd && 10 * ((ctx + 31) & ~31) <= 16 * NTE ? 2 : 1;
+}
 struct LdsA { size_t act, work, q, cur, cs, vred, att, act2, scr, kvb, total; };
 __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g, int kv_lds) {
     LdsA L;
@@ -1415,7 +1434,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
     const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
     // the matrix-core attention (LDS window, hd a multiple of 32, q parts fit beside vred's 2 NWE sums)
-    const bool mfma_att = M.kv_lds && hd % 32 == 0 && 6 * nqd <= 4 * NWE * hd;
+    const bool mfma_att = att_mode(M.kv_lds, hd, G.nq, M.ctx) == 2;
     __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
     rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner, bool lead) {
         if constexpr (G2) y += G.bqkv[i];            // the GPT-2 variant's q, k, v biases; no RoPE
@@ -1640,52 +1659,96 @@ __device__ __forceinline__ int block_min_int(int v, int *iscr) {
     return v;
 }
 
-constexpr int SAMPLE_F4 = L3M_SAMPLE_MAX_VOCAB / NTE / 4;   // float4 of logits per thread at most
-static_assert(SAMPLE_F4 * 4 * NTE == L3M_SAMPLE_MAX_VOCAB, "the vocabulary bound is whole float4 per thread");
-
-// One workgroup samples a token from the V logits at lg (V % 4 == 0, V <= L3M_SAMPLE_MAX_VOCAB), given
-// their maximum gmax and the draw k (engine.c:364-379): the first i whose running sum of weights passes
-// k * 2^-53 times their total, or V - 1 when none does. Thread t owns float4 [t per4, (t + 1) per4); a
-// block scan gives each range the sum of those before it and every thread walks its own range at once;
-// the lowest crossing wins. lg is read with device-coherent loads (other workgroups wrote it). uscr: NWE
-// words, iscr: NWE ints of LDS. Every thread gets the token.
+// One workgroup samples a token from the V logits at lg, given their maximum gmax and the draw k
+// (engine.c:364-379): the first i whose running sum of weights passes k * 2^-53 times their total, or V - 1
+// when none does. Thread t owns logits [t per, (t + 1) per), per = ceil(V / NTE): it sums its weights, a
+// block scan gives each range the sum of those before it, and every thread walks its own range again
+// (the same weights, recomputed); the lowest crossing wins. Any V. lg is read with device-coherent
+// loads (other workgroups wrote it). uscr: NWE words, iscr: NWE ints of LDS. Every thread gets the token.
 __device__ int sample_block(const float *lg, int V, float gmax, float temp, unsigned long long k, unsigned long long *uscr, int *iscr) {
-    const int tid = tidx();
-    const int V4 = V >> 2, per4 = (V4 + NTE - 1) / NTE, f0 = tid * per4;
-    float p[4 * SAMPLE_F4];
-#pragma unroll
-    for (int j = 0; j < SAMPLE_F4; j++) {             // unconditional (clamped) loads, all in flight at once
-        const int f = f0 + j < V4 ? f0 + j : V4 - 1;
-        const float4 v = ld16f<true>(lg, f);
-        p[4 * j] = v.x; p[4 * j + 1] = v.y; p[4 * j + 2] = v.z; p[4 * j + 3] = v.w;
-    }
+    const int tid = tidx(), per = (V + NTE - 1) / NTE, i0 = tid * per, i1 = i0 + per < V ? i0 + per : V;
+    auto weight = [&](int i) {
+        return fixp(sample_weight(__hip_atomic_load(gp<float>(lg + i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), gmax, temp));
+    };
     unsigned long long sum = 0;
-#pragma unroll
-    for (int j = 0; j < SAMPLE_F4; j++) {
-        if (j < per4) {                               // uniform
-            const bool in = f0 + j < V4;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                p[4 * j + e] = in ? sample_weight(p[4 * j + e], gmax, temp) : 0.0f;
-                sum += fixp(p[4 * j + e]);
-            }
-        }
-    }
+    for (int i = i0; i < i1; i++) sum += weight(i);
     unsigned long long z;
     unsigned long long c = block_scan_u64(sum, z, uscr);
     int cand = 0x7FFFFFFF;
-#pragma unroll
-    for (int j = 0; j < SAMPLE_F4; j++) {
-        if (j < per4) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                c += fixp(p[4 * j + e]);
-                if (f0 + j < V4 && cand == 0x7FFFFFFF && crosses(c, k, z)) cand = 4 * (f0 + j) + e;
-            }
-        }
+    for (int i = i0; i < i1; i++) {
+        c += weight(i);
+        if (crosses(c, k, z)) { cand = i; break; }
     }
     const int tok = block_min_int(cand, iscr);
     return tok == 0x7FFFFFFF ? V - 1 : tok;
+}
+
+// ------------------------------------------------------------------ pieces of the decode step, alone
+// For parity tests: the decode step's own device code on inputs the caller gives.
+
+// Rows [row0, row0 + n) of a lane-tile matrix exactly dequantized by lt_elem4, the step's embedding lookup
+// (engine.c:236, pack.c:55-62): out[r][0, 32 nb), one thread per 4 elements.
+__global__ void __launch_bounds__(NT) k_dequant(l3m_dmat m, int row0, int n, float *out) {
+    const int k4 = m.nb * 8;
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= (size_t)n * k4) return;
+    const int r = (int)(i / (size_t)k4), c = (int)(i - (size_t)r * k4);
+    const float4 v = lt_elem4(m, row0 + r, 4 * c);
+    ((float4 *)out)[i] = v;
+}
+
+// LDS regions of k_attend_decode (byte offsets), in the order the attention block keeps them.
+struct LdsAtt { size_t qh, att, cur, vred, sc, kvb, total; };
+__host__ __device__ inline LdsAtt lds_att(int mode, int nq, int nkv, int hd, int ctx) {
+    LdsAtt L;
+    size_t o = 0;
+    const size_t nqd = (size_t)nq * hd, vr = 4 * (size_t)NWE * (hd + 2), vq = 8 * (size_t)NWE + 6 * nqd;
+    L.qh = o;   o += align16(4 * nqd);
+    L.att = o;  o += align16(4 * nqd);
+    L.cur = o;  o += align16(4 * (size_t)nkv * hd);
+    L.vred = o; o += align16(vr > vq ? vr : vq);
+    L.sc = o;   o += mode == 2 ? align16(10 * (size_t)((ctx + 31) & ~31)) : 0;
+    L.kvb = o;  o += mode ? align16(4 * (size_t)nkv * ctx * kv_row(hd)) : 0;
+    L.total = o;
+    return L;
+}
+
+// One head group's attention exactly as the decode step runs it (attn_block): MODE 2 attend_mfma, 1
+// attend_group over the LDS window, 0 attend_group reading the cache. q: [nq][hd] f32 (after RoPE);
+// kc, vc: [nkv][ctx][hd] bf16 holding rows 0..pos (row pos is this step's, which the block takes from its
+// own registers into cur and the window); out: [nq][hd]. Query head h reads kv head h / (nq / nkv).
+template <int MODE>
+__global__ void __launch_bounds__(NTE) k_attend_decode(float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
+                                                       int nkv, int hd, int ctx, int pos, int att_wl) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const LdsAtt L = lds_att(MODE, nq, nkv, hd, ctx);
+    float *qh = (float *)(smem + L.qh), *att = (float *)(smem + L.att), *vred = (float *)(smem + L.vred), *sc = (float *)(smem + L.sc);
+    uint16_t *cur = (uint16_t *)(smem + L.cur), *kvb = (uint16_t *)(smem + L.kvb);
+    __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
+    l3m_dmodel M{};
+    M.hd = hd; M.ctx = ctx; M.n_kv = nkv; M.hpk = nq / nkv; M.att_scale = 1.0f / sqrtf((float)hd); M.kv_lds = MODE != 0;
+    M.kc = (uint16_t *)kc; M.vc = (uint16_t *)vc;
+    l3m_dgroup G{};
+    G.q0 = 0; G.nq = nq; G.kv0 = 0; G.nkv = nkv; G.att_wl = att_wl;
+    const int nqd = nq * hd, nkd = nkv * hd;
+    if (MODE) kv_window_dma<false>(kvb, M, 0, 0, nkv, pos);
+    for (int i = tidx(); i < nqd; i += NTE) {
+        const float y = q[i];
+        qh[i] = y;
+        if (MODE == 2) split3(y, qp[i], qp[nqd + i], qp[2 * nqd + i]);
+    }
+    for (int i = tidx(); i < 2 * nkd; i += NTE) {     // this step's k, v rows, as the block stores them
+        const int kv = i < nkd ? 0 : 1, jj = i - kv * nkd, kvl = jj / hd, d = jj - kvl * hd;
+        const uint16_t hb = (kv ? vc : kc)[((size_t)kvl * ctx + pos) * hd + d];
+        cur[i] = hb;
+        if (MODE) kvb[((size_t)(kv * nkv + kvl) * ctx + pos) * kv_row(hd) + d] = hb;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (MODE == 2) attend_mfma(M, G, pos, qp, kvb, sc, vred, att);
+    else if (MODE == 1) attend_group<true, false>(M, G, 0, pos, qh, cur, kvb, vred, att);
+    else attend_group<false, false>(M, G, 0, pos, qh, cur, kvb, vred, att);
+    for (int i = tidx(); i < nqd; i += NTE) out[i] = att[i];
 }
 
 // ------------------------------------------------------------------ the graph path: one kernel per block
@@ -2189,7 +2252,9 @@ __device__ int deal_role(const l3m_run &R, int n_body, int *lds) {
     return role;
 }
 
-template <int DT>
+// DT: the body's dtype, HDT: the head's (a file may quantize its head differently, as the reference's
+// exporter allows: test_engine.py:187-191).
+template <int DT, int HDT>
 __global__ void __launch_bounds__(NTE) k_decode(const l3m_dmodel *__restrict__ Mp, const l3m_dlayer *__restrict__ layers,
                                                 const l3m_run *__restrict__ Rp) {
     __shared__ int role_lds;
@@ -2202,7 +2267,7 @@ __global__ void __launch_bounds__(NTE) k_decode(const l3m_dmodel *__restrict__ M
         } else if (role < n_body) {
             if (!ffn_role<DT>(Mp, layers, Rp, role - n_groups, s)) return;
         } else if (R.pos0 + s >= R.head_from && role - n_body < R.n_head) {
-            if (!head_role<DT>(Mp, Rp, role - n_body, s)) return;
+            if (!head_role<HDT>(Mp, Rp, role - n_body, s)) return;
         }
     }
     // the last step's token has no next step in this launch to take it: group 0 writes it
@@ -2545,15 +2610,15 @@ template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t
 hipEvent_t g_dec_ev[2];
 int g_dec_timing, g_dec_launches, g_dec_pending;
 double g_dec_us;
-template <int DT> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *layers, const l3m_run *R_dev, int grid, unsigned lds,
-                                    hipStream_t st) {
-    lds_opt_in(k_decode<DT>, lds);
+template <int DT, int HDT> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *layers, const l3m_run *R_dev, int grid,
+                                             unsigned lds, hipStream_t st) {
+    lds_opt_in(k_decode<DT, HDT>, lds);
     const l3m_dmodel *m = M_dev;
     const l3m_dlayer *ly = layers;
     const l3m_run *r = R_dev;
     void *args[] = {&m, &ly, &r};
     if (g_dec_timing) CK(hipEventRecord(g_dec_ev[0], st));
-    const hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode<DT>, dim3(grid), dim3(NTE), args, lds, st);
+    const hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode<DT, HDT>, dim3(grid), dim3(NTE), args, lds, st);
     if (e != hipSuccess) return fail("decode launch", e);
     if (g_dec_timing) {
         CK(hipEventRecord(g_dec_ev[1], st));
@@ -2561,10 +2626,10 @@ template <int DT> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *l
     }
     return 0;
 }
-template <int DT> int decode_fits(int grid, unsigned lds) {
-    lds_opt_in(k_decode<DT>, lds);
+template <int DT, int HDT> int decode_fits(int grid, unsigned lds) {
+    lds_opt_in(k_decode<DT, HDT>, lds);
     int per_cu = 0, cus = 0, coop = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode<DT>, NTE, lds) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode<DT, HDT>, NTE, lds) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, 0) != hipSuccess || !coop) return 0;
     return per_cu >= 1 && grid <= per_cu * cus;
@@ -2580,6 +2645,19 @@ struct l3m_graphs {
 };
 
 extern "C" {
+
+// Everything the library created on the device that no model owns (the stream, the decode timer's
+// events), destroyed at exit before the runtime is torn down (registered with atexit after the runtime's
+// own handlers, so it runs first). Calls after it fail cleanly.
+static void dev_shutdown(void) {
+    if (g_ready != 1) return;
+    (void)hipStreamSynchronize(g_stream);
+    for (int i = 0; i < 2; i++)
+        if (g_dec_ev[i]) { (void)hipEventDestroy(g_dec_ev[i]); g_dec_ev[i] = nullptr; }
+    (void)hipStreamDestroy(g_stream);
+    g_stream = nullptr;
+    g_ready = 0;
+}
 
 int l3m_dev_init(void) {
     if (g_ready >= 0) return g_ready ? 0 : -1;
@@ -2603,6 +2681,7 @@ int l3m_dev_init(void) {
     CKL("first launch");
     CK(hipStreamSynchronize(g_stream));
     g_ready = 1;
+    atexit(dev_shutdown);
     return 0;
 }
 
@@ -2703,6 +2782,44 @@ int l3m_dev_copy(void *dst, const void *src, size_t bytes, void *stream) {
     return 0;
 }
 
+int l3m_dev_evict(const void *buf, size_t bytes, void *stream) {
+    if (bytes < 16 || bytes % 16 || (uintptr_t)buf % 16) return fail_msg("evict: 16-byte multiples and alignment");
+    const size_t n16 = bytes / 16;
+    // the last 16-byte word is the sink: it is never read past the first n16 - 1 words' xor
+    hipLaunchKernelGGL(k_evict, dim3(4 * (unsigned)l3m_dev_cus()), dim3(NT), 0, as_stream(stream), (const u32x4 *)buf, n16 - 1,
+                       (unsigned *)((u32x4 *)buf + n16 - 1));
+    CKL("k_evict");
+    return 0;
+}
+
+int l3m_k_dequant(const l3m_dmat *m, int row0, int n, float *out, void *stream) {
+    if (m->dtype < 0 || m->dtype >= L3M_NDTYPES || n < 1 || row0 < 0 || row0 + n > m->tiles * RT || m->nb < 1)
+        return fail_msg("dequant: rows out of range");
+    const size_t k4 = (size_t)m->nb * 8, threads = (size_t)n * k4;
+    hipLaunchKernelGGL(k_dequant, dim3((unsigned)((threads + NT - 1) / NT)), dim3(NT), 0, as_stream(stream), *m, row0, n, out);
+    CKL("k_dequant");
+    return 0;
+}
+
+int l3m_attention_mode(int kv_lds, int hd, int nq, int ctx) { return att_mode(kv_lds, hd, nq, ctx); }
+
+int l3m_k_attend_decode(int mode, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int nq, int nkv, int hd, int ctx,
+                        int pos, void *stream) {
+    if (l3m_dev_init()) return -1;
+    if (mode < 0 || mode > 2 || hd < 8 || hd % 8 || hd > 256 || nq < 1 || nkv < 1 || nq % nkv || pos < 0 || pos >= ctx ||
+        (mode == 2 && att_mode(1, hd, nq, ctx) != 2))
+        return fail_msg("attend_decode: shape out of range for this mode");
+    const size_t lds = lds_att(mode, nq, nkv, hd, ctx).total;
+    if (lds > g_lds_max) return fail_msg("attend_decode: the K/V window does not fit in LDS");
+    int wmax = nq < NWE ? NWE / nq : 1, wl = 0;       // as l3m_group_layout
+    while ((2 << wl) <= wmax) wl++;
+    auto k = mode == 2 ? k_attend_decode<2> : mode == 1 ? k_attend_decode<1> : k_attend_decode<0>;
+    lds_opt_in(k, (unsigned)lds);
+    hipLaunchKernelGGL(k, dim3(1), dim3(NTE), lds, as_stream(stream), out, q, kc, vc, nq, nkv, hd, ctx, pos, wl);
+    CKL("k_attend_decode");
+    return 0;
+}
+
 int l3m_k_argmax(const float *x, int n, int32_t *out, void *stream) {
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(NT), 0, as_stream(stream), x, n, out);
     CKL("k_argmax");
@@ -2739,10 +2856,15 @@ int l3m_step_slots(int dtype, int which) {
     return dtype == L3M_F32 ? nslot_a<L3M_F32>() : dtype == L3M_BF16 ? nslot_a<L3M_BF16>() : dtype == L3M_Q8_0 ? nslot_a<L3M_Q8_0>() : nslot_a<L3M_Q4_0>();
 }
 
+// The shapes the prefill kernels take: one workgroup's 4 values per thread cover dim, ffn and n_heads * hd
+// (the per-token norm and prep), and k_pf_attend's q row and outputs cover hd.
+int l3m_prefill_fits(int dim, int ffn, int nqd, int hd) {
+    return dim <= 4 * NTE && ffn <= 4 * NTE && nqd <= 4 * NTE && hd <= 256 && hd % 2 == 0;
+}
+
 int l3m_prefill(const l3m_dmodel *M, const l3m_pflayer *L, const l3m_pfbuf *B, int P, void *stream) {
     if (P < 1) return 0;
-    if (P > M->ctx || M->dim > 4 * NTE || M->ffn > 4 * NTE || M->n_heads * M->hd > 4 * NTE || M->hd > 256 || M->hd % 2)
-        return fail_msg("prefill: shape out of range");
+    if (P > M->ctx || !l3m_prefill_fits(M->dim, M->ffn, M->n_heads * M->hd, M->hd)) return fail_msg("prefill: shape out of range");
     hipStream_t st = as_stream(stream);
     const int dim = M->dim, hd = M->hd, nq = M->n_heads * hd, width = nq + 2 * M->n_kv * hd;
     auto gemm = [&](const l3m_dmat &W, float *y, int ystride, int add) {
@@ -2785,15 +2907,24 @@ int l3m_dev_cus(void) {
     return cus;
 }
 
-int l3m_decode_fits(int dtype, int grid, unsigned lds) {
+// The (body, head) dtype pairs the persistent kernel is built for: every dtype with a head of its own
+// dtype, and the mixed heads of the reference's tests (test_engine.py:187-191).
+#define DECODE_PAIRS(X) \
+    X(L3M_F32, L3M_F32) X(L3M_BF16, L3M_BF16) X(L3M_Q8_0, L3M_Q8_0) X(L3M_Q4_0, L3M_Q4_0) X(L3M_MXFP4, L3M_MXFP4) \
+    X(L3M_Q4_0, L3M_Q8_0) X(L3M_MXFP4, L3M_Q8_0) X(L3M_Q8_0, L3M_BF16)
+
+int l3m_decode_pair(int dtype, int head_dtype) {
+#define PAIR_KNOWN(a, b) if (dtype == a && head_dtype == b) return 1;
+    DECODE_PAIRS(PAIR_KNOWN)
+#undef PAIR_KNOWN
+    return 0;
+}
+
+int l3m_decode_fits(int dtype, int head_dtype, int grid, unsigned lds) {
     if (l3m_dev_init()) return 0;
-    switch (dtype) {
-    case L3M_F32: return decode_fits<L3M_F32>(grid, lds);
-    case L3M_BF16: return decode_fits<L3M_BF16>(grid, lds);
-    case L3M_Q8_0: return decode_fits<L3M_Q8_0>(grid, lds);
-    case L3M_Q4_0: return decode_fits<L3M_Q4_0>(grid, lds);
-    case L3M_MXFP4: return decode_fits<L3M_MXFP4>(grid, lds);
-    }
+#define PAIR_FITS(a, b) if (dtype == a && head_dtype == b) return decode_fits<a, b>(grid, lds);
+    DECODE_PAIRS(PAIR_FITS)
+#undef PAIR_FITS
     return 0;
 }
 
@@ -2836,17 +2967,13 @@ int l3m_decode_placement(int grid, unsigned lds, int *xcc) {
     return e == hipSuccess ? 0 : fail("placement probe", e);
 }
 
-int l3m_decode_launch(int dtype, const l3m_dmodel *M_dev, const l3m_dlayer *layers_dev, const l3m_run *R_dev, int grid, unsigned lds,
-                      void *stream) {
+int l3m_decode_launch(int dtype, int head_dtype, const l3m_dmodel *M_dev, const l3m_dlayer *layers_dev, const l3m_run *R_dev, int grid,
+                      unsigned lds, void *stream) {
     hipStream_t st = as_stream(stream);
-    switch (dtype) {
-    case L3M_F32: return launch_decode<L3M_F32>(M_dev, layers_dev, R_dev, grid, lds, st);
-    case L3M_BF16: return launch_decode<L3M_BF16>(M_dev, layers_dev, R_dev, grid, lds, st);
-    case L3M_Q8_0: return launch_decode<L3M_Q8_0>(M_dev, layers_dev, R_dev, grid, lds, st);
-    case L3M_Q4_0: return launch_decode<L3M_Q4_0>(M_dev, layers_dev, R_dev, grid, lds, st);
-    case L3M_MXFP4: return launch_decode<L3M_MXFP4>(M_dev, layers_dev, R_dev, grid, lds, st);
-    }
-    return fail_msg("decode: bad dtype");
+#define PAIR_LAUNCH(a, b) if (dtype == a && head_dtype == b) return launch_decode<a, b>(M_dev, layers_dev, R_dev, grid, lds, st);
+    DECODE_PAIRS(PAIR_LAUNCH)
+#undef PAIR_LAUNCH
+    return fail_msg("decode: no persistent kernel for this pair of dtypes");
 }
 
 l3m_graphs *l3m_graphs_build(const l3m_dmodel *M, const l3m_dlayer *layers) {
@@ -2897,6 +3024,26 @@ double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, f
     if (l3m_dev_init() || n_mats < 1 || iters < 1) return -1;
     GemvCtx c{mats, n_mats, act, k, y};
     return time_launches(iters, gemv_one, &c);
+}
+
+// The measured roofline of a matvec: one streaming read of the same number of bytes, in the same
+// residency (the same buffer again: warm; round robin over buffers totalling more than the Infinity
+// Cache: cold). Each launch reads one buffer with enough workgroups for every CU.
+struct ReadCtx { void *const *bufs; int n; size_t bytes; unsigned grid; };
+static int read_one(void *c, int i) {
+    ReadCtx *r = (ReadCtx *)c;
+    void *b = r->bufs[i % r->n];
+    hipLaunchKernelGGL(k_evict, dim3(r->grid), dim3(NT), 0, g_stream, (const u32x4 *)b, r->bytes / 16 - 1, (unsigned *)((u32x4 *)b + r->bytes / 16 - 1));
+    CKL("k_evict");
+    return 0;
+}
+
+double l3m_time_read(void *const *bufs, int n_bufs, size_t bytes, int iters) {
+    if (l3m_dev_init() || n_bufs < 1 || iters < 1 || bytes < 32 || bytes % 16) return -1;
+    const size_t n16 = bytes / 16, want = (n16 + 4 * NT - 1) / (4 * NT);      // about 4 words per thread
+    const size_t cap = 4 * (size_t)l3m_dev_cus();
+    ReadCtx c{bufs, n_bufs, bytes, (unsigned)(want < 1 ? 1 : want < cap ? want : cap)};
+    return time_launches(iters, read_one, &c);
 }
 
 struct StepCtx { const l3m_dmodel *M; const l3m_dlayer *L; int kind, layer; };

@@ -4,8 +4,11 @@
 // count must fit the section at 6 bytes per token at least, and bos must be an id or negative (none).
 //
 // Decoding is exact. Encoding maps each input byte to its single-byte piece and applies no merges: text
-// tokenization is not on the decode hot path, and for files whose pieces never merge (the synthetic
-// models: the 256 bytes and empty pieces) it gives the reference's ids.
+// tokenization is not on the decode hot path, and for files whose pieces never merge (no piece of more
+// than one byte, as in the synthetic models: the 256 bytes and empty pieces) it gives the reference's
+// ids. A vocabulary with merge pieces is refused (-1, once with a message) rather than tokenized into
+// ids the reference would not produce; such callers pass token ids.
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include "host.h"
@@ -40,6 +43,8 @@ int l3m_vocab_init(l3m_vocab_table *t, const void *section, size_t size) {
         if (take(&c, NULL, len[i])) { l3m_vocab_free(t); return -1; }
     }
     t->n = (int)n;
+    t->merges = 0;
+    for (size_t i = 0; i < n; i++) t->merges |= len[i] > 1;
     t->bos = hdr.bos < 0 ? -1 : hdr.bos;
     t->eos = hdr.eos;
     t->max_len = (int)hdr.max_len;
@@ -59,6 +64,12 @@ static int piece_of_byte(const l3m_vocab_table *t, uint8_t b) {
 }
 
 int l3m_vocab_encode(const l3m_vocab_table *t, const char *text, int add_bos, int32_t *out, int max) {
+    if (t->merges) {
+        static int told;
+        if (!told++) fprintf(stderr, "l3m: this vocabulary merges bytes into longer pieces, which this backend's byte-level "
+                                     "encoder does not apply; pass token ids instead\n");
+        return -1;
+    }
     int n = 0;
     if (add_bos && t->bos >= 0) {
         if (max < 1) return -1;

@@ -56,6 +56,7 @@ class Oracle:
             "or_seed_state": (C.c_uint64, [C.c_uint64]),
             "or_sample": (C.c_int, [_f, C.c_int, C.c_float, C.POINTER(C.c_uint64)]),
             "or_generate_sampled": (C.c_int, [C.c_void_p, _i32, C.c_int, C.c_int, C.c_float, C.c_uint64, _i32]),
+            "or_kv_rows": (None, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, _u16, _u16]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -157,6 +158,17 @@ class OracleModel:
 
     def logits(self):
         return np.ctypeslib.as_array(self.o.lib.or_logits(self.h), shape=(self.vocab,)).copy()
+
+    def forward(self, tok, pos, logits=True):
+        """One position (engine.c:230-281): the logits after it when asked for (teacher forcing)."""
+        self.o.lib.or_forward(self.h, tok, pos, int(logits))
+        return self.logits() if logits else None
+
+    def kv_rows(self, layer, kvh, pos0, n, hd):
+        """bf16 K and V rows [pos0, pos0 + n) of kv head kvh in layer `layer`, uint16 [n, hd] each."""
+        k, v = np.zeros((n, hd), np.uint16), np.zeros((n, hd), np.uint16)
+        self.o.lib.or_kv_rows(self.h, layer, kvh, pos0, n, _p(k, _u16), _p(v, _u16))
+        return k, v
 
 
 class _Vec(C.Structure):

@@ -38,16 +38,38 @@ def summary(logits, k=8):
 
 
 def margins(oracle, path, prompt, tokens):
-    """Top-2 logit margin / max|logit| of the scalar engine before each generated token (the oracle is
-    bit-exact with the reference's scalar engine, checked through the prompt-logits hash)."""
+    """Before each generated token: the top-2 logit margin / max|logit| of the scalar engine, its two
+    highest-scoring ids (first maximum first) and its logits, teacher-forced over prompt + tokens. The
+    oracle is bit-exact with the reference's scalar engine (checked through the prompt-logits hash); each
+    step's argmax must be the reference's token."""
     om = oracle.load(path)
-    out, seq = [], list(prompt)
-    for t in tokens:
-        om.generate(seq, 0)
-        lg = np.sort(om.logits().astype(np.float64))
-        out.append(round(float((lg[-1] - lg[-2]) / np.abs(lg).max()), 6))
-        seq.append(t)
-    return out
+    seq, out, top2, logits = list(prompt) + list(tokens), [], [], []
+    for pos in range(len(seq) - 1):
+        lg = om.forward(seq[pos], pos, logits=pos >= len(prompt) - 1)
+        if lg is None:
+            continue
+        order = np.argsort(-lg.astype(np.float64), kind="stable")
+        assert int(order[0]) == seq[pos + 1], "the oracle left the reference's tokens"
+        lv = np.sort(lg.astype(np.float64))
+        out.append(round(float((lv[-1] - lv[-2]) / np.abs(lv).max()), 6))
+        top2.append([int(order[0]), int(order[1])])
+        logits.append(lg)
+    return out, top2, logits
+
+
+def simd_teacher_forced(ref, path, prompt, tokens, scalar_logits):
+    """The reference's SIMD table fed the scalar engine's tokens: per step its argmax, and the largest
+    max|SIMD logit - scalar logit| / max|scalar logit| over the steps (its own activation-quantization
+    spread on this model)."""
+    m = ref.load(path)
+    picks, spread = [], 0.0
+    for k, ls in enumerate(scalar_logits):
+        m.generate(list(prompt) + list(tokens[:k]), 0)
+        la = m.logits()
+        picks.append(int(np.argmax(la)))
+        spread = max(spread, float(np.abs(la.astype(np.float64) - ls).max() / np.abs(ls).max()))
+    del m
+    return picks, round(spread, 6)
 
 
 def main():
@@ -67,16 +89,19 @@ def main():
                 case[f"{mode}_last_logits"] = summary(m.logits())
                 case[f"{mode}_describe"] = m.describe()
                 del m
-            case["scalar_margins"] = margins(oracle, path, prompt, case["scalar_tokens"])
+            case["scalar_margins"], case["scalar_top2"], scalar_logits = margins(oracle, path, prompt, case["scalar_tokens"])
             os.environ["L3M_ISA"] = "avx512" if ref.usable("avx512") else "avx2"
             m = ref.load(path)
             simd = m.generate(prompt, N_GEN)
             del m
+            picks, case["simd_spread"] = simd_teacher_forced(ref, path, prompt, case["scalar_tokens"], scalar_logits)
+            case["simd_tf_disagree"] = [k for k, (a, b) in enumerate(zip(picks, case["scalar_tokens"])) if a != b]
             os.environ["L3M_ISA"] = "scalar"
             case["simd_table"] = "avx512" if ref.usable("avx512") else "avx2"
             case["simd_agree"] = next((i for i, (a, b) in enumerate(zip(simd, case["scalar_tokens"])) if a != b), N_GEN)
             print(name, dtype, case["scalar_tokens"][:8], "ref agrees on", sum(a == b for a, b in zip(case["scalar_tokens"], case["ref_tokens"])),
-                  "simd agrees on", case["simd_agree"], "min margin", min(case["scalar_margins"]), flush=True)
+                  "simd agrees on", case["simd_agree"], "min margin", min(case["scalar_margins"]), "simd spread", case["simd_spread"],
+                  "simd teacher-forced disagrees at", case["simd_tf_disagree"], flush=True)
             out["cases"].append(case)
     (Path(__file__).parent / "decode.json").write_text(json.dumps(out, indent=1) + "\n")
 

@@ -7,6 +7,7 @@
   main.c:291), and a max-abs bound relative to max|logit| (SPREAD below says why it is not 1e-3).
 - The stop rules, callbacks, perf counters and run-to-run determinism of engine.c:322-362, 549-602.
 """
+import dataclasses
 import hashlib
 import os
 
@@ -82,6 +83,67 @@ def test_greedy_tokens_match_reference(golden_cases, oracle, i):
     m.close()
 
 
+# The attention each golden configuration's decode step runs (l3m_attention_mode): stories15M's hd 48 takes
+# the VALU form over the LDS window; stories42M's window at ctx 512 does not fit in LDS, so it reads the
+# cache; stories110M and SmolLM2 (hd 64) take the matrix cores.
+GOLDEN_ATTENTION = {"stories15M": 1, "stories42M": 0, "stories110M": 2, "smollm2": 2}
+
+
+@pytest.mark.parametrize("prefill", ["0", "1"])
+@pytest.mark.parametrize("i", range(5))
+def test_teacher_forced_golden_steps(golden_cases, oracle, monkeypatch, i, prefill):
+    """Every one of the 64 golden steps, teacher-forced: the GPU is fed the reference scalar engine's own
+    tokens up to step k and must predict its token k. At every step its logits meet the engine bar
+    against the oracle's (bit-exact with the scalar engine) fed the same tokens. The one exception is a
+    step whose scalar top-2 margin is within the reference's own SIMD-vs-scalar spread on this model
+    (simd_spread: its avx512 table fed the same tokens differs from its scalar table by that much, and
+    picks the second token at some of those steps itself, simd_tf_disagree); there the GPU's token must be
+    the scalar engine's first or second. With prefill 1 the prompt and the forced tokens before the last
+    position run through the batched prefill (the SmolLM2 prompts are 64 tokens; the others grow past
+    8 positions after a few steps)."""
+    c, path = golden_cases[i]
+    if "simd_spread" not in c:
+        pytest.fail("tests/golden/decode.json predates the teacher-forced fields: rerun tests/golden/make_golden.py")
+    monkeypatch.setenv("L3M_PREFILL", prefill)
+    print(f"case {c['config']} {c['dtype']} prefill={prefill}", flush=True)
+    m, om = A.Model(path), oracle.load(path)
+    assert m.attention_mode == GOLDEN_ATTENTION[c["config"]], m.attention_mode
+    prompt, ref, tie = c["prompt"], c["scalar_tokens"], c["simd_spread"]
+    # the logits bar at every step: the engine bar, or the reference's own SIMD spread with half again as
+    # much, whichever is looser (bf16 activations round too: its avx512 table is 2.4e-3 from its scalar
+    # table on stories15M)
+    bar = max(SPREAD[c["dtype"]], 1.5 * tie)
+    got, bad, worst, prefilled = [], [], (0.0, 0.0), 0
+    for pos in range(len(prompt) - 1):
+        om.forward(prompt[pos], pos, logits=False)
+    for k in range(len(ref)):
+        seq = prompt + ref[:k]
+        out = m.generate(seq, 1)
+        assert len(out) == 1
+        got.append(out[0])
+        prefilled += m.prefilled > 0
+        lg, lo = m.logits_at(len(seq) - 1), om.forward(seq[-1], len(seq) - 1)
+        err, d = float(np.abs(lg - lo).max() / np.abs(lo).max()), kl(lo, lg)
+        worst = (max(worst[0], err), max(worst[1], d))
+        assert int(np.argmax(lo)) == ref[k]
+        top = c["scalar_top2"][k]
+        if not (out[0] == top[0] or (c["scalar_margins"][k] < tie and out[0] == top[1])) or err > bar or d >= 0.01:
+            bad.append(k)
+    m.close()
+    exact = sum(g == t for g, t in zip(got, ref))
+    msg = (f"{c['config']}-{c['dtype']} prefill={prefill}: {exact} of {len(ref)} steps equal the reference's token "
+           f"(second at {[k for k in range(len(ref)) if got[k] != ref[k]]}; the reference's own avx512 table at "
+           f"{c['simd_tf_disagree']}); {sum(mg < tie for mg in c['scalar_margins'])} steps within its spread {tie}; "
+           f"worst logits max-abs / max|logit| {worst[0]:.2e} (bar {bar:.2e}), KL {worst[1]:.2e}; failing steps {bad}; attention mode "
+           f"{GOLDEN_ATTENTION[c['config']]}; prefilled calls {prefilled}")
+    print(msg, flush=True)
+    assert not bad, msg
+    if prefill == "0":
+        assert prefilled == 0
+    elif c["config"] == "smollm2":
+        assert prefilled == len(ref)
+
+
 @pytest.mark.parametrize("i", [0, 2])
 def test_reference_mode_matches_reference_ref_path(golden_cases, i):
     c, path = golden_cases[i]
@@ -119,6 +181,100 @@ def test_small_model_every_position_matches_oracle(oracle, models, dtype):
     gref, oref = A.Model(path, reference=True), oracle.load(path, ref=True)
     assert gref.generate(ids, 40) == oref.generate(ids, 40)
     assert np.abs(gref.logits - oref.logits()).max() <= 1e-4 * np.abs(oref.logits()).max()
+
+
+def oracle_follow(om, ids, got, vocab):
+    """Teacher-forces the oracle along the prompt and the GPU's tokens: per generated step, (the oracle's
+    argmax, its second, its top-2 margin / max|logit|), and its logits at each step."""
+    seq, steps, logits = list(ids) + list(got), [], []
+    for pos in range(len(seq) - 1):
+        lg = om.forward(seq[pos], pos, logits=pos >= len(ids) - 1)
+        if lg is None:
+            continue
+        order = np.argsort(-lg.astype(np.float64), kind="stable")
+        lv = np.sort(lg.astype(np.float64))
+        steps.append((int(order[0]), int(order[1]), float((lv[-1] - lv[-2]) / np.abs(lv).max())))
+        logits.append(lg)
+    return steps, logits
+
+
+def assert_follows_oracle(got, steps, what):
+    bad = [k for k, (g, (a, b, mg)) in enumerate(zip(got, steps)) if g != a and not (mg < NEAR_TIE and g == b)]
+    exact = sum(g == a for g, (a, _, _) in zip(got, steps))
+    msg = f"{what}: {exact} of {len(got)} steps equal the oracle's argmax, failing steps {bad[:10]}"
+    print(msg, flush=True)
+    assert not bad, msg
+
+
+@pytest.mark.parametrize("cfg,ctx,n_new", [(A.CONFIGS["stories42M"], 1024, 600), (dataclasses.replace(SMALL, name="tiny2k", ctx=2048), 2048, 1500)],
+                         ids=["stories42M-ctx1024", "tiny-ctx2048"])
+def test_long_context_follows_oracle(models, oracle, cfg, ctx, n_new):
+    """Decoding far past the positions whose K/V window fits in LDS (attention reads the cache): every step
+    of a long greedy run, teacher-forcing the oracle along the GPU's own tokens, and the logits of the last
+    positions at the engine bar. stories42M runs at its configured ctx 1024 (engine.c:22, 435 cap the default
+    at 512)."""
+    path = models.get(cfg, cfg.dtype, seed=11, std=0.05 if cfg.dim < 256 else 0.02, norm_jitter=0.1 if cfg.dim < 256 else 0.0)
+    ids = A.prompt(11, cfg.vocab, 4)
+    m = A.Model(path, ctx=ctx)
+    assert m.ctx == ctx and m.attention_mode == 0
+    got = m.generate(ids, n_new)
+    assert len(got) == n_new
+    om = oracle.load(path, ctx=ctx)
+    steps, logits = oracle_follow(om, ids, got, cfg.vocab)
+    assert_follows_oracle(got, steps, f"{cfg.name} ctx {ctx}")
+    for pos in range(len(ids) - 1 + n_new - 60, len(ids) - 1 + n_new, 7):   # logits kept for the last 64 positions
+        lg, lo = m.logits_at(pos), logits[pos - (len(ids) - 1)]
+        assert int(np.argmax(lg)) == int(np.argmax(lo)) or steps[pos - (len(ids) - 1)][2] < NEAR_TIE
+        assert kl(lo, lg) < 0.01 and np.abs(lg - lo).max() <= SPREAD[cfg.dtype] * np.abs(lo).max(), pos
+    m.close()
+
+
+@pytest.mark.parametrize("body,head", [("q4_0", "q8_0"), ("mxfp4", "q8_0"), ("q8_0", "bf16")])
+def test_mixed_head_dtype(models, oracle, body, head):
+    """A head quantized differently from the body (the reference's test_mixed_head_dtype,
+    test_engine.py:187-191), on the persistent kernel: the oracle teacher-forced along the GPU's tokens."""
+    cfg = A.Config("mixed", dim=192, n_layers=2, n_heads=6, n_kv_heads=2, ffn_dim=512, vocab=512, ctx=128, dtype=body)
+    path = models.get(cfg, body, seed=12, std=0.06, norm_jitter=0.1, head_dtype=head)
+    ids = A.prompt(12, cfg.vocab, 5)
+    m = A.Model(path)
+    assert m.persistent
+    got = m.generate(ids, 40)
+    om = oracle.load(path)
+    steps, logits = oracle_follow(om, ids, got, cfg.vocab)
+    assert_follows_oracle(got, steps, f"{body} body, {head} head")
+    lo, lg = logits[-1], m.logits_at(len(ids) - 2 + len(got))
+    assert kl(lo, lg) < 0.01 and np.abs(lg - lo).max() <= SPREAD[body] * np.abs(lo).max()
+    m.close()
+
+
+def test_cold_matches_warm(models):
+    """--cold (engine.c:330-338): the same tokens as warm decoding (the reference's test_cold_matches_warm),
+    one forward pass per launch after an eviction, and the eviction left out of the per-token time."""
+    path = models.get(SMALL, "q8_0", seed=6, std=0.08, norm_jitter=0.2)
+    ids = A.prompt(6, SMALL.vocab, 4)
+    warm, cold = A.Model(path), A.Model(path, cold=True)
+    a, b = warm.generate(ids, 24), cold.generate(ids, 24)
+    assert a == b and len(a) == 24
+    np.testing.assert_array_equal(warm.logits, cold.logits)
+    cold.perf()
+    cold.generate(ids, 8)
+    p = cold.perf()
+    assert p["tokens"] == len(ids) + 8 and p["ns_token"] > 0
+    warm.close(); cold.close()
+
+
+def test_prefill_refuses_unsupported_shape_and_decodes(models, oracle):
+    """A model whose ffn is past what the prefill kernels take (4 * 1024) loads with prefill off and decodes
+    its long prompt token by token, matching the oracle."""
+    cfg = A.Config("wide_ffn", dim=128, n_layers=2, n_heads=4, n_kv_heads=4, ffn_dim=4128, vocab=512, ctx=64, dtype="q8_0")
+    path = models.get(cfg, "q8_0", seed=13, std=0.05, norm_jitter=0.1)
+    ids = A.prompt(13, cfg.vocab, 20)
+    m, om = A.Model(path), oracle.load(path)
+    got = m.generate(ids, 16)
+    assert m.prefilled == 0
+    steps, _ = oracle_follow(om, ids, got, cfg.vocab)
+    assert_follows_oracle(got, steps, "ffn 4128")
+    m.close()
 
 
 def test_runs_are_bitwise_identical_and_graph_matches_eager(models):

@@ -57,3 +57,26 @@ def test_gpt2_reference_path(models, oracle):
     gref, oref = A.Model(path, reference=True), oracle.load(path, ref=True)
     assert gref.generate(ids, 16) == oref.generate(ids, 16)
     assert np.abs(gref.logits - oref.logits()).max() <= 1e-4 * np.abs(oref.logits()).max()
+
+
+@pytest.mark.parametrize("dtype", ["q8_0", "bf16"])
+def test_gptneo_without_qkv_biases(models, oracle, dtype):
+    """GPT-Neo: an output bias but no q, k, v biases (the reference's test_attention_without_qkv_biases,
+    test_engine.py:194-201). The oracle is teacher-forced along the GPU's greedy tokens: each is its argmax
+    (its top two at a near-tie)."""
+    print(f"case gptneo {dtype}", flush=True)
+    path = models.get(CFG, dtype, seed=7, std=0.06, norm_jitter=0.1, arch="gptneo")
+    ids = A.prompt(7, CFG.vocab, 9)
+    m, om = A.Model(path), oracle.load(path)
+    got = m.generate(ids, 20)
+    seq = list(ids) + got
+    for pos in range(len(seq) - 1):
+        lg = om.forward(seq[pos], pos, logits=pos >= len(ids) - 1)
+        if lg is None:
+            continue
+        k = pos - (len(ids) - 1)
+        order = np.argsort(-lg.astype(np.float64), kind="stable")
+        assert got[k] == order[0] or (margin(lg) < 0.005 and got[k] == order[1]), (k, got[k], order[:2])
+        if k == 0:
+            lo, lgpu = lg, m.logits_at(pos)
+            assert kl(lo, lgpu) < 0.01 and np.abs(lgpu - lo).max() <= SPREAD[dtype] * np.abs(lo).max()

@@ -186,3 +186,26 @@ def test_table_attend_matches_reference(reference):
     f, u16 = C.POINTER(C.c_float), C.POINTER(C.c_uint16)
     table.attend(out.ctypes.data_as(f), q.ctypes.data_as(f), k.ctypes.data_as(u16), v.ctypes.data_as(u16), pos, hd, stride)
     assert np.abs(out - reference.attend("scalar", q, k, v, pos, hd, stride)).max() <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, Q8_0, Q4_0, MXFP4], ids=NAMES.get)
+@pytest.mark.parametrize("k", [288, 1376])
+def test_dequant_bit_exact(dev, oracle, dtype, k):
+    """The decode step's device dequantization (lt_elem4: the embedding lookup, engine.c:236) against the
+    reference's l3m_dequant_row restated (pack.c:55-62), bit for bit, including the values the quantizers
+    never make (q8 -128, subnormal mxfp4 scales) and zero rows."""
+    n = 40
+    w = rows(dtype, n, k, seed=k + 10 * dtype)
+    if dtype in (Q8_0, MXFP4):
+        w = extremes(dtype, w, k)
+    w_list = [w[i] if i < n - 3 else None for i in range(n)]
+    m = dev.matrix(dtype, w_list, k)
+    got = dev.dequant(m, 0, n)
+    w0 = w.copy()
+    w0[n - 3:] = 0
+    want = oracle.dequant(dtype, w0, k)
+    assert np.array_equal(got[:, :k].view(np.uint32), want.view(np.uint32))
+    assert not got[:, k:].any()
+    part = dev.dequant(m, 17, 5)                      # a row range inside and across tiles
+    assert np.array_equal(part[:, :k].view(np.uint32), want[17:22].view(np.uint32))
+    dev.free_all()

@@ -28,6 +28,18 @@ def kl(lr, lf):
     return float((pr * (lpr - lpf)).sum())
 
 
+def bf16(u):
+    return (np.asarray(u, np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def ulps(a, b):
+    """Distance in bf16 units in the last place (values of one sign; a sign change counts through zero)."""
+    def key(u):
+        u = np.asarray(u, np.int64)
+        return np.where(u & 0x8000, -(u & 0x7FFF), u)
+    return np.abs(key(a) - key(b))
+
+
 def close(a, b):
     return int(np.argmax(a)) == int(np.argmax(b)) and kl(b, a) < 0.01 and np.abs(a - b).max() <= 0.02 * np.abs(b).max()
 
@@ -52,9 +64,38 @@ def test_prefill_logits(models, oracle, monkeypatch, cfg, n_prompt):
     lo = om.logits()
     assert close(lf, lo), (kl(lo, lf), np.abs(lf - lo).max() / np.abs(lo).max())
     assert close(lf, ls)
-    # the continuation decodes over the prefilled cache: its greedy tokens follow the oracle's while the
-    # margins are clear (checked on the first 8 tokens)
+    # the K/V rows the prefill wrote, against the oracle's (the reference's token-by-token order) and the
+    # GPU's own token-by-token rows
+    hd, P = cfg.dim // cfg.n_heads, n_prompt - 1
+    worst = {}
+    for layer in range(cfg.n_layers):
+        for kvh in range(cfg.n_kv_heads):
+            kp, vp = fast.kv_rows(layer, kvh, 0, P, hd)
+            ks, vs = step.kv_rows(layer, kvh, 0, P, hd)
+            ko, vo = om.kv_rows(layer, kvh, 0, P, hd)
+            for name, got_, tok_, ora in (("k", kp, ks, ko), ("v", vp, vs, vo)):
+                g, t, o = bf16(got_), bf16(tok_), bf16(ora)
+                scale = np.abs(o).max()
+                assert np.abs(g - o).max() <= 0.02 * scale, (layer, kvh, name)
+                assert np.abs(g - t).max() <= 0.02 * scale, (layer, kvh, name)
+                if layer == 0:                        # before activation rounding can cascade: nearly exact
+                    assert np.abs(g - o).max() <= 0.005 * scale, (layer, kvh, name)
+                    assert np.mean(ulps(got_, ora) <= 1) >= 0.99, (layer, kvh, name)
+                worst[name] = max(worst.get(name, 0.0), float(np.abs(g - o).max() / scale))
+    print(f"prefill K/V vs oracle, worst max-abs / max|x|: {worst}", flush=True)
+    # the continuation decodes over the prefilled cache: at every one of its 8 steps the GPU's token is the
+    # oracle's argmax given the same prefix (its top two at a near-tie)
     got = fast.generate(ids, 8)
-    want = om.generate(ids, 8)
-    first = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), len(got))
-    assert first >= 4, (got, want)
+    assert fast.prefilled == P
+    om2 = oracle.load(path)
+    seq = list(ids) + got
+    for k in range(len(got)):
+        pos = len(ids) - 1 + k
+        if k == 0:
+            for p in range(pos):
+                om2.forward(seq[p], p, logits=False)
+        lg = om2.forward(seq[pos], pos).astype(np.float64)
+        order = np.argsort(-lg, kind="stable")
+        lv = np.sort(lg)
+        tie = (lv[-1] - lv[-2]) / np.abs(lv).max() < 0.005
+        assert got[k] == order[0] or (tie and got[k] == order[1]), (k, got, order[:2])
