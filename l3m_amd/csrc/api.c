@@ -20,6 +20,7 @@
 struct l3m_model {
     l3m_mapped   f;
     int          reference, dtype;
+    int          mx_wide;      // an mxfp4 body whose blocks all widen exactly: its step matrices are q8_0
     l3m_dmodel   dm;
     l3m_dlayer  *layers;
     void       **allocs;
@@ -167,6 +168,7 @@ static int upload_widened(l3m_model *m, l3m_dmat *out, int src_dtype, int rows, 
 }
 
 static int upload_step_mat(l3m_model *m, l3m_dmat *out, int src_dtype, int rows, int k, const void *const *src) {
+    if (m->mx_wide && src_dtype == L3M_MXFP4) return upload_widened(m, out, src_dtype, rows, k, src);
     int dt = m->reference ? src_dtype : l3m_step_a_dtype(src_dtype);
     if (dt == src_dtype) return upload_mat(m, out, src_dtype, rows, k, src);
     if (src_dtype != L3M_Q4_0 || dt != L3M_Q8_0) return -1;
@@ -295,6 +297,11 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     if (d->dim > 4096) return fail(m, "dim up to 4096 is supported by the GPU kernels");
     if (d->ctx > 8192) return fail(m, "ctx up to 8192 is supported by the GPU attention kernel");
     m->dtype = (int)l3m_map_blk(f, 0, "w_up")->dtype;
+    // An mxfp4 body whose every block widens exactly (d = 2^(e-128) an f16, or all codes zero) runs its
+    // step matrices as q8_0 blocks of the same values: the same integer dots and float operations as the
+    // e2m1 path, without the per-code decode in the matvec loop (L3M_WIDEN=0 keeps the mxfp4 blocks).
+    const char *wd_ = getenv("L3M_WIDEN");
+    m->mx_wide = !m->reference && m->dtype == L3M_MXFP4 && (!wd_ || strcmp(wd_, "0")) && mxfp4_body_widens(f, (int)h->n_layers);
 
     // weights: per layer the head groups (q/k/v rows and Wo columns) and the FFN chunks (gate/up rows
     // and Wdown columns) of the two step kernels, then the head
@@ -304,13 +311,13 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     d->n_groups = d->n_heads / nq;
     // FFN chunk: the most rows (a multiple of 32) whose gate/up rows and Wdown columns fit the weight
     // slots a workgroup holds in flight, so one pass of loads covers the chunk
-    int sdt = m->reference ? L3M_F32 : m->dtype, cap_a = 64 * l3m_step_slots(sdt, 0), cap_b = 64 * l3m_step_slots(sdt, 1);
+    int sdt = m->reference ? L3M_F32 : m->mx_wide ? L3M_Q8_0 : m->dtype, cap_a = 64 * l3m_step_slots(sdt, 0), cap_b = 64 * l3m_step_slots(sdt, 1);
     int nbd = (d->dim + 31) / 32, chunk = 32;
     for (int c = 256; c >= 32; c -= 32)
         if (2 * c / 16 * nbd <= cap_a && (d->dim + 15) / 16 * (c / 32) <= cap_b) { chunk = c; break; }
     while ((d->ffn + chunk - 1) / chunk > MAX_PARTS) chunk += 32;
     d->n_chunks = (d->ffn + chunk - 1) / chunk;
-    d->body_dtype = m->reference ? L3M_F32 : m->dtype;
+    d->body_dtype = sdt;
     if (d->n_groups > MAX_PARTS || d->n_chunks > MAX_PARTS) return fail(m, "too many head groups or FFN chunks for the GPU kernels");
     l3m_model_layout(d);
     m->layers = calloc((size_t)d->n_layers, sizeof *m->layers);
@@ -319,7 +326,7 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     const char *pe_ = getenv("L3M_PREFILL"), *pm_ = getenv("L3M_PREFILL_MIN");
     const int qb_ = d->dim % 32 == 0 && (d->n_heads * d->hd) % 32 == 0 && d->ffn % 32 == 0;
     if ((!pe_ || strcmp(pe_, "0")) && !m->reference && !gpt2 && qb_ && l3m_prefill_fits(d->dim, d->ffn, d->n_heads * d->hd, d->hd) &&
-        (m->dtype == L3M_Q8_0 || m->dtype == L3M_Q4_0 || (m->dtype == L3M_MXFP4 && mxfp4_body_widens(f, d->n_layers))))
+        (m->dtype == L3M_Q8_0 || m->dtype == L3M_Q4_0 || m->mx_wide || (m->dtype == L3M_MXFP4 && mxfp4_body_widens(f, d->n_layers))))
         m->pf = calloc((size_t)d->n_layers, sizeof *m->pf);
     m->prefill_min = pm_ ? atoi(pm_) : 8;
     l3m_dgroup *groups = calloc((size_t)d->n_groups, sizeof *groups);

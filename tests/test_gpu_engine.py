@@ -109,10 +109,11 @@ def test_teacher_forced_golden_steps(golden_cases, oracle, monkeypatch, i, prefi
     m, om = A.Model(path), oracle.load(path)
     assert m.attention_mode == GOLDEN_ATTENTION[c["config"]], m.attention_mode
     prompt, ref, tie = c["prompt"], c["scalar_tokens"], c["simd_spread"]
-    # the logits bar at every step: the engine bar, or the reference's own SIMD spread with half again as
-    # much, whichever is looser (bf16 activations round too: its avx512 table is 2.4e-3 from its scalar
-    # table on stories15M)
-    bar = max(SPREAD[c["dtype"]], 1.5 * tie)
+    # the logits bar at every step: the engine bar, or twice the reference's own SIMD spread, whichever is
+    # looser. The spread is the largest of 64 steps' max over the vocabulary of |avx512 - scalar|; the GPU
+    # adds in a third order, so its largest deviation from the scalar table is of the same kind and may be
+    # up to twice that (bf16 activations round too: the avx512 table is 2.4e-3 from scalar on stories15M)
+    bar = max(SPREAD[c["dtype"]], 2 * tie)
     got, bad, worst, prefilled = [], [], (0.0, 0.0), 0
     for pos in range(len(prompt) - 1):
         om.forward(prompt[pos], pos, logits=False)
