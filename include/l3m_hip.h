@@ -79,6 +79,13 @@ extern const l3m_kernels l3m_kernels_hip;          // name "hip"; joins TABLES /
 int                l3m_kernels_usable(const l3m_kernels *k);   // src/kernels.h:46, dispatch.c:23-26
 const l3m_kernels *l3m_kernels_pick(void);                     // src/kernels.h:45, dispatch.c:28-36: NULL without a GPU
 const char        *l3m_hip_last_error(void);                   // the table's sticky error (its functions return void)
+// No counterpart in the reference: l3m_kernels_hip.attend for callers that cannot allocate device memory
+// (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments
+// (host pointers), same kernel, same result; it stages q, the K and V rows and the output through one
+// fixed 4 MiB device array instead of buffers grown on demand, so it refuses (-1, the reason on stderr) a
+// call whose (pos * stride + head_dim) * 2 bytes of K, and of V, exceed 2 MiB less 1 KiB. Calls are
+// serialized by a lock (two overlapping on one GPU would race on the array). 0 on success.
+int l3m_hip_attend_noalloc(float *out, const float *q, const uint16_t *k, const uint16_t *v, int pos, int head_dim, int stride);
 
 // ============================================================== 3. device-level (pointers are device memory)
 

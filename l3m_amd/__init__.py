@@ -71,7 +71,7 @@ l3m_prefill_positions i p       | l3m_probe_stream i z i i i *d   | l3m_probe_ex
 l3m_probe_graph_node i i i *d
 l3m_k_dequant i M i i p p       | l3m_attention_mode i i i i i   | l3m_k_attend_decode i i p p p p i i i i i p
 l3m_dev_evict i p z p           | l3m_decode_attention i p       | l3m_kv_rows i p i i i i p p
-l3m_time_read d ** i z i
+l3m_time_read d ** i z i         | l3m_hip_attend_noalloc i p p p p i i i
 """
 _SIG = {}
 for _entry in _SIGNATURES.replace("\n", "|").split("|"):

@@ -9,6 +9,7 @@
 // Reductions are fixed-order (wavefront shuffles, then LDS), so results are run-to-run identical.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -2556,6 +2557,9 @@ __global__ void k_probe_empty() {}
 char g_err[512];
 int g_has_err;
 hipStream_t g_stream;
+// The device address of `scratch` (below) on each device the library set up, from hipGetSymbolAddress: the
+// array's name in host code is a host-side stand-in, not a device address.
+void *g_scratch_dev[16];
 int g_ready = -1;
 char g_name[128];
 unsigned g_lds_max = 65536;
@@ -2654,6 +2658,12 @@ template <int DT, int HDT> int decode_fits(int grid, unsigned lds) {
 
 }  // namespace
 
+// The only device memory l3m_hip_attend_noalloc uses: the staged q, K rows, V rows and the output of one
+// call (the staging the kernel table's attend allocates and grows on demand). One copy per GPU, held until
+// the process ends; every call on a GPU shares it and it keeps the last call's contents.
+constexpr size_t ATTEND_STATIC_BYTES = 4u << 20;
+static __device__ __align__(256) uint8_t scratch[ATTEND_STATIC_BYTES];
+
 // =============================================================================================== C ABI
 
 struct l3m_graphs {
@@ -2691,6 +2701,7 @@ int l3m_dev_init(void) {
         return fail_msg(msg);
     }
     CK(hipSetDevice(0));
+    CK(hipGetSymbolAddress(&g_scratch_dev[0], HIP_SYMBOL(scratch)));
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, 0) == hipSuccess && lds > 0) g_lds_max = (unsigned)lds;
     CK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
@@ -2797,6 +2808,42 @@ int l3m_dev_copy(void *dst, const void *src, size_t bytes, void *stream) {
     if (grid) hipLaunchKernelGGL(k_copy, dim3(grid), dim3(NT), 0, as_stream(stream), (u32x4 *)dst, (const u32x4 *)src, n16);
     CKL("k_copy");
     return 0;
+}
+
+// l3m_kernels_hip.attend without allocating: q, the K and V rows and the output staged through `scratch`
+// (its device address from l3m_dev_init), the same kernel, the same result. Calls are serialized by a
+// lock; without it, two calls overlapping on one GPU would race on the one array.
+static pthread_mutex_t g_scratch_lock = PTHREAD_MUTEX_INITIALIZER;
+static size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+int l3m_hip_attend_noalloc(float *out, const float *q, const uint16_t *k, const uint16_t *v, int pos, int head_dim, int stride) {
+    if (l3m_dev_init()) return -1;
+    if (pos < 0 || head_dim < 8 || head_dim % 8 || head_dim > NT || stride < head_dim || stride % 8)
+        return fail_msg("attend_noalloc: head_dim must be a multiple of 8 up to 256, stride a multiple of 8 of at least head_dim");
+    const size_t kv = ((size_t)pos * stride + head_dim) * 2, vec = up256((size_t)head_dim * 4);
+    if (2 * vec + 2 * up256(kv) > ATTEND_STATIC_BYTES) {
+        char msg[200];
+        snprintf(msg, sizeof msg, "attend_noalloc: (pos * stride + head_dim) * 2 = %zu bytes of K (and of V) exceed the %zu-byte staging array",
+                 kv, (ATTEND_STATIC_BYTES - 2 * vec) / 2);
+        return fail_msg(msg);
+    }
+    const size_t sm = 4 * ((size_t)head_dim + ((pos + 4) & ~3) + NT + 8);
+    if (sm > LDS_MAX) return fail_msg("attend_noalloc: pos too large for the kernel's LDS");
+    uint8_t *base = (uint8_t *)g_scratch_dev[0];
+    float *dq = (float *)base, *dout = (float *)(base + vec);
+    uint16_t *dk = (uint16_t *)(base + 2 * vec), *dv = (uint16_t *)(base + 2 * vec + up256(kv));
+    pthread_mutex_lock(&g_scratch_lock);
+    hipError_t e = hipMemcpyAsync(dq, q, (size_t)head_dim * 4, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dk, k, kv, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dv, v, kv, hipMemcpyHostToDevice, g_stream);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_attend, dim3(1), dim3(NT), sm, g_stream, dout, dq, dk, dv, pos, (const int *)nullptr, head_dim, stride, 1, (size_t)0);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(out, dout, (size_t)head_dim * 4, hipMemcpyDeviceToHost, g_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    pthread_mutex_unlock(&g_scratch_lock);
+    return e == hipSuccess ? 0 : fail("attend_noalloc", e);
 }
 
 int l3m_dev_evict(const void *buf, size_t bytes, void *stream) {
