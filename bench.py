@@ -340,6 +340,60 @@ def cold_rate(A, path, prompt, n_tokens):
         return {"value": round(1.0 / m.bench_decode(prompt, n_tokens), 1), "unit": "tok/s", "tokens": n_tokens}
 
 
+A_PHASES = ["weights issued", "wait", "prologue", "norm+prep", "qkv", "rope+kv", "attention", "prep", "wo", "write", "flag"]
+F_PHASES = ["weights issued", "wait", "prologue", "norm+prep", "gate/up", "rows", "silu+prep", "down", "write", "flag"]
+
+
+def phase_report(A, d, name, dtype, pos, layer):
+    """Per-phase durations of the decode step (the library built with L3M_PHASE_STAMPS): for layers
+    (layer, layer + 1) at position pos, each phase's median and largest duration over the attention groups
+    and the FFN chunks, the hand-overs between them, and the layer's span, in microseconds."""
+    import numpy as np
+    lib, cfg = A.lib(), A.CONFIGS[name]
+    path = A.write_model(Path(d) / f"{name}-{dtype}-phases.l3m", cfg, dtype=dtype, seed=1)
+    prompt = [0]
+    with A.Model(path) as m:
+        m.bench_decode(prompt, 64)
+        if lib.l3m_phase_stamps(0, pos, layer, None):
+            raise RuntimeError("phase stamps unavailable: run with the library built by `make -C l3m_amd/csrc phases`")
+        m.generate(prompt, min(pos + 8, cfg.ctx - 2))
+        lib.l3m_dev_sync()
+        out, clk = np.zeros((2, 192, 16), np.uint64), np.zeros((2, 192, 16), np.uint64)
+        lib.l3m_phase_stamps(1, pos, layer, out.ctypes.data)
+        lib.l3m_phase_stamps(2, pos, layer, clk.ctypes.data)
+    t = out.astype(np.float64) * 0.01                 # 100 MHz ticks -> us
+    groups = [g for g in range(64) if t[0, g, 1] > 0]
+    chunks = [c for c in range(64, 128) if t[0, c, 1] > 0]
+
+    def spans(rows, names, lay):
+        res = {}
+        for e in range(1, len(names)):
+            v = [t[lay, r, e] - t[lay, r, e - 1] for r in rows if t[lay, r, e] > 0 and t[lay, r, e - 1] > 0]
+            if v:
+                res[names[e]] = {"median": round(float(np.median(v)), 3), "max": round(float(np.max(v)), 3)}
+        return res
+
+    a_done = max(t[0, g, 10] for g in groups)
+    f_start = min(t[0, c, 1] for c in chunks)
+    f_done = max(t[0, c, 9] for c in chunks)
+    a_next = min(t[1, g, 1] for g in groups) if all(t[1, g, 1] > 0 for g in groups) else None
+    rep = {"config": name, "dtype": dtype, "pos": pos, "layer": layer, "attention_groups": len(groups), "ffn_chunks": len(chunks),
+           "attention": spans(groups, A_PHASES, 0), "ffn": spans(chunks, F_PHASES, 0),
+           "attention_block_us": round(float(np.median([t[0, g, 10] - t[0, g, 1] for g in groups])), 3),
+           "ffn_block_us": round(float(np.median([t[0, c, 9] - t[0, c, 1] for c in chunks])), 3),
+           "handover_attention_to_ffn_us": round(float(f_start - a_done), 3),
+           "handover_ffn_to_attention_us": round(float(a_next - f_done), 3) if a_next else None,
+           "layer_us": round(float(np.median([t[1, g, 1] - t[0, g, 1] for g in groups])), 3) if a_next else None}
+    # the shader clock over attention group 0's block: s_memtime ticks per microsecond of the 100 MHz clock
+    g0 = groups[0]
+    rep["shader_clock_mhz"] = round(float((clk[0, g0, 10].astype(np.float64) - clk[0, g0, 1]) / (t[0, g0, 10] - t[0, g0, 1])), 1)
+    heads = [h for h in range(128, 192) if t[1 if layer + 1 == cfg.n_layers - 1 else 0, h, 1] > 0]
+    if heads:
+        lay = 1 if layer + 1 == cfg.n_layers - 1 else 0
+        rep["head"] = {"wait_to_block_end_median": round(float(np.median([t[lay, h, 2] - t[lay, h, 1] for h in heads])), 3)}
+    return rep
+
+
 def probes(A):
     """The residency and exchange probes (the GPU analogues of bench/residency.c and bench/exchange.c)."""
     lib, out = A.lib(), {"stream": [], "exchange": [], "graph_node_us": None}
@@ -376,6 +430,8 @@ def main():
     ap.add_argument("--sample-temp", type=float, default=1.0, help="temperature of the sampled-decode side figure (0 to skip)")
     ap.add_argument("--cold", type=int, default=1, help="the --cold side figure (0 to skip)")
     ap.add_argument("--probes", action="store_true", help="run only the residency and exchange probes, one JSON line")
+    ap.add_argument("--phases", default="", help="only per-phase timing of CONFIG:DTYPE:POS:LAYER (e.g. stories110M:q4_0:64:5), "
+                                                "with l3m_amd/libl3m_hip_phases.so, one JSON line")
     ap.add_argument("--only-decode", action="store_true", help="the headline decode only (for profiling runs)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the plain copy kernel once over this many MiB (counter calibration under rocprofv3)")
@@ -385,7 +441,14 @@ def main():
               "(one GPU's throughput is the figure; multi-GPU sharding is described, not run)", file=sys.stderr)
         sys.exit(2)
 
+    if a.phases:
+        os.environ["L3M_HIP_LIB"] = str(ROOT / "l3m_amd" / "libl3m_hip_phases.so")
     import l3m_amd as A
+    if a.phases:
+        name, dt, pos, layer = a.phases.split(":")
+        with tempfile.TemporaryDirectory() as d:
+            print(json.dumps({"phases": phase_report(A, d, name, dt, int(pos), int(layer))}), flush=True)
+        return
     if a.probes:
         print(json.dumps({"probes": probes(A)}), flush=True)
         return

@@ -95,6 +95,7 @@ typedef struct {
 } l3m_dmat;
 
 int         l3m_dev_init(void);
+void        l3m_dev_shutdown(void);   // the library's stream and events destroyed; later calls fail cleanly
 const char *l3m_dev_error(void);
 void        l3m_dev_clear_error(void);
 const char *l3m_dev_name(void);
@@ -164,6 +165,13 @@ double l3m_weight_bytes(const l3m_model *m);                       // weight byt
 // 1 when decode runs as one persistent cooperative kernel per chunk of steps (L3M_PERSIST=0 at load
 // selects the one-graph-per-step path), 0 otherwise.
 int    l3m_decode_persistent(const l3m_model *m);
+// Per-phase timing of the persistent decode kernel, in the library built with L3M_PHASE_STAMPS
+// (libl3m_hip_phases.so; -1 in the product build): mode 0 arms the stamps for layers (layer, layer + 1) at
+// one position and clears them; mode 1 copies them out: out[2][3 * 64][16], per layer the 100 MHz clock at
+// each phase boundary of attention group g (row g), FFN chunk c (row 64 + c) and head workgroup h (row
+// 128 + h, on the last layer), 0 where unrecorded; mode 2 copies out the shader clock (s_memtime) at the
+// same points.
+int    l3m_phase_stamps(int mode, int pos, int layer, unsigned long long *out);
 // The logits the last generate call computed at position pos (the prediction for pos + 1), into out
 // [vocab]: positions within the last 64 that call ran; -1 otherwise. An inspection hook (the sampled and
 // greedy tokens are checked against the logits they came from).

@@ -7,6 +7,7 @@ seeded synthetic models of the benchmark configurations.
 
 There is no CPU fallback: if the library is missing this module raises, and without a GPU `Model` raises.
 """
+import atexit
 import ctypes as C
 import os
 from dataclasses import dataclass
@@ -56,7 +57,7 @@ l3m_hip_last_error s            | l3m_dev_init i                 | l3m_dev_error
 l3m_dev_clear_error v           | l3m_dev_name s                 | l3m_dev_alloc p z
 l3m_dev_free v p                | l3m_dev_upload i p p z         | l3m_dev_download i p p z
 l3m_dev_sync i                  | l3m_dev_stream p               | l3m_lt_qbytes i i
-l3m_dev_copy i p p z p
+l3m_dev_copy i p p z p          | l3m_dev_shutdown v
 l3m_lt_sbytes i i               | l3m_lt_quant_size z i i i      | l3m_lt_scale_size z i i i
 l3m_lt_pack_rows v i i i ** p p | l3m_lt_pack_ltiles v i i i p p p | l3m_act_bytes z i i
 l3m_k_prep i i p i p p          | l3m_k_gemv i M p i p p         | l3m_k_attend i p p p p i i i p
@@ -71,7 +72,7 @@ l3m_prefill_positions i p       | l3m_probe_stream i z i i i *d   | l3m_probe_ex
 l3m_probe_graph_node i i i *d
 l3m_k_dequant i M i i p p       | l3m_attention_mode i i i i i   | l3m_k_attend_decode i i p p p p i i i i i p
 l3m_dev_evict i p z p           | l3m_decode_attention i p       | l3m_kv_rows i p i i i i p p
-l3m_time_read d ** i z i         | l3m_hip_attend_noalloc i p p p p i i i
+l3m_time_read d ** i z i         | l3m_hip_attend_noalloc i p p p p i i i | l3m_phase_stamps i i i i p
 """
 _SIG = {}
 for _entry in _SIGNATURES.replace("\n", "|").split("|"):
@@ -95,6 +96,9 @@ def lib():
             fn = getattr(handle, name)
             fn.restype, fn.argtypes = res, args
         _lib = handle
+        # the library's stream and events go before the interpreter exits, while HIP (and a profiler
+        # wrapping it) is still up
+        atexit.register(handle.l3m_dev_shutdown)
     return _lib
 
 

@@ -545,8 +545,8 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     if (m->reference)
         snprintf(m->desc, sizeof m->desc, "%s: %s, %d layers, reference fp32 on 1 gpu (hip)", base, l3m_dtype_name(m->dtype), d->n_layers);
     else
-        snprintf(m->desc, sizeof m->desc, "%s: %s, %d layers, %.1f MiB on 1 gpu (hip)", base, l3m_dtype_name(m->dtype), d->n_layers,
-                 m->weight_bytes / MiB);
+        snprintf(m->desc, sizeof m->desc, "%s: %s, %d layers, %.1f MiB on 1 gpu (hip)%s", base, l3m_dtype_name(m->dtype), d->n_layers,
+                 m->weight_bytes / MiB, m->mx_wide ? ", blocks widened exactly to q8_0" : "");
     if (o.verbose)
         fprintf(stderr, "l3m: %s, ctx %d, %s; %d head groups, %d ffn chunks, head %d x %d tiles, lds %u/%u/%u, kv in lds %d; "
                 "persistent %d (grid %d, body on xcd %d, head %d x %d tiles, lds %u)\n", m->desc, d->ctx, l3m_dev_name(), d->n_groups,

@@ -26,9 +26,18 @@ __host__ __device__ constexpr int qbytes(int dt) { return dt == L3M_F32 ? 128 : 
 __host__ __device__ constexpr int sbytes(int dt) { return dt == L3M_Q8_0 || dt == L3M_Q4_0 ? 2 : dt == L3M_MXFP4 ? 1 : 0; }
 __host__ __device__ constexpr bool quantized(int dt) { return dt >= L3M_Q8_0; }
 __host__ __device__ inline int kpad(int k) { return (k + 31) & ~31; }
+// A prepared activation (l3m_vec_prepare's values, pack.c:101-123) in the form the matvec of a dtype reads:
+//   q8_0   per 32-block the 32 int8 values q
+//   q4_0   per 32-block 16 bytes of high nibbles h = q >> 4 and 16 of low nibbles l = q & 15, dword k of each
+//          pairing values 4k + i (nibble 2i) and 4k + i + 16 (nibble 2i + 1), as a q4_0 weight dword pairs its
+//          inputs (its byte j holds inputs j and j + 16)
+//   mxfp4  per 32-block 16 f16 pairs (q[j], q[j + 16]), as a code byte's two e2m1 values convert
+// then the nb block scales (f32) and the nb block sums (int32: the sum of q, for q4_0 the sum of l); bf16
+// and f32 activations are plain vectors.
+__host__ __device__ constexpr int act_qbytes(int dt) { return dt == L3M_MXFP4 ? 64 : 32; }
 __host__ __device__ inline size_t act_size(int dt, int k) {
     const int kp = kpad(k);
-    return quantized(dt) ? (size_t)kp + 8 * (size_t)(kp / 32) : dt == L3M_BF16 ? 2 * (size_t)kp : 4 * (size_t)kp;
+    return quantized(dt) ? (size_t)act_qbytes(dt) * (kp / 32) + 8 * (size_t)(kp / 32) : dt == L3M_BF16 ? 2 * (size_t)kp : 4 * (size_t)kp;
 }
 __host__ __device__ inline size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
 
@@ -107,6 +116,10 @@ __device__ __forceinline__ int dot4(uint32_t a, int b, int c) { return __builtin
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float fdot2h(f16x2 a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(a, __builtin_bit_cast(f16x2, b), c, false);
 }
 
 // Elements i..i+3 (i a multiple of 4) of row r of a lane-tile matrix, exactly dequantized (the
@@ -195,14 +208,44 @@ __device__ void stage_x(float *xs, Src src, int k, int kp, const float *nw, floa
     __syncthreads();
 }
 
+// The lane holding values 4m..4m+3 of a 32-block (m = lane & 7) writes its share of the block's prepared
+// form at blk (the block's bytes): P = its four int8 values packed, Pp = those of lane m + 4 (values
+// 4m + 16 ..), used by lanes m < 4 only. Returns the lane's part of the block sum.
+template <int DT>
+__device__ __forceinline__ int put_block(uint8_t *blk, int m, uint32_t P, uint32_t Pp, int q0, int q1, int q2, int q3) {
+    if constexpr (DT == L3M_Q4_0) {
+        if (m < 4) {
+            // byte i: nibble 0 this lane's value i, nibble 1 the partner's value i
+            ((uint32_t *)blk)[m] = ((P >> 4) & 0x0F0F0F0Fu) | (Pp & 0xF0F0F0F0u);
+            ((uint32_t *)blk)[4 + m] = (P & 0x0F0F0F0Fu) | ((Pp & 0x0F0F0F0Fu) << 4);
+        }
+        return (q0 & 15) + (q1 & 15) + (q2 & 15) + (q3 & 15);
+    } else if constexpr (DT == L3M_MXFP4) {
+        if (m < 4) {
+            uint32_t d[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const _Float16 lo = (_Float16)(float)(int8_t)(P >> (8 * i)), hi = (_Float16)(float)(int8_t)(Pp >> (8 * i));
+                d[i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | (uint32_t)__builtin_bit_cast(uint16_t, hi) << 16;
+            }
+            *(uint4 *)(blk + 16 * m) = make_uint4(d[0], d[1], d[2], d[3]);
+        }
+        return q0 + q1 + q2 + q3;
+    } else {
+        ((uint32_t *)blk)[m] = P;
+        return q0 + q1 + q2 + q3;
+    }
+}
+
 // Activation prep (pack.c:101-123): quantized -> per 32-block amax, inv = 127/amax, q = rint(x*inv),
-// scale = amax/127, sum = sum(q); bf16 -> nearest even; f32 -> as is. 8 lanes per block.
+// scale = amax/127, sum = sum(q); bf16 -> nearest even; f32 -> as is. 8 lanes per block; the quantized
+// values are stored in the form the dtype's matvec reads (act_size).
 template <int DT>
 __device__ void prep_act(uint8_t *act, const float *xs, int kp) {
     if constexpr (quantized(DT)) {
         const int nb = kp / 32, g = threadIdx.x >> 3, l = threadIdx.x & 7;
-        float *scale = (float *)(act + kp);
-        int *sum = (int *)(act + kp + 4 * nb);
+        float *scale = (float *)(act + act_qbytes(DT) * nb);
+        int *sum = (int *)(act + act_qbytes(DT) * nb + 4 * nb);
         for (int b = g; b < nb; b += NT / 8) {
             const float4 v = *(const float4 *)(xs + b * 32 + 4 * l);
             float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
@@ -211,8 +254,9 @@ __device__ void prep_act(uint8_t *act, const float *xs, int kp) {
             am = fmaxf(am, __shfl_xor(am, 4));
             const float inv = am > 0.f ? 127.0f / am : 0.f;
             const int q0 = (int)rintf(v.x * inv), q1 = (int)rintf(v.y * inv), q2 = (int)rintf(v.z * inv), q3 = (int)rintf(v.w * inv);
-            *(uint32_t *)(act + b * 32 + 4 * l) = (uint32_t)(q0 & 255) | (uint32_t)(q1 & 255) << 8 | (uint32_t)(q2 & 255) << 16 | (uint32_t)(q3 & 255) << 24;
-            int s = q0 + q1 + q2 + q3;
+            const uint32_t P = (uint32_t)(q0 & 255) | (uint32_t)(q1 & 255) << 8 | (uint32_t)(q2 & 255) << 16 | (uint32_t)(q3 & 255) << 24;
+            const uint32_t Pp = (uint32_t)__shfl_xor((int)P, 4);
+            int s = put_block<DT>(act + b * act_qbytes(DT), l, P, Pp, q0, q1, q2, q3);
             s += __shfl_xor(s, 1);
             s += __shfl_xor(s, 2);
             s += __shfl_xor(s, 4);
@@ -235,29 +279,48 @@ __device__ void prep_act(uint8_t *act, const float *xs, int kp) {
 template <int DT>
 __device__ __forceinline__ float block_fma(float acc, const uint4 *w, uint32_t sc, const uint8_t *act, int kp, int b) {
     if constexpr (quantized(DT)) {
-        const int4 *xv = (const int4 *)(act + b * 32);
-        const int4 x0 = xv[0], x1 = xv[1];
-        const float xs = ((const float *)(act + kp))[b];
-        int dot = 0;
+        const int nb = kp >> 5;
+        const float xs = ((const float *)(act + act_qbytes(DT) * nb))[b];
         if constexpr (DT == L3M_Q8_0) {
+            const int4 *xv = (const int4 *)(act + b * 32);
+            const int4 x0 = xv[0], x1 = xv[1];
+            int dot = 0;
             dot = dot4(w[0].x, x0.x, dot); dot = dot4(w[0].y, x0.y, dot);
             dot = dot4(w[0].z, x0.z, dot); dot = dot4(w[0].w, x0.w, dot);
             dot = dot4(w[1].x, x1.x, dot); dot = dot4(w[1].y, x1.y, dot);
             dot = dot4(w[1].z, x1.z, dot); dot = dot4(w[1].w, x1.w, dot);
             return fmaf(xs * f16_f32(sc), (float)dot, acc);
+        } else if constexpr (DT == L3M_Q4_0) {
+            // sum (n - 8) q over the block with q = 16 h + l: 16 * sum (n - 8) h (signed 4-bit dots, the
+            // codes' top bits flipped make n - 8) + sum n l (unsigned 4-bit dots) - 8 * sum l
+            const uint4 *xv = (const uint4 *)(act + b * 32);
+            const uint4 h = xv[0], l = xv[1];
+            const int lsum = ((const int *)(act + 32 * nb + 4 * nb))[b];
+            int dh = 0, dl = 0;
+            dh = __builtin_amdgcn_sdot8((int)(w[0].x ^ 0x88888888u), (int)h.x, dh, false);
+            dh = __builtin_amdgcn_sdot8((int)(w[0].y ^ 0x88888888u), (int)h.y, dh, false);
+            dh = __builtin_amdgcn_sdot8((int)(w[0].z ^ 0x88888888u), (int)h.z, dh, false);
+            dh = __builtin_amdgcn_sdot8((int)(w[0].w ^ 0x88888888u), (int)h.w, dh, false);
+            dl = (int)__builtin_amdgcn_udot8(w[0].x, l.x, (unsigned)dl, false);
+            dl = (int)__builtin_amdgcn_udot8(w[0].y, l.y, (unsigned)dl, false);
+            dl = (int)__builtin_amdgcn_udot8(w[0].z, l.z, (unsigned)dl, false);
+            dl = (int)__builtin_amdgcn_udot8(w[0].w, l.w, (unsigned)dl, false);
+            return fmaf(xs * f16_f32(sc), (float)(16 * dh + dl - 8 * lsum), acc);
         } else {
-            const int xsum = ((const int *)(act + kp + 4 * (kp / 32)))[b];
+            // each code byte's two e2m1 values, doubled, as f16 (exact), dotted with the (q[j], q[j + 16])
+            // pairs in f32: every partial sum is an integer below 2^24, so the dot is exact
+            const uint4 *xv = (const uint4 *)(act + b * 64);
+            float dot = 0.f;
             const uint32_t v[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
-            const int lo[4] = {x0.x, x0.y, x0.z, x0.w}, hi[4] = {x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                uint32_t a = v[j] & 0x0F0F0F0Fu, c = (v[j] >> 4) & 0x0F0F0F0Fu;
-                if constexpr (DT == L3M_MXFP4) { a = e2m1x2_plus16(a); c = e2m1x2_plus16(c); }
-                dot = dot4(a, lo[j], dot);
-                dot = dot4(c, hi[j], dot);
+                const uint4 x = xv[j];
+                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 0), x.x, dot);
+                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 1), x.y, dot);
+                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 2), x.z, dot);
+                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 3), x.w, dot);
             }
-            if constexpr (DT == L3M_Q4_0) return fmaf(xs * f16_f32(sc), (float)(dot - 8 * xsum), acc);
-            else return fmaf(xs * e8m0_half(sc), (float)(dot - 16 * xsum), acc);
+            return fmaf(xs * e8m0_half(sc), dot, acc);
         }
     } else if constexpr (DT == L3M_BF16) {
         const uint4 *xv = (const uint4 *)(act + b * 64);
@@ -742,15 +805,23 @@ __device__ void block_argmax(float &v, int &i, float *sv, int *si) {
 template <class F>
 __device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, int rows, F f) {
     const int nb = m.nb;
+    // Reads are unconditional (row and block clamped into range) and issued together; the sums then take
+    // only the values in range, in block order.
     if (nb <= 4) {
+        // each quarter holds at most one block: quarter q has block (q * nb) / 4 when that is below
+        // ((q + 1) * nb) / 4
         for (int base = 0; base < rows; base += NTE) {
-            const int i = base + tidx();
-            float s[4] = {0.f, 0.f, 0.f, 0.f};
-            if (i < rows) {
-                const float *p = res + (size_t)(i >> 4) * nb * 16 + (i & 15);
+            const int i = base + tidx(), ic = i < rows ? i : rows - 1;
+            const float *p = res + (size_t)(ic >> 4) * nb * 16 + (ic & 15);
+            float v[4];
 #pragma unroll
-                for (int q = 0; q < 4; q++)
-                    for (int b = q * nb >> 2; b < (q + 1) * nb >> 2; b++) s[q] += p[b * 16];
+            for (int b = 0; b < 4; b++) v[b] = p[(b < nb ? b : nb - 1) * 16];
+            float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int lo = q * nb >> 2, hi = (q + 1) * nb >> 2;
+                const float vq = lo == 0 ? v[0] : lo == 1 ? v[1] : lo == 2 ? v[2] : v[3];
+                if (i < rows && lo < hi) s[q] += vq;
             }
             const float y = (s[0] + s[1]) + (s[2] + s[3]);
             const float partner = dppf<QP_X1>(y);     // row i ^ 1 is the neighbouring lane
@@ -773,18 +844,55 @@ __device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, i
     }
 }
 
+// ------------------------------------------------------------------------------- phase stamps
+// Per-phase timing of the decode step, in a build of its own (L3M_PHASE_STAMPS: make -C l3m_amd/csrc
+// phases, l3m_amd/libl3m_hip_phases.so; bench.py --phases): thread 0 of each attention group (role g),
+// FFN chunk (64 + c) and head workgroup (128 + h) records the 100 MHz clock at each phase boundary of two
+// consecutive layers (layer, layer + 1) at one position, armed by l3m_phase_stamps. The product build
+// compiles every stamp away.
+#ifdef L3M_PHASE_STAMPS
+__device__ unsigned long long g_phase[2][3 * 64][16];
+__device__ unsigned long long g_phase_clk[2][3 * 64][16];   // the shader clock (s_memtime) at the same points
+__device__ int g_phase_at[2];
+__shared__ int s_phase_row;      // thread 0's: which of the two recorded layers this one is, or -1
+// At the top of a layer (before its wait): whether this (position, layer) is recorded. One global read per
+// layer, off the measured phases; the stamps then read only thread 0's LDS word.
+__device__ __forceinline__ void phase_arm(int pos, int layer) {
+    if (tidx() != 0) return;
+    const int d = layer - __hip_atomic_load(&g_phase_at[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_phase_row = pos == __hip_atomic_load(&g_phase_at[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) && (d == 0 || d == 1) ? d : -1;
+}
+__device__ __forceinline__ void phase(int role, int ev, int, int) {
+    if (tidx() != 0 || role >= 3 * 64) return;
+    const int d = s_phase_row;                        // the graph path never arms it: only 0 or 1 records
+    if (d == 0 || d == 1) {
+        g_phase[d][role][ev] = __builtin_amdgcn_s_memrealtime();
+        g_phase_clk[d][role][ev] = __builtin_amdgcn_s_memtime();
+    }
+}
+#else
+__device__ __forceinline__ void phase_arm(int, int) {}
+__device__ __forceinline__ void phase(int, int, int, int) {}
+#endif
+
 // ----------------------------------------------------------------------------------- prologue
 // The incoming residual x = base + parts[0] + ... + parts[n-1] (or, for layer 0, the embedding row of
 // tok), with thread f < dim/4 owning x[4f, 4f+4). The parts are split over G = NTE / (dim/4) thread
-// groups; pro_load only issues the loads (with the norm weights and RoPE angles the kernel needs),
+// groups; pro_load only issues the loads (the norm weights and RoPE angles come from pro_static),
 // pro_finish adds them: each group's sum goes through LDS and the owners add the groups in order.
 constexpr int FILL_PER = 4;
 struct Pro {
     float4 p[FILL_PER];
     float4 base;
     float4 emb;       // layer 0: the embedding row's owned elements
-    float4 nw;        // norm weights of the owned elements
-    float2 cs;        // RoPE (cos, sin) of angle index tid (tid < hd / 2)
+};
+// The inputs of a block that no other workgroup writes during the step: the owners' norm weights and, for
+// attention, the RoPE (cos, sin) of angle index tid (tid < hd / 2) at the step's position. The persistent
+// path loads them before it waits for the block's exchanged inputs, so their memory latency (the weight
+// stream keeps them out of L2) stays off the step's critical path.
+struct ProStatic {
+    float4 nw;
+    float2 cs;
 };
 struct ProGeom {
     int n4, groups, per, nparts;
@@ -816,25 +924,30 @@ __device__ __forceinline__ void split_tid(int tid, int n4, int &grp, int &f) {
 // Loads are unconditional (indices clamped into range) wherever possible: a load under a branch that
 // later merges makes the compiler wait for it there, before the weight stream is issued.
 // embed is passed by value: a pointer into the kernel's argument struct would move that struct to scratch.
+// Owners load their norm weights and, given rope_row, the angles (hd / 2 <= n4: the angles' threads are
+// owners too).
+__device__ __forceinline__ void pro_static(ProStatic &S, int n4, const float *nw, const float *rope_row, int hd) {
+    const int tid = tidx(), own = tid < n4 ? tid : n4 - 1;
+    if (wave_id() * 64 < n4) {
+        S.nw = ldg16f(nw, own);
+        if (rope_row) {
+            const int i = tid < (hd >> 1) ? tid : (hd >> 1) - 1;
+            const u32x2 c = gp<u32x2>(rope_row)[i];
+            S.cs = make_float2(__uint_as_float(c.x), __uint_as_float(c.y));
+        }
+    }
+}
 template <bool COH>
-__device__ __forceinline__ void pro_load(Pro &P, const float *base, const float *parts, const ProGeom &G, const float *nw,
-                                         l3m_dmat embed, bool use_embed, int tok, const float *rope_row, int hd) {
+__device__ __forceinline__ void pro_load(Pro &P, const float *base, const float *parts, const ProGeom &G,
+                                         l3m_dmat embed, bool use_embed, int tok) {
     const int tid = tidx(), nparts = G.nparts, dim = 4 * G.n4;
     int f, grp;
     split_tid(tid, G.n4, grp, f);
     const int j0 = grp * G.per, own = tid < G.n4 ? tid : G.n4 - 1, wave = wave_id();
     // Each wavefront issues only the loads its threads use (wave-uniform branches: a memory instruction
-    // costs address-unit time whether or not its lanes are needed). Owners (group 0) take the norm
-    // weights, the base and, at layer 0, the embedding row; grouped threads their parts.
-    if (wave * 64 < G.n4) {
-        P.nw = ldg16f(nw, own);
-        P.base = ld16f<COH>(base, f);
-        if (rope_row) {                               // hd / 2 <= n4: the angles' threads are owners too
-            const int i = tid < (hd >> 1) ? tid : (hd >> 1) - 1;
-            const u32x2 c = gp<u32x2>(rope_row)[i];
-            P.cs = make_float2(__uint_as_float(c.x), __uint_as_float(c.y));
-        }
-    }
+    // costs address-unit time whether or not its lanes are needed). Owners (group 0) take the base and,
+    // at layer 0, the embedding row; grouped threads their parts.
+    if (wave * 64 < G.n4) P.base = ld16f<COH>(base, f);
     if (wave * 64 < G.groups * G.n4) {
 #pragma unroll
         for (int j = 0; j < FILL_PER; j++) {
@@ -851,12 +964,12 @@ __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float 
 // RoPE angles to cs_lds when given. pbuf: NTE float4 of LDS. All threads call it.
 template <bool COH>
 __device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, const ProGeom &G, bool use_embed, float4 *pbuf, float *keep,
-                             float *cs_lds, int hd) {
+                             float *cs_lds, float2 cs, int hd) {
     const int tid = tidx(), nparts = G.nparts, dim = 4 * G.n4;
     int f, grp;
     split_tid(tid, G.n4, grp, f);
     const int j0 = grp * G.per;
-    if (cs_lds && tid < (hd >> 1)) ((float2 *)cs_lds)[tid] = P.cs;
+    if (cs_lds && tid < (hd >> 1)) ((float2 *)cs_lds)[tid] = cs;
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
     if (use_embed) {
         if (tid < G.n4) x = P.emb;
@@ -879,9 +992,13 @@ __device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, const P
             __syncthreads();
             if (tid < G.n4) {
                 x = pbuf[tid];
-                for (int g = 1; g < G.groups; g++) {
-                    const float4 p = pbuf[g * G.n4 + tid];
-                    x.x += p.x; x.y += p.y; x.z += p.z; x.w += p.w;
+                for (int g0 = 1; g0 < G.groups; g0 += 4) {   // 4 reads in flight, then their sums in order
+                    float4 p[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) p[u] = pbuf[(g0 + u < G.groups ? g0 + u : G.groups - 1) * G.n4 + tid];
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        if (g0 + u < G.groups) { x.x += p[u].x; x.y += p[u].y; x.z += p[u].z; x.w += p[u].w; }
                 }
             }
         }
@@ -937,13 +1054,17 @@ __device__ __forceinline__ void prep_body(float4 y, uint8_t *act, int kp) {
         am = lanes_max<8>(am);
         const float inv = am > 0.f ? 127.0f / am : 0.f;
         const int q0 = (int)rintf(y.x * inv), q1 = (int)rintf(y.y * inv), q2 = (int)rintf(y.z * inv), q3 = (int)rintf(y.w * inv);
-        const int s = lanes_sumi<8>(q0 + q1 + q2 + q3);
-        if (4 * f < kp) {
-            *(uint32_t *)(act + 4 * f) = (uint32_t)(q0 & 255) | (uint32_t)(q1 & 255) << 8 | (uint32_t)(q2 & 255) << 16 | (uint32_t)(q3 & 255) << 24;
-            if ((f & 7) == 0) {
-                ((float *)(act + kp))[f >> 3] = am / 127.0f;
-                ((int *)(act + kp + 4 * (kp / 32)))[f >> 3] = s;
-            }
+        const uint32_t P = (uint32_t)(q0 & 255) | (uint32_t)(q1 & 255) << 8 | (uint32_t)(q2 & 255) << 16 | (uint32_t)(q3 & 255) << 24;
+        // the partner lane m + 4 of the block's 8 (DPP row shift left by 4: lanes 0-3 and 8-11 of each row
+        // of 16 read lanes 4-7 and 12-15)
+        const uint32_t Pp = DT == L3M_Q8_0 ? 0u : (uint32_t)dppi<0x104>((int)P);
+        const int nb = kp >> 5;
+        int s = 0;
+        if (4 * f < kp) s = put_block<DT>(act + (f >> 3) * act_qbytes(DT), f & 7, P, Pp, q0, q1, q2, q3);
+        s = lanes_sumi<8>(s);
+        if (4 * f < kp && (f & 7) == 0) {
+            ((float *)(act + act_qbytes(DT) * nb))[f >> 3] = am / 127.0f;
+            ((int *)(act + act_qbytes(DT) * nb + 4 * nb))[f >> 3] = s;
         }
     } else if constexpr (DT == L3M_BF16) {
         if (4 * f < kp)
@@ -1032,13 +1153,26 @@ __host__ __device__ inline size_t work_bytes(size_t a, size_t b) {
 // consecutive rows' same 16 bytes on 16 different 4-bank groups, so reads down a column (the MFMA
 // operand layout) are free of bank conflicts.
 __host__ __device__ inline int kv_row(int hd) { return hd + 8; }
+// The matrix-core attention keeps V transposed in the window, V^T [nkv][hd][vt_row(ctx)]: a P.V operand (8
+// consecutive positions of one dimension) is then one 16-byte read. Rows hold every position a 32-position
+// step reads, plus 8 to spread consecutive rows over the banks.
+__host__ __device__ inline int vt_row(int ctx) { return ((ctx + 31) & ~31) + 8; }
+// Bytes of the LDS K/V window: K [nkv][ctx][kv_row(hd)], then V in the same layout or transposed (vt).
+__host__ __device__ inline size_t kv_window_bytes(int nkv, int ctx, int hd, bool vt) {
+    const size_t k = (size_t)nkv * ctx * kv_row(hd), v = vt ? (size_t)nkv * hd * vt_row(ctx) : k;
+    return align16(2 * (k + v));
+}
+// Whether attend_mfma takes the shape (hd a multiple of 32, the q parts beside the wavefront sums in vred,
+// the scores and p parts within the 16 KiB minimum of the work region).
+__host__ __device__ inline bool mfma_fits(int hd, int nq, int ctx) {
+    return hd % 32 == 0 && 6 * nq * hd <= 4 * NWE * hd && 10 * ((ctx + 31) & ~31) <= 16 * NTE;
+}
 // Which attention the decode step runs for a head group of nq query heads: 2 on the matrix cores
-// (attend_mfma: the K/V window in LDS, hd a multiple of 32, the q parts beside the wavefront sums in vred,
-// the scores and p parts within the 16 KiB minimum of the work region), 1 the VALU split softmax over the
-// LDS window, 0 the VALU split softmax reading K and V from the cache.
+// (attend_mfma, over the K/V window in LDS) when the shape fits it, 1 the VALU split softmax over the LDS
+// window, 0 the VALU split softmax reading K and V from the cache (the window does not fit in LDS).
 __host__ __device__ inline int att_mode(int kv_lds, int hd, int nq, int ctx) {
     if (!kv_lds) return 0;
-    return hd % 32 == 0 && 6 * nq * hd <= 4 * NWE * hd && 10 * ((ctx + 31) & ~31) <= 16 * NTE ? 2 : 1;
+    return mfma_fits(hd, nq, ctx) ? 2 : 1;
 }
 struct LdsA { size_t act, work, q, cur, cs, vred, att, act2, scr, kvb, total; };
 __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3m_dgroup &g, int kv_lds) {
@@ -1054,7 +1188,7 @@ __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3
     L.att = o;  o += align16(4 * (size_t)kpad(g.nq * hd));
     L.act2 = o; o += align16(act_size(dt, g.nq * hd));
     L.scr = o;  o += 4 * 64;
-    L.kvb = o;  o += kv_lds ? align16(4 * (size_t)g.nkv * ctx * kv_row(hd)) : 0;   // [K | V][nkv][ctx][kv_row] bf16
+    L.kvb = o;  o += kv_lds ? kv_window_bytes(g.nkv, ctx, hd, mfma_fits(hd, g.nq, ctx)) : 0;   // K, V (or V^T) bf16
     L.total = o;
     return L;
 }
@@ -1095,16 +1229,20 @@ __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg)
     return L;
 }
 
-// K and V rows 0..pos-1 of the group's kv heads, copied from the cache into LDS [K | V][nkv][ctx][hd] by
-// the memory unit (global_load_lds_dwordx4: 64 lanes x 16 bytes into 1 KiB of LDS, no registers).
-// Rows up to pos - 1 were written by earlier steps, so the copy can start at the top of the kernel.
+// K and V rows 0..pos-1 of the group's kv heads, copied from the cache into the LDS window (K [nkv][ctx]
+// [kv_row(hd)], then V the same or, vt, transposed). Rows up to pos - 1 were written by earlier steps, so
+// the copy can start at the top of the kernel. Row-major rows go by the memory unit (global_load_lds_dwordx4:
+// 64 lanes x 16 bytes into 1 KiB of LDS, no registers); V^T through registers, each lane taking one
+// position's 8 dimensions and storing them down 8 rows of V^T, with zeros at the positions past pos up to
+// the end of the 32-position step (P.V reads them with p = 0; zeros keep the products finite). Position
+// pos is the block's own (written with this step's rows).
 template <bool COH>
-__device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int kv0, int nkv, int pos) {
+__device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int kv0, int nkv, int pos, bool vt) {
     const int wave = wave_id(), lane = tidx() & 63, hd = M.hd, rs = kv_row(hd);
     const size_t cwin = (size_t)M.ctx * hd, lwin = (size_t)M.ctx * rs;      // per head: cache, LDS window
     // one row per instruction (the window's rows are padded apart, so a copy cannot span rows): hd / 8
     // lanes of 16 bytes each
-    for (int head = 0; head < 2 * nkv; head++) {
+    for (int head = 0; head < (vt ? nkv : 2 * nkv); head++) {
         const int which = head >= nkv ? 1 : 0, j = head - which * nkv;
         const uint16_t *src = (which ? M.vc : M.kc) + ((size_t)layer * M.n_kv + kv0 + j) * cwin;
         uint16_t *dst = kvb + (size_t)head * lwin;
@@ -1113,6 +1251,21 @@ __device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int
                 __builtin_amdgcn_global_load_lds((const GLOBAL void *)(src + (size_t)t * hd + 8 * lane),
                                                  (__attribute__((address_space(3))) void *)(dst + (size_t)t * rs), 16, 0,
                                                  COH ? 16 : 0);   // 16: sc1
+    }
+    if (!vt) return;
+    const int vr = vt_row(M.ctx), tend = (pos + 32) & ~31;   // the step of position pos ends at tend
+    for (int j = 0; j < nkv; j++) {
+        const uint16_t *src = M.vc + ((size_t)layer * M.n_kv + kv0 + j) * cwin;
+        uint16_t *dst = kvb + (size_t)nkv * lwin + (size_t)j * hd * vr;
+        for (int c = wave; c < (hd >> 3); c += NWE)
+            for (int t = lane; t < tend; t += 64) {
+                if (t == pos) continue;
+                uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                if (t < pos) v = ld16<COH>(src, (size_t)t * (hd >> 3) + c);   // uniform base, 16-byte index
+                uint16_t *d = dst + (size_t)(8 * c) * vr + t;
+                d[0] = (uint16_t)v.x; d[vr] = (uint16_t)(v.x >> 16); d[2 * vr] = (uint16_t)v.y; d[3 * vr] = (uint16_t)(v.y >> 16);
+                d[4 * vr] = (uint16_t)v.z; d[5 * vr] = (uint16_t)(v.z >> 16); d[6 * vr] = (uint16_t)v.w; d[7 * vr] = (uint16_t)(v.w >> 16);
+            }
     }
 }
 
@@ -1284,7 +1437,7 @@ __device__ __forceinline__ void split3(float x, __bf16 &h, __bf16 &m, __bf16 &l)
 // (one per bf16 part) keep the MFMA chains independent. Ends with a barrier.
 __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, const __bf16 *qp, const uint16_t *kvb, float *sc,
                             float *vred, float *att) {
-    const int hd = M.hd, rs = kv_row(hd), ctx = M.ctx, n = pos + 1;
+    const int hd = M.hd, rs = kv_row(hd), vr = vt_row(M.ctx), ctx = M.ctx, n = pos + 1;
     const int lane = tidx() & 63, wave = wave_id(), li = lane & 15, lg = lane >> 4;
     const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
     const size_t win = (size_t)ctx * rs;
@@ -1294,7 +1447,7 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
     for (int h = 0; h < G.nq; h++) {
         // (q0 + h) / hpk by an exact float reciprocal (both far below 2^20)
         const int kvl = (int)(((float)(G.q0 + h) + 0.5f) * ihpk) - G.kv0;
-        const uint16_t *kw = kvb + (size_t)kvl * win, *vw = kvb + (size_t)(G.nkv + kvl) * win;
+        const uint16_t *kw = kvb + (size_t)kvl * win, *vw = kvb + (size_t)G.nkv * win + (size_t)kvl * hd * vr;   // V^T
         float mx = -INFINITY;
         for (int T = wave; T < tiles; T += NWE) {
             const int row = T * 16 + li < n ? T * 16 + li : n - 1;
@@ -1336,7 +1489,8 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
         for (int dt = wave; dt < (hd >> 4); dt += NWE) {
             f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0;
             // two 32-position steps per round, every operand read before the first product; a second
-            // step past the end reads step k's operands again and is not multiplied
+            // step past the end reads step k's operands again and is not multiplied. B: V^T row 16 dt + li,
+            // positions t0..t0+7 (past pos the window holds zeros, p is zero there)
             for (int k = 0; k < steps; k += 2) {
                 bf16x8 a[2][3], b[2];
 #pragma unroll
@@ -1345,14 +1499,7 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
                     a[u][0] = *(const bf16x8 *)(pp + t0);
                     a[u][1] = *(const bf16x8 *)(pp + cap + t0);
                     a[u][2] = *(const bf16x8 *)(pp + 2 * cap + t0);
-                    uint32_t w[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int ta = t0 + 2 * e < n ? t0 + 2 * e : n - 1, tb = t0 + 2 * e + 1 < n ? t0 + 2 * e + 1 : n - 1;
-                        w[e] = (uint32_t)vw[(size_t)ta * rs + 16 * dt + li] | (uint32_t)vw[(size_t)tb * rs + 16 * dt + li] << 16;
-                    }
-                    const u32x4 wv = {w[0], w[1], w[2], w[3]};
-                    b[u] = __builtin_bit_cast(bf16x8, wv);
+                    b[u] = *(const bf16x8 *)(vw + (size_t)(16 * dt + li) * vr + t0);
                 }
                 // every operand in its own registers before the first product (otherwise the compiler
                 // reloads a part into a register an earlier product still reads, one LDS trip per product)
@@ -1387,9 +1534,17 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
 // the byte q - 8 and the same scale, so every integer dot and every float operation is the one q4_0 would
 // do, while the slot loop skips the nibble unpacking. The head stays q4_0.
 template <int DT> constexpr int a_dtype() { return DT == L3M_Q4_0 ? L3M_Q8_0 : DT; }
-template <int DT> struct AttnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_wo<DT>()> b; };
-template <int DT> struct FfnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_b<DT>()> b; };
-template <int DT> struct HeadW { Pref<DT, nslot_a<DT>() + nslot_b<DT>()> a; };
+template <int DT> struct AttnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_wo<DT>()> b; ProStatic st; };
+template <int DT> struct FfnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_b<DT>()> b; ProStatic st; };
+template <int DT> struct HeadW { Pref<DT, nslot_a<DT>() + nslot_b<DT>()> a; ProStatic st; };
+
+// A block's static prologue inputs (ProStatic), issued ahead of its weights.
+__device__ __forceinline__ void attn_static(ProStatic &st, const l3m_dmodel &M, const l3m_dlayer &Lw, int pos) {
+    pro_static(st, M.dim >> 2, Lw.attn_norm, M.rope + (size_t)pos * M.hd, M.hd);
+}
+__device__ __forceinline__ void ffn_static(ProStatic &st, const l3m_dmodel &M, const l3m_dlayer &Lw) {
+    pro_static(st, M.dim >> 2, Lw.ffn_norm, nullptr, 0);
+}
 
 template <int DT> __device__ __forceinline__ void attn_issue(AttnW<DT> &w, const l3m_dgroup &G) {
     pref_load<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, 0);
@@ -1409,7 +1564,7 @@ template <int DT>
 __device__ __forceinline__ void attn_kv_window(const l3m_dmodel &M, const l3m_dgroup &G, int layer, int pos, uint8_t *smem) {
     if (!M.kv_lds) return;
     const LdsA L = lds_of(G);
-    kv_window_dma<true>((uint16_t *)(smem + L.kvb), M, layer, G.kv0, G.nkv, pos);
+    kv_window_dma<true>((uint16_t *)(smem + L.kvb), M, layer, G.kv0, G.nkv, pos, mfma_fits(M.hd, G.nq, M.ctx));
 }
 
 // The attention block of head group gi (engine.c:236-258) at `layer`, position pos: x = xb + the FFN
@@ -1428,9 +1583,11 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
 
     Pro P;
     const ProGeom PG = pro_geom(M, 0);
-    pro_load<PRE>(P, M.xb, M.pd, PG, Lw.attn_norm, M.embed, layer == 0, tok, M.rope + (size_t)pos * hd, hd);
+    if constexpr (!PRE) attn_static(w.st, M, Lw, pos);
+    pro_load<PRE>(P, M.xb, M.pd, PG, M.embed, layer == 0, tok);
     if constexpr (!PRE) attn_issue<DT>(w, G);
-    float4 x = pro_finish<PRE>(P, M.pd, PG, layer == 0, (float4 *)work, G2 && layer == 0 ? nullptr : gi == 0 ? M.xa : nullptr, cs, hd);
+    float4 x = pro_finish<PRE>(P, M.pd, PG, layer == 0, (float4 *)work, G2 && layer == 0 ? nullptr : gi == 0 ? M.xa : nullptr, cs, w.st.cs, hd);
+    phase(gi, 2, pos, layer);
     if constexpr (G2) {
         if (layer == 0) {                             // the learned position row (engine.c:237), then kept
             if (tid < (dim >> 2)) x = add4(x, ((const float4 *)(M.pos_embed + (size_t)pos * dim))[tid]);
@@ -1440,19 +1597,22 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // K, V rows 0..pos-1 (no dependence on this step). Issued after the prologue is consumed: a copy of
     // data-dependent length ahead of it would make the compiler wait for every load in flight there.
     // The persistent path issues it before it waits for the block's inputs (attn_kv_window).
-    if (!PRE && M.kv_lds) kv_window_dma<false>(kvb, M, layer, G.kv0, G.nkv, pos);
-    if constexpr (G2) ln_prep<DT>(x, Lw.attn_norm, Lw.attn_norm_b, dim, kp, M.eps, act, red);
-    else norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
+    if (!PRE && M.kv_lds) kv_window_dma<false>(kvb, M, layer, G.kv0, G.nkv, pos, mfma_fits(hd, G.nq, M.ctx));
+    constexpr int AT = a_dtype<DT>();                // the activations take the form the step matrices read
+    if constexpr (G2) ln_prep<AT>(x, Lw.attn_norm, Lw.attn_norm_b, dim, kp, M.eps, act, red);
+    else norm_prep<AT>(x, w.st.nw, dim, kp, M.eps, act, red);
+    phase(gi, 3, pos, layer);
 
     mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, act, kp, work);
     __syncthreads();
+    phase(gi, 4, pos, layer);
     // q, k rows: RoPE on pairs (2i, 2i+1) of each head by the angle i (ops.c:29-40); k, v rows rounded
     // to bf16 as the cache holds them (engine.c:247-248), into cur, row pos of the LDS window and, for the
     // heads this group writes, the cache
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
     const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
     // the matrix-core attention (LDS window, hd a multiple of 32, q parts fit beside vred's 2 NWE sums)
-    const bool mfma_att = att_mode(M.kv_lds, hd, G.nq, M.ctx) == 2;
+    const bool mfma_att = M.kv_lds && mfma_fits(hd, G.nq, M.ctx);
     __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
     rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner, bool lead) {
         if constexpr (G2) y += G.bqkv[i];            // the GPT-2 variant's q, k, v biases; no RoPE
@@ -1469,35 +1629,50 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
                 const int r = i - nqd, kv = r < nkd ? 0 : 1, jj = r - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
                 const uint16_t hb = f32_bf16(y);
                 cur[kv * nkd + jj] = hb;
-                if (M.kv_lds) kvb[((size_t)(kv * G.nkv + kvl) * M.ctx + pos) * kv_row(hd) + (jj - kvl * hd)] = hb;
-                if (G.write_kv >> kvl & 1u)
-                    gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + (jj - kvl * hd)] = hb;
+                if (mfma_att && kv)                   // V^T
+                    kvb[(size_t)G.nkv * M.ctx * kv_row(hd) + (size_t)jj * vt_row(M.ctx) + pos] = hb;
+                else if (M.kv_lds)
+                    kvb[((size_t)(kv * G.nkv + kvl) * M.ctx + pos) * kv_row(hd) + (jj - kvl * hd)] = hb;
             }
         }
     });
+    // the window's copy (issued long before) is complete; this step's rows go to the cache after the
+    // attention, so their store acknowledgements stay off the path to it
     if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    phase(gi, 5, pos, layer);
     if (mfma_att) attend_mfma(M, G, pos, qp, kvb, work, vred, att);
     else if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
     else attend_group<false, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
+    phase(gi, 6, pos, layer);
+    // this step's k and v rows (bf16, engine.c:247-248) into the cache, for the kv heads this group writes;
+    // the flag after the block waits for them
+    for (int i = tid; i < 2 * nkd; i += NTE) {
+        const int kv = i < nkd ? 0 : 1, jj = i - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
+        if (G.write_kv >> kvl & 1u)
+            gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + (jj - kvl * hd)] = cur[i];
+    }
 
     // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
     const int kq = kpad(nqd);
-    prep_owned<DT>(4 * tid < nqd ? ((const float4 *)att)[tid] : make_float4(0.f, 0.f, 0.f, 0.f), act2, kq);
+    prep_owned<AT>(4 * tid < nqd ? ((const float4 *)att)[tid] : make_float4(0.f, 0.f, 0.f, 0.f), act2, kq);
+    phase(gi, 7, pos, layer);
     mv<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
     __syncthreads();
+    phase(gi, 8, pos, layer);
     float *po = M.po + (size_t)gi * dim;
     rows_sum4(G.wo, work, dim, [&](int i, float y, float, bool lead) {
         if constexpr (G2) y += gi == 0 ? Lw.bo[i] : 0.f;   // bo once, with group 0's partial
         if (lead) gw(po)[i] = y;
     });
+    phase(gi, 9, pos, layer);
 }
 
 // The FFN block of chunk ci (engine.c:259-275): x = xa + the attention partials, RMSNorm, prep, the
 // chunk's gate and up rows, SiLU(gate) * up, prep, its Wdown columns -> pd[ci]. Chunk 0 keeps x in xb.
 template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dchunk &C, int ci, FfnW<DT> &w,
-                                          uint8_t *smem) {
+                                          uint8_t *smem, int layer = 0, int pos = 0) {
     const int tid = tidx(), dim = M.dim, kp = kpad(dim);
     const LdsB L = lds_of(C);
     float *work = (float *)(smem + L.work), *gu = (float *)(smem + L.gu);
@@ -1506,18 +1681,24 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
 
     Pro P;
     const ProGeom PG = pro_geom(M, 1);
-    pro_load<PRE>(P, M.xa, M.po, PG, Lw.ffn_norm, M.embed, false, 0, nullptr, 0);     // x += proj (engine.c:259)
+    if constexpr (!PRE) ffn_static(w.st, M, Lw);
+    pro_load<PRE>(P, M.xa, M.po, PG, M.embed, false, 0);     // x += proj (engine.c:259)
     if constexpr (!PRE) ffn_issue<DT>(w, C);
-    const float4 x = pro_finish<PRE>(P, M.po, PG, false, (float4 *)work, ci == 0 ? M.xb : nullptr, nullptr, 0);
-    if constexpr (G2) ln_prep<DT>(x, Lw.ffn_norm, Lw.ffn_norm_b, dim, kp, M.eps, act, red);
-    else norm_prep<DT>(x, P.nw, dim, kp, M.eps, act, red);
+    const float4 x = pro_finish<PRE>(P, M.po, PG, false, (float4 *)work, ci == 0 ? M.xb : nullptr, nullptr, w.st.cs, 0);
+    phase(64 + ci, 2, pos, layer);
+    constexpr int AT = a_dtype<DT>();                // the activations take the form the step matrices read
+    if constexpr (G2) ln_prep<AT>(x, Lw.ffn_norm, Lw.ffn_norm_b, dim, kp, M.eps, act, red);
+    else norm_prep<AT>(x, w.st.nw, dim, kp, M.eps, act, red);
+    phase(64 + ci, 3, pos, layer);
     mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
     __syncthreads();
+    phase(64 + ci, 4, pos, layer);
     rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float, bool lead) {
         if constexpr (G2) y += i < C.nf ? C.bup[i] : 0.f;   // the up rows only, with b_up
         if (lead) gu[i] = y;
     });
     __syncthreads();
+    phase(64 + ci, 5, pos, layer);
     // h = up * silu(gate) (ops.c:49-51) for the owned 4 rows (gate tile t and up tile t interleave), prepared
     const int kf = kpad(C.nf);
     float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1531,14 +1712,17 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
         }
         hv = make_float4(hh[0], hh[1], hh[2], hh[3]);
     }
-    prep_owned<DT>(hv, act2, kf);
+    prep_owned<AT>(hv, act2, kf);
+    phase(64 + ci, 6, pos, layer);
     mv<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, act2, kf, work);
     __syncthreads();
+    phase(64 + ci, 7, pos, layer);
     float *pd = M.pd + (size_t)ci * dim;
     rows_sum4(C.down, work, dim, [&](int i, float y, float, bool lead) {
         if constexpr (G2) y += ci == 0 ? Lw.bdown[i] : 0.f;   // b_down once, with chunk 0's partial
         if (lead) gw(pd)[i] = y;
     });
+    phase(64 + ci, 8, pos, layer);
 }
 
 // Tiles [t0, t0 + tpw) of the head as a matrix of their own (the last slice may be short).
@@ -1563,23 +1747,23 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
     uint8_t *act = smem + L.act;
     Red red{scr, 0};
 
-    float4 x, nw;
+    float4 x;
     if constexpr (PRE) {
-        // the persistent path sums the final residual once per step (reduce_final) into xf
+        // the persistent path sums the final residual once per step (reduce_final) into xf; the norm
+        // weights came with the head's weights (head_issue)
         const int n4 = dim >> 2, own = tid < n4 ? tid : n4 - 1;
-        nw = ldg16f(M.norm, own);
         const float4 xv = ld16f<true>(M.xf, own);
         x = tid < n4 ? xv : make_float4(0.f, 0.f, 0.f, 0.f);
     } else {
         Pro P;
         const ProGeom PG = pro_geom(M, 0);
-        pro_load<false>(P, M.xb, M.pd, PG, M.norm, M.embed, false, 0, nullptr, 0);   // x += down (engine.c:275), last layer
+        pro_static(w.st, dim >> 2, M.norm, nullptr, 0);
+        pro_load<false>(P, M.xb, M.pd, PG, M.embed, false, 0);   // x += down (engine.c:275), last layer
         head_issue<DT>(w, V);
-        x = pro_finish<false>(P, M.pd, PG, false, (float4 *)work, nullptr, nullptr, 0);
-        nw = P.nw;
+        x = pro_finish<false>(P, M.pd, PG, false, (float4 *)work, nullptr, nullptr, w.st.cs, 0);
     }
     if constexpr (G2) ln_prep<DT>(x, M.norm, M.norm_b, dim, kp, M.eps, act, red);
-    else norm_prep<DT>(x, nw, dim, kp, M.eps, act, red);
+    else norm_prep<DT>(x, w.st.nw, dim, kp, M.eps, act, red);
     mv<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work);
     __syncthreads();
     // each row's logit from the lane that sums it: stored, and kept if it beats the lane's earlier rows
@@ -1726,7 +1910,7 @@ __host__ __device__ inline LdsAtt lds_att(int mode, int nq, int nkv, int hd, int
     L.cur = o;  o += align16(4 * (size_t)nkv * hd);
     L.vred = o; o += align16(vr > vq ? vr : vq);
     L.sc = o;   o += mode == 2 ? align16(10 * (size_t)((ctx + 31) & ~31)) : 0;
-    L.kvb = o;  o += mode ? align16(4 * (size_t)nkv * ctx * kv_row(hd)) : 0;
+    L.kvb = o;  o += mode ? kv_window_bytes(nkv, ctx, hd, mode == 2) : 0;
     L.total = o;
     return L;
 }
@@ -1749,7 +1933,7 @@ __global__ void __launch_bounds__(NTE) k_attend_decode(float *out, const float *
     l3m_dgroup G{};
     G.q0 = 0; G.nq = nq; G.kv0 = 0; G.nkv = nkv; G.att_wl = att_wl;
     const int nqd = nq * hd, nkd = nkv * hd;
-    if (MODE) kv_window_dma<false>(kvb, M, 0, 0, nkv, pos);
+    if (MODE) kv_window_dma<false>(kvb, M, 0, 0, nkv, pos, MODE == 2);
     for (int i = tidx(); i < nqd; i += NTE) {
         const float y = q[i];
         qh[i] = y;
@@ -1759,7 +1943,8 @@ __global__ void __launch_bounds__(NTE) k_attend_decode(float *out, const float *
         const int kv = i < nkd ? 0 : 1, jj = i - kv * nkd, kvl = jj / hd, d = jj - kvl * hd;
         const uint16_t hb = (kv ? vc : kc)[((size_t)kvl * ctx + pos) * hd + d];
         cur[i] = hb;
-        if (MODE) kvb[((size_t)(kv * nkv + kvl) * ctx + pos) * kv_row(hd) + d] = hb;
+        if (MODE == 2 && kv) kvb[(size_t)nkv * ctx * kv_row(hd) + (size_t)jj * vt_row(ctx) + pos] = hb;   // V^T
+        else if (MODE) kvb[((size_t)(kv * nkv + kvl) * ctx + pos) * kv_row(hd) + d] = hb;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -2075,6 +2260,9 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
         const l3m_dlayer Lw = fixed(layers, l);
         const l3m_dgroup G = fixed(Lw.groups, g);
         AttnW<DT> wt;
+        phase_arm(pos, l);
+        phase(g, 0, pos, l);
+        attn_static(wt.st, M, Lw, pos);
         attn_issue<DT>(wt, G);
         attn_kv_window<DT>(M, G, l, pos, smem);
         const unsigned epoch = (unsigned)(s * nl + l);
@@ -2090,8 +2278,10 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
             if (epoch > 0 && !wait_flags<1>(sync + SY_FFN, M.n_chunks, epoch, abort_flag, R.spin_limit, &ok_lds)) return false;
             if (l == 0) tok = __hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        phase(g, 1, pos, l);
         attn_block<DT, true>(M, Lw, G, l, pos, tok, g, wt, smem);
         set_flag<false>(sync + SY_ATTN + g, epoch + 1);
+        phase(g, 10, pos, l);
     }
     return true;
 }
@@ -2109,19 +2299,28 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
         const l3m_dlayer Lw = fixed(layers, l);
         const l3m_dchunk C = fixed(Lw.chunks, ci);
         FfnW<DT> wt;
+        const int pos = R.pos0 + s;
+        phase_arm(pos, l);
+        phase(64 + ci, 0, pos, l);
+        ffn_static(wt.st, M, Lw);
         ffn_issue<DT>(wt, C);
         const unsigned epoch = (unsigned)(s * nl + l);
         if (!wait_flags<1>(sync + SY_ATTN, M.n_groups, epoch + 1, sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
-        ffn_block<DT, true>(M, Lw, C, ci, wt, smem);
+        phase(64 + ci, 1, pos, l);
+        ffn_block<DT, true>(M, Lw, C, ci, wt, smem, l, pos);
         set_flag<false>(sync + SY_FFN + ci, epoch + 1);
+        phase(64 + ci, 9, pos, l);
     }
     const l3m_run R = fixed(per_iteration(Rp));
     if (R.pos0 + s >= R.head_from) {
         unsigned *sync = R.sync;
         if (!wait_flags<1>(sync + SY_FFN, fixed(Mp).n_chunks, (unsigned)((s + 1) * nl), sync + SY_ABORT, R.spin_limit, &ok_lds))
             return false;
+        phase_arm(R.pos0 + s, nl - 1);
+        phase(64 + ci, 10, R.pos0 + s, nl - 1);
         reduce_final(Mp, ci);
         set_flag<true>(sync + SY_XF + ci, (unsigned)s + 1);
+        phase(64 + ci, 11, R.pos0 + s, nl - 1);
     }
     return true;
 }
@@ -2238,14 +2437,22 @@ __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, 
     int idx = 0x7FFFFFFF;
     const l3m_dmat V = head_slice(M, has_tiles ? t0 : 0, R.head_tpw);
     HeadW<DT> wt;
-    if (has_tiles) head_issue<DT>(wt, V);
+    phase_arm(pos, M.n_layers - 1);
+    phase(128 + h, 0, pos, M.n_layers - 1);
+    if (has_tiles) {
+        pro_static(wt.st, M.dim >> 2, M.norm, nullptr, 0);
+        head_issue<DT>(wt, V);
+    }
     if (!wait_flags<4>(R.sync + SY_XF, M.n_chunks, (unsigned)s + 1, R.sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
+    phase(128 + h, 1, pos, M.n_layers - 1);
     const float temp = R.temp;
     float *keep = temp > 0 ? (float *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).lgv) : nullptr;
     if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx, keep);
+    phase(128 + h, 2, pos, M.n_layers - 1);
     if (tidx() == 0)
         __hip_atomic_store(gw((uint64_t *)(R.sync + SY_SLOTS) + h), argmax_key(v, idx, step_tag(s)), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+    phase(128 + h, 3, pos, M.n_layers - 1);
     if (temp > 0 && !sample_step(M, R, h, s, has_tiles ? V.rows : 0, t0 * 16, smem)) return false;
     return true;
 }
@@ -2674,9 +2881,11 @@ struct l3m_graphs {
 extern "C" {
 
 // Everything the library created on the device that no model owns (the stream, the decode timer's
-// events), destroyed at exit before the runtime is torn down (registered with atexit after the runtime's
-// own handlers, so it runs first). Calls after it fail cleanly.
-static void dev_shutdown(void) {
+// events), destroyed by the host before it exits (the Python package registers it with its interpreter's
+// atexit; a C host may call it last or leave it to process exit). Not an atexit handler of the library's
+// own: those run after a profiler's finalization, when HIP calls no longer may be made. Calls after it fail
+// cleanly.
+void l3m_dev_shutdown(void) {
     if (g_ready != 1) return;
     (void)hipStreamSynchronize(g_stream);
     for (int i = 0; i < 2; i++)
@@ -2709,12 +2918,13 @@ int l3m_dev_init(void) {
     CKL("first launch");
     CK(hipStreamSynchronize(g_stream));
     g_ready = 1;
-    atexit(dev_shutdown);
     return 0;
 }
 
 const char *l3m_dev_error(void) { return g_has_err ? g_err : NULL; }
-void l3m_dev_clear_error(void) { g_has_err = 0; g_err[0] = 0; }
+// Also HIP's own last error: a refused launch (a cooperative launch while another process on the GPU holds
+// the device's cooperative dispatch) would otherwise fail the next launch check of the fallback path.
+void l3m_dev_clear_error(void) { (void)hipGetLastError(); g_has_err = 0; g_err[0] = 0; }
 const char *l3m_dev_name(void) { return g_name; }
 unsigned l3m_dev_lds_max(void) { return l3m_dev_init() ? 65536u : g_lds_max; }
 void *l3m_dev_stream(void) { return (void *)g_stream; }
@@ -2867,11 +3077,30 @@ int l3m_k_dequant(const l3m_dmat *m, int row0, int n, float *out, void *stream) 
 
 int l3m_attention_mode(int kv_lds, int hd, int nq, int ctx) { return att_mode(kv_lds, hd, nq, ctx); }
 
+int l3m_phase_stamps(int mode, int pos, int layer, unsigned long long *out) {
+#ifdef L3M_PHASE_STAMPS
+    if (l3m_dev_init()) return -1;
+    if (mode == 0) {
+        static unsigned long long zero[2][3 * 64][16];
+        const int at[2] = {pos, layer};
+        CK(hipMemcpyToSymbol(HIP_SYMBOL(g_phase), zero, sizeof zero, 0, hipMemcpyHostToDevice));
+        CK(hipMemcpyToSymbol(HIP_SYMBOL(g_phase_at), at, sizeof at, 0, hipMemcpyHostToDevice));
+        return 0;
+    }
+    CK(hipMemcpyFromSymbol(out, HIP_SYMBOL(mode == 2 ? g_phase_clk : g_phase), sizeof(unsigned long long) * 2 * 3 * 64 * 16, 0,
+                           hipMemcpyDeviceToHost));
+    return 0;
+#else
+    (void)mode; (void)pos; (void)layer; (void)out;
+    return fail_msg("phase stamps: this library was built without L3M_PHASE_STAMPS (make -C l3m_amd/csrc phases)");
+#endif
+}
+
 int l3m_k_attend_decode(int mode, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int nq, int nkv, int hd, int ctx,
                         int pos, void *stream) {
     if (l3m_dev_init()) return -1;
     if (mode < 0 || mode > 2 || hd < 8 || hd % 8 || hd > 256 || nq < 1 || nkv < 1 || nq % nkv || pos < 0 || pos >= ctx ||
-        (mode == 2 && att_mode(1, hd, nq, ctx) != 2))
+        (mode == 2 && !mfma_fits(hd, nq, ctx)))
         return fail_msg("attend_decode: shape out of range for this mode");
     const size_t lds = lds_att(mode, nq, nkv, hd, ctx).total;
     if (lds > g_lds_max) return fail_msg("attend_decode: the K/V window does not fit in LDS");

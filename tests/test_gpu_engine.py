@@ -84,9 +84,9 @@ def test_greedy_tokens_match_reference(golden_cases, oracle, i):
 
 
 # The attention each golden configuration's decode step runs (l3m_attention_mode): stories15M's hd 48 takes
-# the VALU form over the LDS window; stories42M's window at ctx 512 does not fit in LDS, so it reads the
-# cache; stories110M and SmolLM2 (hd 64) take the matrix cores.
-GOLDEN_ATTENTION = {"stories15M": 1, "stories42M": 0, "stories110M": 2, "smollm2": 2}
+# the VALU form over the LDS window; stories42M (ctx 512), stories110M and SmolLM2 (hd 64) take the matrix
+# cores over the window (its V transposed). The cache-reading form has its own long-context test.
+GOLDEN_ATTENTION = {"stories15M": 1, "stories42M": 2, "stories110M": 2, "smollm2": 2}
 
 
 @pytest.mark.parametrize("prefill", ["0", "1"])
@@ -184,6 +184,25 @@ def test_small_model_every_position_matches_oracle(oracle, models, dtype):
     assert np.abs(gref.logits - oref.logits()).max() <= 1e-4 * np.abs(oref.logits()).max()
 
 
+def test_mxfp4_native_blocks(oracle, models, monkeypatch):
+    """An mxfp4 body run on its own e2m1 blocks (L3M_WIDEN=0; otherwise blocks that widen exactly run as
+    q8_0): its tokens and last logits vs the oracle, and the same tokens as the widened run."""
+    path = models.get(SMALL, "mxfp4", seed=3, std=0.08, norm_jitter=0.2)
+    ids = A.prompt(3, SMALL.vocab, 5)
+    wide = A.Model(path)
+    assert "widened" in wide.describe()
+    monkeypatch.setenv("L3M_WIDEN", "0")
+    gpu, om = A.Model(path), oracle.load(path)
+    assert "widened" not in gpu.describe()
+    want = om.generate(ids, 40)
+    got = gpu.generate(ids, 40)
+    assert got == want == wide.generate(ids, 40)
+    lo, lg = om.logits(), gpu.logits
+    assert kl(lo, lg) < 0.01 and np.abs(lg - lo).max() <= SPREAD["mxfp4"] * np.abs(lo).max()
+    gpu.close()
+    wide.close()
+
+
 def oracle_follow(om, ids, got, vocab):
     """Teacher-forces the oracle along the prompt and the GPU's tokens: per generated step, (the oracle's
     argmax, its second, its top-2 margin / max|logit|), and its logits at each step."""
@@ -230,7 +249,7 @@ def test_long_context_follows_oracle(models, oracle, cfg, ctx, n_new):
     m.close()
 
 
-@pytest.mark.parametrize("body,head", [("q4_0", "q8_0"), ("mxfp4", "q8_0"), ("q8_0", "bf16")])
+@pytest.mark.parametrize("body,head", [("q4_0", "q8_0"), ("mxfp4", "q8_0"), ("q8_0", "bf16"), ("q8_0", "mxfp4")])
 def test_mixed_head_dtype(models, oracle, body, head):
     """A head quantized differently from the body (the reference's test_mixed_head_dtype,
     test_engine.py:187-191), on the persistent kernel: the oracle teacher-forced along the GPU's tokens."""
