@@ -191,7 +191,7 @@ static const float *vec_or_zero(l3m_model *m, const l3m_mapped *f, int l, const 
 
 // A prefill matrix: q8_0 lane tiles (q4_0 widened as the step matrices are; mxfp4 widened exactly).
 static int upload_pf_mat(l3m_model *m, l3m_dmat *out, int src_dtype, int rows, int k, const void *const *src) {
-    if (src_dtype == L3M_MXFP4) return upload_widened(m, out, src_dtype, rows, k, src);
+    if (src_dtype == L3M_MXFP4 || src_dtype == L3M_Q4_0) return upload_widened(m, out, src_dtype, rows, k, src);
     return upload_step_mat(m, out, src_dtype, rows, k, src);
 }
 

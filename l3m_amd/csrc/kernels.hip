@@ -103,14 +103,6 @@ __device__ __forceinline__ float e8m0_half(uint32_t e) {
     const int x = (int)e - 128;
     return x >= -126 ? __uint_as_float((uint32_t)(x + 127) << 23) : __uint_as_float(1u << (x + 149));
 }
-// Four e2m1 codes (one per byte, 0..15) to their doubled magnitudes + 16, i.e. 4..28 (kernels.h:21).
-__device__ __forceinline__ uint32_t e2m1x2_plus16(uint32_t n) {
-    const uint32_t sel = n & 0x07070707u;
-    const uint32_t pos = __builtin_amdgcn_perm(0x1C181614u, 0x13121110u, sel);   // 16 17 18 19 20 22 24 28
-    const uint32_t neg = __builtin_amdgcn_perm(0x04080A0Cu, 0x0D0E0F10u, sel);   // 16 15 14 13 12 10  8  4
-    const uint32_t m = ((n >> 3) & 0x01010101u) * 0xFFu;
-    return (neg & m) | (pos & ~m);
-}
 __device__ __forceinline__ int dot4(uint32_t a, int b, int c) { return __builtin_amdgcn_sdot4((int)a, b, c, false); }
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -1533,7 +1525,12 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
 // for a body of dtype DT. A q4_0 body holds them as q8_0: the same blocks with each nibble q widened to
 // the byte q - 8 and the same scale, so every integer dot and every float operation is the one q4_0 would
 // do, while the slot loop skips the nibble unpacking. The head stays q4_0.
+#ifdef L3M_Q4_STEPS_NATIVE
+// Measurement build only (make -C l3m_amd/csrc q4native): q4_0 step matrices kept as q4_0 blocks.
+template <int DT> constexpr int a_dtype() { return DT; }
+#else
 template <int DT> constexpr int a_dtype() { return DT == L3M_Q4_0 ? L3M_Q8_0 : DT; }
+#endif
 template <int DT> struct AttnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_wo<DT>()> b; ProStatic st; };
 template <int DT> struct FfnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_b<DT>()> b; ProStatic st; };
 template <int DT> struct HeadW { Pref<DT, nslot_a<DT>() + nslot_b<DT>()> a; ProStatic st; };
