@@ -173,7 +173,7 @@ int    l3m_decode_persistent(const l3m_model *m);
 // same points.
 int    l3m_phase_stamps(int mode, int pos, int layer, unsigned long long *out);
 // The logits the last generate call computed at position pos (the prediction for pos + 1), into out
-// [vocab]: positions within the last 64 that call ran; -1 otherwise. An inspection hook (the sampled and
+// [vocab]: positions within the last 128 that call ran; -1 otherwise. An inspection hook (the sampled and
 // greedy tokens are checked against the logits they came from).
 int    l3m_logits_at(const l3m_model *m, int pos, float *out);
 // Prompt positions the last generate call ran as one batched prefill (0: token by token). Prompts of at

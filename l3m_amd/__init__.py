@@ -209,7 +209,7 @@ class Model:
         return self._lib.l3m_prefill_positions(self._handle())
 
     def logits_at(self, pos):
-        """The logits the last generate computed at position pos (within its last 64 positions)."""
+        """The logits the last generate computed at position pos (within its last 128 positions)."""
         out = np.empty(self.vocab, np.float32)
         if self._lib.l3m_logits_at(self._handle(), pos, out.ctypes.data_as(_f)) != 0:
             raise ValueError(f"no logits kept for position {pos}")

@@ -12,7 +12,7 @@
 
 #define MiB (1024.0 * 1024.0)
 #define DEFAULT_CTX 512        // engine.c:22
-#define NSLOTS 64              // logits slots = the most steps enqueued between two host reads
+#define NSLOTS 128             // logits slots = the most steps enqueued between two host reads
 #define HEAD_WGS 256           // workgroups of the head kernel
 #define MAX_PARTS 64           // partial residual vectors a step kernel adds (head groups, FFN chunks)
 #define EVICT_BYTES (512u << 20)   // --cold: read before each forward pass, twice the 256 MiB Infinity Cache
@@ -29,6 +29,7 @@ struct l3m_model {
     l3m_dlayer  *layers_dev;   // the layer descriptors in device memory (persistent kernel)
     l3m_dmodel  *dm_dev;       // dm in device memory
     l3m_run     *run_dev;      // the persistent kernel's launch parameters
+    l3m_run     *run_host;     // their pinned host copy (queued to run_dev without a wait)
     int          persist;      // decode with the persistent kernel (else one graph per step)
     int          grid, head_tpw, n_head, body_xcc;
     unsigned     lds_decode;
@@ -518,6 +519,7 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     d->part_idx = dalloc(m, (size_t)parts * 4);
     m->sync = dalloc(m, (size_t)L3M_SYNC_WORDS * 4);
     m->run_dev = dalloc(m, sizeof(l3m_run));
+    m->run_host = l3m_dev_host_alloc(sizeof(l3m_run));
     m->dm_dev = dalloc(m, sizeof(l3m_dmodel));
     m->layers_dev = dupload(m, m->layers, (size_t)d->n_layers * sizeof *m->layers);
     d->done = dalloc(m, 4);
@@ -530,7 +532,7 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     m->tok_host = calloc((size_t)d->ctx + 1, sizeof *m->tok_host);
     m->logits = calloc((size_t)d->vocab, sizeof *m->logits);
     if (!d->pos || !d->tokens || !d->xa || !d->xb || !d->po || !d->pd || !d->xf || !d->samp || !d->logits || !d->part_val || !d->part_idx || !d->done ||
-        !d->kc || !d->vc || !d->rope || !d->norm || !m->tok_host || !m->logits || !m->sync || !m->layers_dev || !m->run_dev ||
+        !d->kc || !d->vc || !d->rope || !d->norm || !m->tok_host || !m->logits || !m->sync || !m->layers_dev || !m->run_dev || !m->run_host ||
         !m->dm_dev || l3m_dev_upload(m->dm_dev, d, sizeof *d))
         return fail(m, "device allocation failed");
     m->cold = o.cold != 0;
@@ -559,6 +561,7 @@ void l3m_free(l3m_model *m) {
     if (!m) return;
     l3m_dev_sync();
     l3m_graphs_free(m->graphs);
+    l3m_dev_host_free(m->run_host);
     for (int i = 0; i < m->n_allocs; i++) l3m_dev_free(m->allocs[i]);
     free(m->allocs); free(m->layers); free(m->tok_host); free(m->logits); free(m->pf);
     if (m->f.map) l3m_map_close(&m->f);
@@ -568,12 +571,14 @@ void l3m_free(l3m_model *m) {
 // Positions first..last in one launch of the persistent kernel; -1 on a device error or a timed-out wait.
 static int decode_launch(l3m_model *m, int first, int last, int head_from) {
     const l3m_dmodel *d = &m->dm;
-    static const unsigned zero[L3M_SYNC_WORDS];
     unsigned abort_flag = 0;
-    if (l3m_dev_upload(m->sync, zero, sizeof zero)) return -1;
-    l3m_run r = {first, last - first + 1, head_from, m->head_tpw, m->n_head, m->body_xcc, m->sync, 100000000ull,   // waits end after 1 s
-                 m->temp, 0};
-    if (l3m_dev_upload(m->run_dev, &r, sizeof r)) return -1;
+    // the sync words zeroed and the launch parameters copied on the stream, behind the previous launch
+    // (whose results the host has read, so run_host is free), without a wait of their own
+    if (l3m_dev_zero_async(m->sync, (size_t)L3M_SYNC_WORDS * 4)) return -1;
+    const l3m_run r = {first, last - first + 1, head_from, m->head_tpw, m->n_head, m->body_xcc, m->sync, 100000000ull,   // waits end after 1 s
+                       m->temp, 0};
+    *m->run_host = r;
+    if (l3m_dev_upload_async(m->run_dev, m->run_host, sizeof r)) return -1;
     if (l3m_decode_launch(d->body_dtype, d->head.dtype, m->dm_dev, m->layers_dev, m->run_dev, m->grid, m->lds_decode, NULL)) return -1;
     if (l3m_dev_download(&abort_flag, m->sync + L3M_SYNC_ABORT, 4)) return -1;
     if (l3m_decode_timer(2, NULL, NULL)) return -1;

@@ -103,6 +103,10 @@ void        l3m_dev_clear_error(void);
 const char *l3m_dev_name(void);
 void       *l3m_dev_alloc(size_t bytes);        // zeroed; NULL on failure
 void        l3m_dev_free(void *p);
+int         l3m_dev_upload_async(void *dst, const void *src_pinned, size_t bytes);   // queued, not waited for
+int         l3m_dev_zero_async(void *dst, size_t bytes);
+void       *l3m_dev_host_alloc(size_t bytes);   // pinned host memory
+void        l3m_dev_host_free(void *p);
 int         l3m_dev_upload(void *dst, const void *src, size_t bytes);
 int         l3m_dev_download(void *dst, const void *src, size_t bytes);
 int         l3m_dev_sync(void);

@@ -2945,6 +2945,25 @@ int l3m_dev_upload(void *dst, const void *src, size_t bytes) {
     CK(hipStreamSynchronize(g_stream));
     return 0;
 }
+// Queued on the library's stream without waiting: a copy from pinned host memory (l3m_dev_host_alloc,
+// which must stay unchanged until the stream has run it) and a fill with zero bytes.
+int l3m_dev_upload_async(void *dst, const void *src_pinned, size_t bytes) {
+    if (l3m_dev_init()) return -1;
+    CK(hipMemcpyAsync(dst, src_pinned, bytes, hipMemcpyHostToDevice, g_stream));
+    return 0;
+}
+int l3m_dev_zero_async(void *dst, size_t bytes) {
+    if (l3m_dev_init()) return -1;
+    CK(hipMemsetAsync(dst, 0, bytes, g_stream));
+    return 0;
+}
+void *l3m_dev_host_alloc(size_t bytes) {
+    void *p = NULL;
+    if (l3m_dev_init()) return NULL;
+    if (hipHostMalloc(&p, bytes ? bytes : 16, hipHostMallocDefault) != hipSuccess) { fail_msg("hipHostMalloc failed"); return NULL; }
+    return p;
+}
+void l3m_dev_host_free(void *p) { if (p) (void)hipHostFree(p); }
 int l3m_dev_download(void *dst, const void *src, size_t bytes) {
     if (l3m_dev_init()) return -1;
     CK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
