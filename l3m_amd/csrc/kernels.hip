@@ -1154,10 +1154,10 @@ __host__ __device__ inline size_t kv_window_bytes(int nkv, int ctx, int hd, bool
     const size_t k = (size_t)nkv * ctx * kv_row(hd), v = vt ? (size_t)nkv * hd * vt_row(ctx) : k;
     return align16(2 * (k + v));
 }
-// Whether attend_mfma takes the shape (hd a multiple of 32, the q parts beside the wavefront sums in vred,
+// Whether attend_mfma takes the shape (hd a multiple of 16, the q parts beside the wavefront sums in vred,
 // the scores and p parts within the 16 KiB minimum of the work region).
 __host__ __device__ inline bool mfma_fits(int hd, int nq, int ctx) {
-    return hd % 32 == 0 && 6 * nq * hd <= 4 * NWE * hd && 10 * ((ctx + 31) & ~31) <= 16 * NTE;
+    return hd % 16 == 0 && 6 * nq * hd <= 4 * NWE * hd && 10 * ((ctx + 31) & ~31) <= 16 * NTE;
 }
 // Which attention the decode step runs for a head group of nq query heads: 2 on the matrix cores
 // (attend_mfma, over the K/V window in LDS) when the shape fits it, 1 the VALU split softmax over the LDS
@@ -1415,18 +1415,21 @@ __device__ __forceinline__ void split3(float x, __bf16 &h, __bf16 &m, __bf16 &l)
 }
 
 // Attention of the group's query heads over positions 0..pos (ops.c:58-73) on the matrix cores, for a
-// head dimension that is a multiple of 32, with every K, V row in the LDS window (row stride kv_row(hd),
-// row pos included: the block stores this step's rows there first). One head at a time, three passes
-// with a barrier after each:
-//  1. scores: wavefront w takes 16-position tiles w, w + NWE, ...: S = K_tile (16 x hd, from the window
-//     as it lies) times q (in every column of B), q split into three bf16 parts (qp, written with q) so
-//     the products are f32 exact; s_t = S / sqrt(hd) into sc, and each wavefront's maximum into smax;
+// head dimension that is a multiple of 16, with every K, V row in the LDS window (row stride kv_row(hd),
+// row pos included: the block stores this step's rows there first). q and p are split into three bf16
+// parts (split3), so each product with an exact bf16 operand is f32 exact; the three parts ride in rows
+// 0-2 of the A operand of one product, the other 13 rows zero, and their sums, which land in one lane,
+// are added (h + m) + l. One head at a time, three passes with a barrier after each:
+//  1. scores: wavefront w takes 16-position tiles w, w + NWE, ...: S = A (row j < 3 = q's part j) times
+//     K_tile^T (hd x 16, B taken from the window as it lies: lane l supplies row l % 16); lane t < 16 holds
+//     rows 0-3 of column t, so s_t = ((S[0][t] + S[1][t]) + S[2][t]) / sqrt(hd) in one lane, into sc, and
+//     each wavefront's maximum into smax;
 //  2. p_t = exp(s_t - m) over the head's maximum m, stored as three bf16 parts (zero past pos, up to a
 //     multiple of 32), and each wavefront's sum of p into lpart;
-//  3. o = P V: wavefront w takes dims [16w, 16w + 16): 32 positions per step, A = the p parts (every row
-//     the same), B = V rows 32 at a time; att = o / sum(lpart).
-// sc: 10 * ceil32(ctx) bytes of LDS; vred: 2 * NWE floats; qp: [3][nq * hd] bf16. Three accumulators
-// (one per bf16 part) keep the MFMA chains independent. Ends with a barrier.
+//  3. o = P V: wavefront w takes dims [16w, 16w + 16): 32 positions per step, A row j < 3 = p's part j,
+//     B = V^T rows, 32 positions at a time; lanes 0-15 hold rows 0-3 of their dim's column, and
+//     att = ((row 0 + row 1) + row 2) / sum(lpart).
+// sc: 10 * ceil32(ctx) bytes of LDS; vred: 2 * NWE floats; qp: [3][nq * hd] bf16. Ends with a barrier.
 __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, const __bf16 *qp, const uint16_t *kvb, float *sc,
                             float *vred, float *att) {
     const int hd = M.hd, rs = kv_row(hd), vr = vt_row(M.ctx), ctx = M.ctx, n = pos + 1;
@@ -1434,6 +1437,8 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
     const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
     const size_t win = (size_t)ctx * rs;
     const int tiles = (n + 15) >> 4, steps = (n + 31) >> 5, cap = (ctx + 31) & ~31, nqd = G.nq * hd;
+    const int part = li < 3 ? li : 0;                 // the q (p) part this lane supplies, when li < 3
+    const bf16x8 z = {};
     float *s_arr = sc, *smax = vred, *lpart = vred + NWE;
     __bf16 *pp = (__bf16 *)(sc + cap);                // [3][cap]
     for (int h = 0; h < G.nq; h++) {
@@ -1443,28 +1448,27 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
         float mx = -INFINITY;
         for (int T = wave; T < tiles; T += NWE) {
             const int row = T * 16 + li < n ? T * 16 + li : n - 1;
-            f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0;
+            f32x4 c = {0.f, 0.f, 0.f, 0.f};
             for (int kk = 0; kk < hd; kk += 32) {
-                const int qo = h * hd + kk + 8 * lg;
-                bf16x8 a = *(const bf16x8 *)(kw + (size_t)row * rs + kk + 8 * lg), b0 = *(const bf16x8 *)(qp + qo),
-                       b1 = *(const bf16x8 *)(qp + nqd + qo), b2 = *(const bf16x8 *)(qp + 2 * nqd + qo);
-                asm volatile("" : "+v"(a), "+v"(b0), "+v"(b1), "+v"(b2));   // all four read before the products
-                c0 = mfma_bf16(a, b0, c0);
-                c1 = mfma_bf16(a, b1, c1);
-                c2 = mfma_bf16(a, b2, c2);
+                bf16x8 a = *(const bf16x8 *)(qp + part * nqd + h * hd + kk + 8 * lg),
+                       b = *(const bf16x8 *)(kw + (size_t)row * rs + kk + 8 * lg);
+                asm volatile("" : "+v"(a), "+v"(b));   // both read before the product
+                // rows 3-15 of A are zero; so is the upper half of the last step when hd = 32 j + 16
+                // (what was read there, the row's padding or the next head's q, is never multiplied)
+                const bool live = kk + 8 * lg < hd;
+                a = live && li < 3 ? a : z;
+                b = live ? b : z;
+                c = mfma_bf16(a, b, c);
             }
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = T * 16 + 4 * lg + r;
-                const float sv = ((c0[r] + c1[r]) + c2[r]) * scale;
-                if (li == 0) s_arr[t] = t < n ? sv : -INFINITY;
-                mx = fmaxf(mx, t < n ? sv : -INFINITY);
-            }
+            // lanes 0-15: rows 0-2 (the parts) of column li, position T * 16 + li
+            const int t = T * 16 + li;
+            const float sv = ((c[0] + c[1]) + c[2]) * scale;
+            const bool mine = lg == 0 && t < n;
+            if (lg == 0) s_arr[t] = mine ? sv : -INFINITY;
+            mx = fmaxf(mx, mine ? sv : -INFINITY);
         }
-        if (wave < tiles) {                           // the four row groups' maxima (lanes 16 apart)
-            float lo, hi;
-            swap16(mx, lo, hi); mx = fmaxf(lo, hi);
-            swap32(mx, lo, hi); mx = fmaxf(lo, hi);
+        if (wave < tiles) {                           // lane 0: the maximum over lanes 0-15
+            mx = lanes_max<16>(mx);
         }
         if (lane == 0) smax[wave] = mx;
         __syncthreads();
@@ -1479,36 +1483,30 @@ __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, c
         if (lane == 0) lpart[wave] = lw;
         __syncthreads();
         for (int dt = wave; dt < (hd >> 4); dt += NWE) {
-            f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0;
+            f32x4 c = {0.f, 0.f, 0.f, 0.f};
             // two 32-position steps per round, every operand read before the first product; a second
-            // step past the end reads step k's operands again and is not multiplied. B: V^T row 16 dt + li,
-            // positions t0..t0+7 (past pos the window holds zeros, p is zero there)
+            // step past the end reads step k's operands again and is not multiplied. A: row li < 3 = p's
+            // part li at positions t0..t0+7 (zero rows past 3); B: V^T row 16 dt + li, the same positions
+            // (past pos the window holds zeros, p is zero there)
             for (int k = 0; k < steps; k += 2) {
-                bf16x8 a[2][3], b[2];
+                bf16x8 a[2], b[2];
 #pragma unroll
                 for (int u = 0; u < 2; u++) {
                     const int t0 = 32 * (k + u < steps ? k + u : k) + 8 * lg;
-                    a[u][0] = *(const bf16x8 *)(pp + t0);
-                    a[u][1] = *(const bf16x8 *)(pp + cap + t0);
-                    a[u][2] = *(const bf16x8 *)(pp + 2 * cap + t0);
+                    a[u] = *(const bf16x8 *)(pp + part * cap + t0);
                     b[u] = *(const bf16x8 *)(vw + (size_t)(16 * dt + li) * vr + t0);
                 }
-                // every operand in its own registers before the first product (otherwise the compiler
-                // reloads a part into a register an earlier product still reads, one LDS trip per product)
 #pragma unroll
-                for (int u = 0; u < 2; u++) asm volatile("" : "+v"(a[u][0]), "+v"(a[u][1]), "+v"(a[u][2]), "+v"(b[u]));
-                c0 = mfma_bf16(a[0][0], b[0], c0);
-                c1 = mfma_bf16(a[0][1], b[0], c1);
-                c2 = mfma_bf16(a[0][2], b[0], c2);
-                if (k + 1 < steps) {
-                    c0 = mfma_bf16(a[1][0], b[1], c0);
-                    c1 = mfma_bf16(a[1][1], b[1], c1);
-                    c2 = mfma_bf16(a[1][2], b[1], c2);
+                for (int u = 0; u < 2; u++) {
+                    asm volatile("" : "+v"(a[u]), "+v"(b[u]));
+                    a[u] = li < 3 ? a[u] : z;
                 }
+                c = mfma_bf16(a[0], b[0], c);
+                if (k + 1 < steps) c = mfma_bf16(a[1], b[1], c);
             }
             // the wavefronts' sums of p: lane k < NWE reads wavefront k's (lanes 16 and up repeat them)
             const float l = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(lanes_sum<16>(lpart[li]))));
-            if (lg == 0) att[h * hd + 16 * dt + li] = ((c0[0] + c1[0]) + c2[0]) / l;
+            if (lg == 0) att[h * hd + 16 * dt + li] = ((c[0] + c[1]) + c[2]) / l;
         }
         __syncthreads();
     }
@@ -1608,7 +1606,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // heads this group writes, the cache
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
     const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
-    // the matrix-core attention (LDS window, hd a multiple of 32, q parts fit beside vred's 2 NWE sums)
+    // the matrix-core attention (LDS window, hd a multiple of 16, q parts fit beside vred's 2 NWE sums)
     const bool mfma_att = M.kv_lds && mfma_fits(hd, G.nq, M.ctx);
     __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
     rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner, bool lead) {

@@ -3,7 +3,7 @@ three forms, against the oracle's l3m_attend (ops.c:42-73) per query head, withi
 reference's own bar against double precision (tests/test_kernels.c:145).
 
   mode 2  attend_mfma: scores and P.V on the matrix cores, q and p split into three bf16 parts
-  mode 1  attend_group over the K/V window in LDS (head dims that are not a multiple of 32)
+  mode 1  attend_group over the K/V window in LDS (head dims that are not a multiple of 16)
   mode 0  attend_group reading K and V from the cache (windows too long for LDS)
 
 Positions cover the 16-position tiles and 32-position steps of mode 2 and the split-softmax rounds of
@@ -32,7 +32,7 @@ def want(oracle, q, kc, vc, nq, nkv, hd, pos):
 
 # (mode, hd, nq, nkv, ctx): the window of modes 1 and 2 must fit in LDS beside the rest, so their ctx is
 # the largest that does for the shape; mode 0 takes the longest positions.
-CASES = [(2, 64, 1, 1, 512), (2, 64, 2, 1, 320), (1, 64, 1, 1, 512), (1, 48, 2, 2, 256), (1, 48, 2, 1, 512),
+CASES = [(2, 64, 1, 1, 512), (2, 64, 2, 1, 320), (2, 48, 1, 1, 512), (2, 48, 2, 2, 256), (2, 48, 2, 1, 512), (1, 64, 1, 1, 512), (1, 48, 2, 2, 256), (1, 48, 2, 1, 512),
          (0, 64, 1, 1, 1024), (0, 48, 2, 2, 1024), (0, 64, 3, 1, 1024), (0, 32, 1, 1, 1024)]
 
 
@@ -56,10 +56,12 @@ def test_decode_attention_matches_oracle(dev, oracle, case, qscale):
 
 def test_attention_modes_agree_with_decode_choice(dev):
     """The mode a decode step picks (l3m_attention_mode) for the benchmark shapes: matrix cores for hd 64
-    with the window in LDS, the VALU window form for hd 48, the cache form without a window."""
+    and 48 with the window in LDS, the VALU window form for a head dimension off the multiples of 16, the
+    cache form without a window."""
     import l3m_amd as A
     lib = A.lib()
     assert lib.l3m_attention_mode(1, 64, 1, 128) == 2
-    assert lib.l3m_attention_mode(1, 48, 2, 256) == 1
+    assert lib.l3m_attention_mode(1, 48, 2, 256) == 2
+    assert lib.l3m_attention_mode(1, 40, 2, 256) == 1
     assert lib.l3m_attention_mode(0, 64, 1, 1024) == 0
     assert lib.l3m_attention_mode(1, 64, 12, 128) == 1    # too many heads' q parts beside the sums

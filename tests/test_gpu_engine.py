@@ -83,10 +83,10 @@ def test_greedy_tokens_match_reference(golden_cases, oracle, i):
     m.close()
 
 
-# The attention each golden configuration's decode step runs (l3m_attention_mode): stories15M's hd 48 takes
-# the VALU form over the LDS window; stories42M (ctx 512), stories110M and SmolLM2 (hd 64) take the matrix
-# cores over the window (its V transposed). The cache-reading form has its own long-context test.
-GOLDEN_ATTENTION = {"stories15M": 1, "stories42M": 2, "stories110M": 2, "smollm2": 2}
+# The attention each golden configuration's decode step runs (l3m_attention_mode): stories15M (hd 48),
+# stories42M (ctx 512), stories110M and SmolLM2 (hd 64) take the matrix cores over the LDS window (its V
+# transposed). The cache-reading form has its own long-context test.
+GOLDEN_ATTENTION = {"stories15M": 2, "stories42M": 2, "stories110M": 2, "smollm2": 2}
 
 
 @pytest.mark.parametrize("prefill", ["0", "1"])
