@@ -193,16 +193,20 @@ def cpu_first_logits(path, prompt, ctx, runs=3):
 
 
 def gpu_first_logits(A, path, prompt, ctx, reps=5):
-    """Milliseconds to the first logits of the prompt on the GPU: batched prefill, and token by token
-    (L3M_PREFILL=0); median of reps."""
+    """Milliseconds to the first logits of the prompt on the GPU, median of reps after one call: batched
+    prefill replaying its captured graph (and the first call, which captures it), the same launches one by
+    one (L3M_PREFILL_GRAPH=0), and token by token (L3M_PREFILL=0)."""
     out = {}
-    for key, env in (("ms_prefill", None), ("ms_token_by_token", "0")):
-        if env is None:
-            os.environ.pop("L3M_PREFILL", None)
-        else:
-            os.environ["L3M_PREFILL"] = env
+    for key, env in (("ms_prefill", {}), ("ms_prefill_loose_launches", {"L3M_PREFILL_GRAPH": "0"}),
+                     ("ms_token_by_token", {"L3M_PREFILL": "0"})):
+        for k in ("L3M_PREFILL", "L3M_PREFILL_GRAPH"):
+            os.environ.pop(k, None)
+        os.environ.update(env)
         with A.Model(path, ctx=ctx) as m:
+            t0 = time.perf_counter()
             m.generate(prompt, 0)
+            A.lib().l3m_dev_sync()
+            first = (time.perf_counter() - t0) * 1e3
             times = []
             for _ in range(reps):
                 t0 = time.perf_counter()
@@ -210,9 +214,11 @@ def gpu_first_logits(A, path, prompt, ctx, reps=5):
                 A.lib().l3m_dev_sync()
                 times.append((time.perf_counter() - t0) * 1e3)
             out[key] = round(statistics.median(times), 3)
-            if env is None:
+            if not env:
+                out["ms_prefill_first_call"] = round(first, 3)
                 out["prefilled_positions"] = m.prefilled
-    os.environ.pop("L3M_PREFILL", None)
+    for k in ("L3M_PREFILL", "L3M_PREFILL_GRAPH"):
+        os.environ.pop(k, None)
     return out
 
 
@@ -347,7 +353,9 @@ F_PHASES = ["weights issued", "wait", "prologue", "norm+prep", "gate/up", "rows"
 def phase_report(A, d, name, dtype, pos, layer):
     """Per-phase durations of the decode step (the library built with L3M_PHASE_STAMPS): for layers
     (layer, layer + 1) at position pos, each phase's median and largest duration over the attention groups
-    and the FFN chunks, the hand-overs between them, and the layer's span, in microseconds."""
+    and the FFN chunks, the hand-overs between them, and the layer's span, in microseconds. For the last
+    layer the second layer is layer 0 of position pos + 1, and the report adds the step's tail through the
+    head (head_chain_us)."""
     import numpy as np
     lib, cfg = A.lib(), A.CONFIGS[name]
     path = A.write_model(Path(d) / f"{name}-{dtype}-phases.l3m", cfg, dtype=dtype, seed=1)
@@ -391,6 +399,22 @@ def phase_report(A, d, name, dtype, pos, layer):
     if heads:
         lay = 1 if layer + 1 == cfg.n_layers - 1 else 0
         rep["head"] = {"wait_to_block_end_median": round(float(np.median([t[lay, h, 2] - t[lay, h, 1] for h in heads])), 3)}
+    if layer == cfg.n_layers - 1 and heads and a_next:
+        # the step's tail: from the last FFN chunk's flag of the last layer, the medians of each event up to
+        # the next position's attention groups waking with the token
+        z = f_done
+
+        def med(vals):
+            return round(float(np.median(vals)) - z, 3)
+        rep["head_chain_us"] = {
+            "ffn_chunks_see_every_chunk": med([t[0, c, 10] for c in chunks]),
+            "final_residual_stored_and_flagged": med([t[0, c, 11] for c in chunks]),
+            "head_workgroups_see_it": med([t[0, h, 1] for h in heads]),
+            "head_blocks_end": med([t[0, h, 2] for h in heads]),
+            "head_keys_stored": med([t[0, h, 3] for h in heads]),
+            "next_position_attention_wakes": med([t[1, g, 1] for g in groups]),
+            "next_position_prologue_done": med([t[1, g, 2] for g in groups]),
+        }
     return rep
 
 

@@ -41,6 +41,7 @@ struct l3m_model {
     float        temp;         // the running generate call's temperature (0: greedy)
     l3m_pflayer *pf;           // batched prompt prefill: per-layer full matrices, NULL when unavailable
     l3m_pfbuf    pfb;
+    l3m_pfgraphs *pfg;         // the prefill's captured graphs (NULL: loose launches, L3M_PREFILL_GRAPH=0)
     int          prefill_min;  // prompts of at least this many tokens are prefilled (L3M_PREFILL_MIN)
     int          prefilled;    // positions the last generate call prefilled
     int          logits_fresh;
@@ -479,6 +480,8 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
         m->pfb.att = dalloc(m, ctx * (size_t)d->n_heads * d->hd * 4);
         m->pfb.gu = dalloc(m, ctx * 2 * (size_t)d->ffn * 4);
         if (!m->pfb.x || !m->pfb.act || !m->pfb.qkv || !m->pfb.att || !m->pfb.gu) return fail(m, "out of device memory");
+        const char *pg = getenv("L3M_PREFILL_GRAPH");  // 0: loose launches (for comparison)
+        if ((!pg || strcmp(pg, "0")) && !(m->pfg = l3m_pfgraphs_new())) return fail(m, "out of host memory");
     }
     d->samp = dalloc(m, sizeof(l3m_dsample));
     d->logits = dalloc(m, (size_t)NSLOTS * d->vocab * 4);
@@ -561,6 +564,7 @@ void l3m_free(l3m_model *m) {
     if (!m) return;
     l3m_dev_sync();
     l3m_graphs_free(m->graphs);
+    l3m_pfgraphs_free(m->pfg);
     l3m_dev_host_free(m->run_host);
     for (int i = 0; i < m->n_allocs; i++) l3m_dev_free(m->allocs[i]);
     free(m->allocs); free(m->layers); free(m->tok_host); free(m->logits); free(m->pf);
@@ -628,7 +632,9 @@ static int run(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, f
     int next = 0;
     m->prefilled = 0;
     if (m->pf && n_prompt - 1 >= m->prefill_min && n_prompt - 1 >= 1) {
-        if ((m->cold && evict(m)) || l3m_prefill(d, m->pf, &m->pfb, n_prompt - 1, NULL)) return -1;
+        if (m->cold && evict(m)) return -1;
+        if (m->pfg ? l3m_prefill_graph(m->pfg, d, m->pf, &m->pfb, n_prompt - 1) : l3m_prefill(d, m->pf, &m->pfb, n_prompt - 1, NULL))
+            return -1;
         next = m->prefilled = n_prompt - 1;
     }
     if (l3m_dev_upload(d->pos, &next, 4)) return -1;

@@ -161,6 +161,13 @@ typedef struct {
 int l3m_prefill(const l3m_dmodel *m, const l3m_pflayer *layers, const l3m_pfbuf *b, int P, void *stream);
 // 1 when l3m_prefill takes a model of these sizes (nqd = n_heads * hd); the loader enables prefill only then.
 int l3m_prefill_fits(int dim, int ffn, int nqd, int hd);
+// The prefill of P positions as one captured graph per P (the launches' grids and arguments depend on P
+// only; every buffer is the model's own), kept for the PF_GRAPHS most recently used lengths: a length seen
+// before replays its graph, a new one is captured and instantiated first. -1 on a device error.
+typedef struct l3m_pfgraphs l3m_pfgraphs;
+l3m_pfgraphs *l3m_pfgraphs_new(void);
+int           l3m_prefill_graph(l3m_pfgraphs *g, const l3m_dmodel *m, const l3m_pflayer *layers, const l3m_pfbuf *b, int P);
+void          l3m_pfgraphs_free(l3m_pfgraphs *g);
 
 // The persistent decode kernel (one cooperative launch for R->nsteps steps; layers_dev in device memory).
 int l3m_dev_cus(void);

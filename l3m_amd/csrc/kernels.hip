@@ -840,8 +840,9 @@ __device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, i
 // Per-phase timing of the decode step, in a build of its own (L3M_PHASE_STAMPS: make -C l3m_amd/csrc
 // phases, l3m_amd/libl3m_hip_phases.so; bench.py --phases): thread 0 of each attention group (role g),
 // FFN chunk (64 + c) and head workgroup (128 + h) records the 100 MHz clock at each phase boundary of two
-// consecutive layers (layer, layer + 1) at one position, armed by l3m_phase_stamps. The product build
-// compiles every stamp away.
+// consecutive layers at one position, armed by l3m_phase_stamps: (layer, layer + 1), or for the last
+// layer (its layer and the head, then layer 0 of the next position). The product build compiles every
+// stamp away.
 #ifdef L3M_PHASE_STAMPS
 __device__ unsigned long long g_phase[2][3 * 64][16];
 __device__ unsigned long long g_phase_clk[2][3 * 64][16];   // the shader clock (s_memtime) at the same points
@@ -849,10 +850,14 @@ __device__ int g_phase_at[2];
 __shared__ int s_phase_row;      // thread 0's: which of the two recorded layers this one is, or -1
 // At the top of a layer (before its wait): whether this (position, layer) is recorded. One global read per
 // layer, off the measured phases; the stamps then read only thread 0's LDS word.
-__device__ __forceinline__ void phase_arm(int pos, int layer) {
+__device__ __forceinline__ void phase_arm(int pos, int layer, int nl) {
     if (tidx() != 0) return;
-    const int d = layer - __hip_atomic_load(&g_phase_at[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_phase_row = pos == __hip_atomic_load(&g_phase_at[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) && (d == 0 || d == 1) ? d : -1;
+    const int at_pos = __hip_atomic_load(&g_phase_at[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int at_layer = __hip_atomic_load(&g_phase_at[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int d = layer - at_layer;
+    if (pos == at_pos && (d == 0 || d == 1)) s_phase_row = d;
+    else if (at_layer == nl - 1 && pos == at_pos + 1 && layer == 0) s_phase_row = 1;   // after the last layer
+    else s_phase_row = -1;
 }
 __device__ __forceinline__ void phase(int role, int ev, int, int) {
     if (tidx() != 0 || role >= 3 * 64) return;
@@ -863,7 +868,7 @@ __device__ __forceinline__ void phase(int role, int ev, int, int) {
     }
 }
 #else
-__device__ __forceinline__ void phase_arm(int, int) {}
+__device__ __forceinline__ void phase_arm(int, int, int) {}
 __device__ __forceinline__ void phase(int, int, int, int) {}
 #endif
 
@@ -2255,7 +2260,7 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
         const l3m_dlayer Lw = fixed(layers, l);
         const l3m_dgroup G = fixed(Lw.groups, g);
         AttnW<DT> wt;
-        phase_arm(pos, l);
+        phase_arm(pos, l, nl);
         phase(g, 0, pos, l);
         attn_static(wt.st, M, Lw, pos);
         attn_issue<DT>(wt, G);
@@ -2295,7 +2300,7 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
         const l3m_dchunk C = fixed(Lw.chunks, ci);
         FfnW<DT> wt;
         const int pos = R.pos0 + s;
-        phase_arm(pos, l);
+        phase_arm(pos, l, nl);
         phase(64 + ci, 0, pos, l);
         ffn_static(wt.st, M, Lw);
         ffn_issue<DT>(wt, C);
@@ -2311,7 +2316,7 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
         unsigned *sync = R.sync;
         if (!wait_flags<1>(sync + SY_FFN, fixed(Mp).n_chunks, (unsigned)((s + 1) * nl), sync + SY_ABORT, R.spin_limit, &ok_lds))
             return false;
-        phase_arm(R.pos0 + s, nl - 1);
+        phase_arm(R.pos0 + s, nl - 1, nl);
         phase(64 + ci, 10, R.pos0 + s, nl - 1);
         reduce_final(Mp, ci);
         set_flag<true>(sync + SY_XF + ci, (unsigned)s + 1);
@@ -2432,7 +2437,7 @@ __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, 
     int idx = 0x7FFFFFFF;
     const l3m_dmat V = head_slice(M, has_tiles ? t0 : 0, R.head_tpw);
     HeadW<DT> wt;
-    phase_arm(pos, M.n_layers - 1);
+    phase_arm(pos, M.n_layers - 1, M.n_layers);
     phase(128 + h, 0, pos, M.n_layers - 1);
     if (has_tiles) {
         pro_static(wt.st, M.dim >> 2, M.norm, nullptr, 0);
@@ -2549,47 +2554,65 @@ __global__ void __launch_bounds__(NTE) k_pf_silu_prep(const float *gu, int ffn, 
 
 // y[t][r] = sum over blocks b of d_w[r][b] * s_t[b] * (the int8 dot of row r and token t over block b):
 // the q8_0 gemv of every token at once (kernels_scalar.c:30-45), with the integer dots on
-// v_mfma_i32_16x16x32_i8 (one 32-input block per product). A workgroup takes one 16-row tile and 64
-// tokens, one wavefront per 16 tokens: lane l holds weights of row l % 16 and activations of token
-// l % 16, 8 bytes each at byte 8 (l / 16) of the block, and gets rows 4 (l / 16) + i of that token. Eight
-// blocks are loaded before their products (clamped indices, masked), so the loads overlap. add: y += the
-// result (the residual adds, engine.c:259, 275), else y = it.
+// v_mfma_i32_16x16x32_i8 (one 32-input block per product). A workgroup takes one 16-row tile and 16
+// tokens; its S = blockDim / 64 wavefronts (pf_split) split the blocks into S contiguous ranges of at most
+// PF_BATCH blocks each (more only past 16 * PF_BATCH blocks), each range's loads issued before its
+// products. The kernel is short: its time goes to instruction issue, so a wavefront gets few blocks. Lane
+// l holds weights of row l % 16 and activations of token l % 16, 8 bytes each at byte 8 (l / 16) of the
+// block, and gets rows 4 (l / 16) + i of that token; the S ranges' sums are added in range order through
+// LDS. add: y += the result (the residual adds, engine.c:259, 275), else y = it.
 typedef int v4i32 __attribute__((ext_vector_type(4)));
-constexpr int PF_BATCH = 8;
-__global__ void __launch_bounds__(256) k_pf_gemm(l3m_dmat W, const uint8_t *act, int astride, int P, float *y, int ystride, int add) {
-    const int lane = tidx() & 63, tile = blockIdx.x, tg = blockIdx.y * 4 + wave_id();
-    if (tg * 16 >= P) return;                                   // whole wavefronts past the tokens
+constexpr int PF_BATCH = 4;
+__host__ __device__ inline int pf_split(int nb) {
+    const int s = (nb + PF_BATCH - 1) / PF_BATCH;
+    return s < 1 ? 1 : s > NWE ? NWE : s;
+}
+__global__ void __launch_bounds__(NTE) k_pf_gemm(l3m_dmat W, const uint8_t *act, int astride, int P, float *y, int ystride, int add) {
+    __shared__ f32x4 part[NWE][64];
+    const int lane = tidx() & 63, wave = wave_id(), S = blockDim.x >> 6, tile = blockIdx.x, tg = blockIdx.y;
     const int nb = W.nb, kp = 32 * nb, quarter = lane >> 4, col = lane & 15;
+    const int per = (nb + S - 1) / S, r0 = wave * per, r1 = r0 + per < nb ? r0 + per : nb;   // this wavefront's blocks
     const int tok = tg * 16 + col < P ? tg * 16 + col : P - 1;
     const uint8_t *wq = (const uint8_t *)W.q + (size_t)tile * nb * 512 + col * 32 + quarter * 8;
     const uint16_t *ws = (const uint16_t *)W.s + (size_t)tile * nb * 16 + quarter * 4;
     const uint8_t *aq = act + (size_t)tok * astride + quarter * 8;
     const float *as = (const float *)(act + (size_t)tok * astride + kp);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int b0 = 0; b0 < nb; b0 += PF_BATCH) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = r0; b0 < r1; b0 += PF_BATCH) {
         long a8[PF_BATCH], x8[PF_BATCH];
         u32x2 sw[PF_BATCH];
         float sa[PF_BATCH];
 #pragma unroll
         for (int i = 0; i < PF_BATCH; i++) {
-            const int b = b0 + i < nb ? b0 + i : nb - 1;
+            const int b = b0 + i < r1 ? b0 + i : r1 - 1;
             a8[i] = *gp<long>(wq + (size_t)b * 512);
             x8[i] = *gp<long>(aq + (size_t)b * 32);
             sw[i] = *gp<u32x2>(ws + (size_t)b * 16);
             sa[i] = *gp<float>(as + b);
         }
+        // every load of the batch is issued before the first product: the loads cannot sink below the
+        // memory clobber, and the products read their operands through the moves after it
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < PF_BATCH; i++) asm volatile("" : "+v"(a8[i]), "+v"(x8[i]), "+v"(sw[i]), "+v"(sa[i]));
 #pragma unroll
         for (int i = 0; i < PF_BATCH; i++) {
             const v4i32 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a8[i], x8[i], v4i32{0, 0, 0, 0}, 0, 0, 0);
-            const float m = b0 + i < nb ? sa[i] : 0.f;
+            const float m = b0 + i < r1 ? sa[i] : 0.f;
             acc[0] += (float)c[0] * (f16_f32(sw[i].x & 0xFFFF) * m);
             acc[1] += (float)c[1] * (f16_f32(sw[i].x >> 16) * m);
             acc[2] += (float)c[2] * (f16_f32(sw[i].y & 0xFFFF) * m);
             acc[3] += (float)c[3] * (f16_f32(sw[i].y >> 16) * m);
         }
     }
+    if (wave) part[wave][lane] = acc;
+    __syncthreads();
     const int t = tg * 16 + col;
-    if (t < P) {
+    if (wave == 0 && t < P) {
+        for (int w = 1; w < S; w++) {
+            const f32x4 p = part[w][lane];
+            acc[0] += p[0]; acc[1] += p[1]; acc[2] += p[2]; acc[3] += p[3];
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = tile * 16 + 4 * quarter + i;
@@ -3175,7 +3198,8 @@ int l3m_prefill(const l3m_dmodel *M, const l3m_pflayer *L, const l3m_pfbuf *B, i
     hipStream_t st = as_stream(stream);
     const int dim = M->dim, hd = M->hd, nq = M->n_heads * hd, width = nq + 2 * M->n_kv * hd;
     auto gemm = [&](const l3m_dmat &W, float *y, int ystride, int add) {
-        hipLaunchKernelGGL(k_pf_gemm, dim3(W.tiles, (P + 63) / 64), dim3(256), 0, st, W, (const uint8_t *)B->act, B->astride, P, y, ystride, add);
+        hipLaunchKernelGGL(k_pf_gemm, dim3(W.tiles, (P + 15) / 16), dim3(64 * pf_split(W.nb)), 0, st, W, (const uint8_t *)B->act, B->astride, P, y,
+                           ystride, add);
     };
     hipLaunchKernelGGL(k_pf_embed, dim3(P), dim3(NTE), 0, st, M->embed, (const int32_t *)M->tokens, dim, B->x);
     for (int l = 0; l < M->n_layers; l++) {
@@ -3301,6 +3325,46 @@ bad:
 
 int l3m_graphs_launch(l3m_graphs *g, int with_head, void *stream) {
     CK(hipGraphLaunch(g->e[with_head ? 1 : 0], as_stream(stream)));
+    return 0;
+}
+
+constexpr int PF_GRAPHS = 8;
+struct l3m_pfgraphs {
+    int P[PF_GRAPHS];                 // 0: an empty entry
+    hipGraphExec_t e[PF_GRAPHS];
+    unsigned long long used[PF_GRAPHS], tick;
+};
+
+l3m_pfgraphs *l3m_pfgraphs_new(void) { return (l3m_pfgraphs *)calloc(1, sizeof(l3m_pfgraphs)); }
+
+void l3m_pfgraphs_free(l3m_pfgraphs *g) {
+    if (!g) return;
+    for (int i = 0; i < PF_GRAPHS; i++)
+        if (g->P[i]) (void)hipGraphExecDestroy(g->e[i]);
+    free(g);
+}
+
+int l3m_prefill_graph(l3m_pfgraphs *g, const l3m_dmodel *M, const l3m_pflayer *L, const l3m_pfbuf *B, int P) {
+    if (P < 1) return 0;
+    int k = -1, lru = 0;
+    for (int i = 0; i < PF_GRAPHS; i++) {
+        if (g->P[i] == P) k = i;
+        if (g->used[i] < g->used[lru]) lru = i;
+    }
+    if (k < 0) {                                       // capture this length into the least recently used entry
+        k = lru;
+        if (g->P[k]) { (void)hipGraphExecDestroy(g->e[k]); g->P[k] = 0; }
+        hipGraph_t graph;
+        if (hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal) != hipSuccess) return fail_msg("prefill graph capture");
+        const int rc = l3m_prefill(M, L, B, P, g_stream);
+        if (hipStreamEndCapture(g_stream, &graph) != hipSuccess || rc) return fail_msg("prefill graph capture");
+        const hipError_t e = hipGraphInstantiate(&g->e[k], graph, NULL, NULL, 0);
+        (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) return fail_msg("prefill graph instantiate");
+        g->P[k] = P;
+    }
+    g->used[k] = ++g->tick;
+    CK(hipGraphLaunch(g->e[k], g_stream));
     return 0;
 }
 

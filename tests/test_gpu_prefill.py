@@ -99,3 +99,28 @@ def test_prefill_logits(models, oracle, monkeypatch, cfg, n_prompt):
         lv = np.sort(lg)
         tie = (lv[-1] - lv[-2]) / np.abs(lv).max() < 0.005
         assert got[k] == order[0] or (tie and got[k] == order[1]), (k, got, order[:2])
+
+
+def test_prefill_graph_replays_equal_loose_launches(models, monkeypatch):
+    """The prefill runs as one captured graph per prompt length (L3M_PREFILL_GRAPH=0: the same launches
+    one by one). Every call, including replays of a length captured earlier with decoding and other lengths
+    run in between, gives logits and K/V rows bit-identical to the loose launches of the same prompt."""
+    cfg = GQA
+    path = models.get(cfg, cfg.dtype, seed=9, std=0.05, norm_jitter=0.1)
+    hd = cfg.dim // cfg.n_heads
+    graph = A.Model(path)
+    monkeypatch.setenv("L3M_PREFILL_GRAPH", "0")
+    loose = A.Model(path)
+    for i, n_prompt in enumerate([40, 100, 40, 57, 100, 40]):
+        print(f"call {i}: prompt {n_prompt}", flush=True)
+        ids = A.prompt(20 + i, cfg.vocab, n_prompt)
+        got = graph.generate(ids, 3)
+        want = loose.generate(ids, 3)
+        assert graph.prefilled == loose.prefilled == n_prompt - 1
+        assert got == want
+        assert np.array_equal(graph.logits, loose.logits)
+        for layer in range(cfg.n_layers):
+            for kvh in range(cfg.n_kv_heads):
+                kg, vg = graph.kv_rows(layer, kvh, 0, n_prompt - 1, hd)
+                kl_, vl = loose.kv_rows(layer, kvh, 0, n_prompt - 1, hd)
+                assert np.array_equal(kg, kl_) and np.array_equal(vg, vl), (i, layer, kvh)
