@@ -15,6 +15,7 @@
 #define NSLOTS 128             // logits slots = the most steps enqueued between two host reads
 #define HEAD_WGS 256           // workgroups of the head kernel
 #define MAX_PARTS 64           // partial residual vectors a step kernel adds (head groups, FFN chunks)
+#define BODY_CUS 32            // the CUs of one MI355X XCD (256 in 8), where the persistent kernel keeps the body
 #define EVICT_BYTES (512u << 20)   // --cold: read before each forward pass, twice the 256 MiB Infinity Cache
 
 struct l3m_model {
@@ -311,13 +312,15 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     while (quant && nq * d->hd % 32) nq++;                   // Wo slices of whole activation blocks
     if (d->n_heads % nq) nq = d->n_heads;
     d->n_groups = d->n_heads / nq;
-    // FFN chunk: the most rows (a multiple of 32) whose gate/up rows and Wdown columns fit the weight
-    // slots a workgroup holds in flight, so one pass of loads covers the chunk
+    // FFN chunk: the most rows (a multiple of 32) whose gate/up rows (up rows only for GPT-2) and Wdown
+    // columns fit the weight slots a workgroup holds in flight, so one pass of loads covers the chunk; then
+    // larger (more passes of loads) while the head groups and chunks would not fit the CUs of one XCD,
+    // where the persistent kernel keeps the body
     int sdt = m->reference ? L3M_F32 : m->mx_wide ? L3M_Q8_0 : m->dtype, cap_a = 64 * l3m_step_slots(sdt, 0), cap_b = 64 * l3m_step_slots(sdt, 1);
-    int nbd = (d->dim + 31) / 32, chunk = 32;
+    int nbd = (d->dim + 31) / 32, chunk = 32, gu = gpt2 ? 1 : 2;
     for (int c = 256; c >= 32; c -= 32)
-        if (2 * c / 16 * nbd <= cap_a && (d->dim + 15) / 16 * (c / 32) <= cap_b) { chunk = c; break; }
-    while ((d->ffn + chunk - 1) / chunk > MAX_PARTS) chunk += 32;
+        if (gu * c / 16 * nbd <= cap_a && (d->dim + 15) / 16 * (c / 32) <= cap_b) { chunk = c; break; }
+    while ((d->ffn + chunk - 1) / chunk > MAX_PARTS || (d->n_groups + (d->ffn + chunk - 1) / chunk > BODY_CUS && chunk < d->ffn)) chunk += 32;
     d->n_chunks = (d->ffn + chunk - 1) / chunk;
     d->body_dtype = sdt;
     if (d->n_groups > MAX_PARTS || d->n_chunks > MAX_PARTS) return fail(m, "too many head groups or FFN chunks for the GPU kernels");
@@ -500,9 +503,9 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
         if (lh > m->lds_decode) m->lds_decode = lh;
         if (m->lds_decode < lds_max / 2 + 16) m->lds_decode = lds_max / 2 + 16;
         const char *pe = getenv("L3M_PERSIST");
-        m->persist = (!pe || strcmp(pe, "0")) && !gpt2 && l3m_decode_pair(d->body_dtype, d->head.dtype) && d->n_groups <= 64 &&
+        m->persist = (!pe || strcmp(pe, "0")) && l3m_decode_pair(d->body_dtype, d->head.dtype, gpt2) && d->n_groups <= 64 &&
                      d->n_chunks <= 64 && d->vocab <= 0x20000 && m->head_tpw <= 64 && m->lds_decode <= lds_max &&
-                     l3m_decode_fits(d->body_dtype, d->head.dtype, m->grid, m->lds_decode);
+                     l3m_decode_fits(d->body_dtype, d->head.dtype, gpt2, m->grid, m->lds_decode);
         int *xcc = m->persist ? calloc((size_t)m->grid, sizeof *xcc) : NULL;
         if (xcc && !l3m_decode_placement(m->grid, m->lds_decode, xcc)) {
             int count[16] = {0};
@@ -583,7 +586,7 @@ static int decode_launch(l3m_model *m, int first, int last, int head_from) {
                        m->temp, 0};
     *m->run_host = r;
     if (l3m_dev_upload_async(m->run_dev, m->run_host, sizeof r)) return -1;
-    if (l3m_decode_launch(d->body_dtype, d->head.dtype, m->dm_dev, m->layers_dev, m->run_dev, m->grid, m->lds_decode, NULL)) return -1;
+    if (l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, m->dm_dev, m->layers_dev, m->run_dev, m->grid, m->lds_decode, NULL)) return -1;
     if (l3m_dev_download(&abort_flag, m->sync + L3M_SYNC_ABORT, 4)) return -1;
     if (l3m_decode_timer(2, NULL, NULL)) return -1;
     for (int p = first; p <= last; p++) {

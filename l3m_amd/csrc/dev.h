@@ -174,10 +174,10 @@ int l3m_dev_cus(void);
 // The XCD each block of a cooperative grid of `grid` 1024-thread workgroups with lds bytes lands on
 // (xcc[grid]); 0, or -1 on a device error.
 int l3m_decode_placement(int grid, unsigned lds, int *xcc);
-int l3m_decode_pair(int dtype, int head_dtype);              // 1 if the kernel is built for this (body, head) pair
-int l3m_decode_fits(int dtype, int head_dtype, int grid, unsigned lds);   // 1 if grid workgroups with lds bytes can all be resident
+int l3m_decode_pair(int dtype, int head_dtype, int gpt2);    // 1 if the kernel is built for this (body, head, variant)
+int l3m_decode_fits(int dtype, int head_dtype, int gpt2, int grid, unsigned lds);   // 1 if grid workgroups with lds bytes can all be resident
 // m_dev, layers_dev, r_dev: device-memory copies (the kernel reads its parameters from there)
-int l3m_decode_launch(int dtype, int head_dtype, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev, int grid,
+int l3m_decode_launch(int dtype, int head_dtype, int gpt2, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev, int grid,
                       unsigned lds, void *stream);
 
 // Timing (microseconds per launch, hipEvents on the library stream, after one untimed launch).

@@ -2246,7 +2246,7 @@ __device__ __noinline__ void reduce_final(const l3m_dmodel *Mp, int c) {
 
 // The roles, each in a function of its own (so each gets its own register allocation and nothing of one
 // role stays live in another). They return false when the run is being abandoned.
-template <int DT>
+template <int DT, bool G2>
 __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *layers, const l3m_run *Rp, int g, int s) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int ok_lds;
@@ -2279,14 +2279,14 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
             if (l == 0) tok = __hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         phase(g, 1, pos, l);
-        attn_block<DT, true>(M, Lw, G, l, pos, tok, g, wt, smem);
+        attn_block<DT, true, G2>(M, Lw, G, l, pos, tok, g, wt, smem);
         set_flag<false>(sync + SY_ATTN + g, epoch + 1);
         phase(g, 10, pos, l);
     }
     return true;
 }
 
-template <int DT>
+template <int DT, bool G2>
 __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *layers, const l3m_run *Rp, int ci, int s) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int ok_lds;
@@ -2307,7 +2307,7 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
         const unsigned epoch = (unsigned)(s * nl + l);
         if (!wait_flags<1>(sync + SY_ATTN, M.n_groups, epoch + 1, sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
         phase(64 + ci, 1, pos, l);
-        ffn_block<DT, true>(M, Lw, C, ci, wt, smem, l, pos);
+        ffn_block<DT, true, G2>(M, Lw, C, ci, wt, smem, l, pos);
         set_flag<false>(sync + SY_FFN + ci, epoch + 1);
         phase(64 + ci, 9, pos, l);
     }
@@ -2424,7 +2424,7 @@ __device__ bool sample_step(const l3m_dmodel &M, const l3m_run &R, int h, int s,
 }
 
 // Head workgroup h: tiles [h * head_tpw, (h + 1) * head_tpw) of step s, once the final residual is out.
-template <int DT>
+template <int DT, bool G2>
 __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, int h, int s) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int ok_lds;
@@ -2447,7 +2447,7 @@ __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, 
     phase(128 + h, 1, pos, M.n_layers - 1);
     const float temp = R.temp;
     float *keep = temp > 0 ? (float *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).lgv) : nullptr;
-    if (has_tiles) head_block<DT, true>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx, keep);
+    if (has_tiles) head_block<DT, true, G2>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx, keep);
     phase(128 + h, 2, pos, M.n_layers - 1);
     if (tidx() == 0)
         __hip_atomic_store(gw((uint64_t *)(R.sync + SY_SLOTS) + h), argmax_key(v, idx, step_tag(s)), __ATOMIC_RELAXED,
@@ -2478,8 +2478,8 @@ __device__ int deal_role(const l3m_run &R, int n_body, int *lds) {
 }
 
 // DT: the body's dtype, HDT: the head's (a file may quantize its head differently, as the reference's
-// exporter allows: test_engine.py:187-191).
-template <int DT, int HDT>
+// exporter allows: test_engine.py:187-191); G2: the GPT-2 variant (model.h:19-26).
+template <int DT, int HDT, bool G2>
 __global__ void __launch_bounds__(NTE) k_decode(const l3m_dmodel *__restrict__ Mp, const l3m_dlayer *__restrict__ layers,
                                                 const l3m_run *__restrict__ Rp) {
     __shared__ int role_lds;
@@ -2488,11 +2488,11 @@ __global__ void __launch_bounds__(NTE) k_decode(const l3m_dmodel *__restrict__ M
     const int role = deal_role(R, n_body, &role_lds);
     for (int s = 0; s < R.nsteps; s++) {
         if (role < n_groups) {
-            if (!attn_role<DT>(Mp, layers, Rp, role, s)) return;
+            if (!attn_role<DT, G2>(Mp, layers, Rp, role, s)) return;
         } else if (role < n_body) {
-            if (!ffn_role<DT>(Mp, layers, Rp, role - n_groups, s)) return;
+            if (!ffn_role<DT, G2>(Mp, layers, Rp, role - n_groups, s)) return;
         } else if (R.pos0 + s >= R.head_from && role - n_body < R.n_head) {
-            if (!head_role<HDT>(Mp, Rp, role - n_body, s)) return;
+            if (!head_role<HDT, G2>(Mp, Rp, role - n_body, s)) return;
         }
     }
     // the last step's token has no next step in this launch to take it: group 0 writes it
@@ -2856,15 +2856,15 @@ template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t
 hipEvent_t g_dec_ev[2];
 int g_dec_timing, g_dec_launches, g_dec_pending;
 double g_dec_us;
-template <int DT, int HDT> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *layers, const l3m_run *R_dev, int grid,
-                                             unsigned lds, hipStream_t st) {
-    lds_opt_in(k_decode<DT, HDT>, lds);
+template <int DT, int HDT, bool G2> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *layers, const l3m_run *R_dev, int grid,
+                                                      unsigned lds, hipStream_t st) {
+    lds_opt_in(k_decode<DT, HDT, G2>, lds);
     const l3m_dmodel *m = M_dev;
     const l3m_dlayer *ly = layers;
     const l3m_run *r = R_dev;
     void *args[] = {&m, &ly, &r};
     if (g_dec_timing) CK(hipEventRecord(g_dec_ev[0], st));
-    const hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode<DT, HDT>, dim3(grid), dim3(NTE), args, lds, st);
+    const hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode<DT, HDT, G2>, dim3(grid), dim3(NTE), args, lds, st);
     if (e != hipSuccess) return fail("decode launch", e);
     if (g_dec_timing) {
         CK(hipEventRecord(g_dec_ev[1], st));
@@ -2872,10 +2872,10 @@ template <int DT, int HDT> int launch_decode(const l3m_dmodel *M_dev, const l3m_
     }
     return 0;
 }
-template <int DT, int HDT> int decode_fits(int grid, unsigned lds) {
-    lds_opt_in(k_decode<DT, HDT>, lds);
+template <int DT, int HDT, bool G2> int decode_fits(int grid, unsigned lds) {
+    lds_opt_in(k_decode<DT, HDT, G2>, lds);
     int per_cu = 0, cus = 0, coop = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode<DT, HDT>, NTE, lds) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode<DT, HDT, G2>, NTE, lds) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, 0) != hipSuccess || !coop) return 0;
     return per_cu >= 1 && grid <= per_cu * cus;
@@ -3238,23 +3238,26 @@ int l3m_dev_cus(void) {
     return cus;
 }
 
-// The (body, head) dtype pairs the persistent kernel is built for: every dtype with a head of its own
-// dtype, the mixed heads of the reference's tests (test_engine.py:187-191), and an mxfp4 model whose body
-// runs as q8_0 (its blocks widened exactly) with its mxfp4 head.
+// The (body, head, GPT-2) kinds the persistent kernel is built for: every dtype with a head of its own
+// dtype, the mixed heads of the reference's tests (test_engine.py:187-191), an mxfp4 model whose body runs
+// as q8_0 (its blocks widened exactly) with its mxfp4 head, and the GPT-2 variant in the dtypes its
+// exporter writes (f32, bf16, q8_0, q4_0, each with a head of its own dtype).
 #define DECODE_PAIRS(X) \
-    X(L3M_F32, L3M_F32) X(L3M_BF16, L3M_BF16) X(L3M_Q8_0, L3M_Q8_0) X(L3M_Q4_0, L3M_Q4_0) X(L3M_MXFP4, L3M_MXFP4) \
-    X(L3M_Q4_0, L3M_Q8_0) X(L3M_MXFP4, L3M_Q8_0) X(L3M_Q8_0, L3M_BF16) X(L3M_Q8_0, L3M_MXFP4)
+    X(L3M_F32, L3M_F32, false) X(L3M_BF16, L3M_BF16, false) X(L3M_Q8_0, L3M_Q8_0, false) X(L3M_Q4_0, L3M_Q4_0, false) \
+    X(L3M_MXFP4, L3M_MXFP4, false) X(L3M_Q4_0, L3M_Q8_0, false) X(L3M_MXFP4, L3M_Q8_0, false) X(L3M_Q8_0, L3M_BF16, false) \
+    X(L3M_Q8_0, L3M_MXFP4, false) X(L3M_F32, L3M_F32, true) X(L3M_BF16, L3M_BF16, true) X(L3M_Q8_0, L3M_Q8_0, true) \
+    X(L3M_Q4_0, L3M_Q4_0, true)
 
-int l3m_decode_pair(int dtype, int head_dtype) {
-#define PAIR_KNOWN(a, b) if (dtype == a && head_dtype == b) return 1;
+int l3m_decode_pair(int dtype, int head_dtype, int gpt2) {
+#define PAIR_KNOWN(a, b, g) if (dtype == a && head_dtype == b && !gpt2 == !g) return 1;
     DECODE_PAIRS(PAIR_KNOWN)
 #undef PAIR_KNOWN
     return 0;
 }
 
-int l3m_decode_fits(int dtype, int head_dtype, int grid, unsigned lds) {
+int l3m_decode_fits(int dtype, int head_dtype, int gpt2, int grid, unsigned lds) {
     if (l3m_dev_init()) return 0;
-#define PAIR_FITS(a, b) if (dtype == a && head_dtype == b) return decode_fits<a, b>(grid, lds);
+#define PAIR_FITS(a, b, g) if (dtype == a && head_dtype == b && !gpt2 == !g) return decode_fits<a, b, g>(grid, lds);
     DECODE_PAIRS(PAIR_FITS)
 #undef PAIR_FITS
     return 0;
@@ -3299,10 +3302,11 @@ int l3m_decode_placement(int grid, unsigned lds, int *xcc) {
     return e == hipSuccess ? 0 : fail("placement probe", e);
 }
 
-int l3m_decode_launch(int dtype, int head_dtype, const l3m_dmodel *M_dev, const l3m_dlayer *layers_dev, const l3m_run *R_dev, int grid,
-                      unsigned lds, void *stream) {
+int l3m_decode_launch(int dtype, int head_dtype, int gpt2, const l3m_dmodel *M_dev, const l3m_dlayer *layers_dev, const l3m_run *R_dev,
+                      int grid, unsigned lds, void *stream) {
     hipStream_t st = as_stream(stream);
-#define PAIR_LAUNCH(a, b) if (dtype == a && head_dtype == b) return launch_decode<a, b>(M_dev, layers_dev, R_dev, grid, lds, st);
+#define PAIR_LAUNCH(a, b, g) \
+    if (dtype == a && head_dtype == b && !gpt2 == !g) return launch_decode<a, b, g>(M_dev, layers_dev, R_dev, grid, lds, st);
     DECODE_PAIRS(PAIR_LAUNCH)
 #undef PAIR_LAUNCH
     return fail_msg("decode: no persistent kernel for this pair of dtypes");

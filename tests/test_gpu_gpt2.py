@@ -1,8 +1,9 @@
 """The GPT-2 variant on the GPU (LayerNorm with biases, learned positions, biases on every matrix, GELU
 MLP without gate; model.h:19-26, engine.c:236-275), through the l3m.h API, against the oracle (pinned
-bit-exact against the reference's --ref path in test_cpu_sampling.py). It runs on the one-graph-per-step
-path; the bar is the engine's: equal argmax, KL < 0.01 nats, max-abs within SPREAD of max|logit| after
-the prompt, and the greedy tokens of the oracle until its first near-tie.
+bit-exact against the reference's --ref path in test_cpu_sampling.py). It runs on the persistent decode
+kernel, whose tokens and logits equal the one-graph-per-step path's (L3M_PERSIST=0) bit for bit; the bar
+against the oracle is the engine's: equal argmax, KL < 0.01 nats, max-abs within SPREAD of max|logit|
+after the prompt, and the greedy tokens of the oracle until its first near-tie.
 """
 import numpy as np
 import pytest
@@ -33,7 +34,7 @@ def test_gpt2_matches_oracle(models, oracle, dtype):
     path = models.get(CFG, dtype, seed=5, std=0.06, norm_jitter=0.1, arch="gpt2")
     ids = A.prompt(5, CFG.vocab, 12)
     m, om = A.Model(path), oracle.load(path)
-    assert not m.persistent
+    assert m.persistent
     m.generate(ids, 0)
     assert m.prefilled == 0
     om.generate(ids, 0)
@@ -80,3 +81,20 @@ def test_gptneo_without_qkv_biases(models, oracle, dtype):
         if k == 0:
             lo, lgpu = lg, m.logits_at(pos)
             assert kl(lo, lgpu) < 0.01 and np.abs(lgpu - lo).max() <= SPREAD[dtype] * np.abs(lo).max()
+
+
+@pytest.mark.parametrize("arch,dtype", [("gpt2", "f32"), ("gpt2", "q4_0"), ("gptneo", "q8_0"), ("gptneo", "bf16")])
+def test_persistent_kernel_equals_graph_path(models, monkeypatch, arch, dtype):
+    """The GPT-2 family on the persistent kernel against the same model decoded one graph per step: the
+    same greedy tokens and bit-identical logits at the end of each of three calls."""
+    print(f"case {arch} {dtype}", flush=True)
+    path = models.get(CFG, dtype, seed=11, std=0.06, norm_jitter=0.1, arch=arch)
+    fast = A.Model(path)
+    assert fast.persistent
+    monkeypatch.setenv("L3M_PERSIST", "0")
+    step = A.Model(path)
+    assert not step.persistent
+    for i, (n_prompt, n_new) in enumerate([(5, 40), (1, 62), (20, 10)]):
+        ids = A.prompt(30 + i, CFG.vocab, n_prompt)
+        assert fast.generate(ids, n_new) == step.generate(ids, n_new), i
+        assert np.array_equal(fast.logits, step.logits), i

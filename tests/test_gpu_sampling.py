@@ -46,16 +46,18 @@ def test_sampled_tokens_match_oracle(models, oracle, monkeypatch, dtype, persist
     assert len(seen) > 4
 
 
+@pytest.mark.parametrize("persist", ["1", "0"])
 @pytest.mark.parametrize("arch,vocab", [("llama", 1001), ("gpt2", 50257)])
-def test_sampled_any_vocabulary(models, oracle, arch, vocab):
+def test_sampled_any_vocabulary(models, oracle, monkeypatch, arch, vocab, persist):
     """Temperature sampling with a vocabulary that is not a multiple of 4 (GPT-2's 50257 among them): the
-    GPU's picks equal the oracle's from the GPU's own logits (GPT-2 on the one-graph-per-step path, the Llama
-    model on the persistent kernel)."""
+    GPU's picks equal the oracle's from the GPU's own logits, on the persistent kernel and on the
+    one-graph-per-step path."""
+    monkeypatch.setenv("L3M_PERSIST", persist)
     cfg = A.Config(f"samp{vocab}", dim=128, n_layers=2, n_heads=4, n_kv_heads=4 if arch == "gpt2" else 2, ffn_dim=256, vocab=vocab,
                    ctx=64, dtype="q8_0")
     path = models.get(cfg, "q8_0", seed=9, std=0.08, arch=arch)
     m = A.Model(path)
-    assert m.persistent == (arch == "llama")
+    assert m.persistent == (persist == "1")
     ids = A.prompt(9, vocab, 4)
     for seed in range(3):
         check_against_oracle(m, oracle, ids, 0.8, seed, 24)
