@@ -130,7 +130,8 @@ int    l3m_k_argmax(const float *x, int n, int32_t *out, void *stream);         
 // into out[n][32 * m->nb];
 int    l3m_k_dequant(const l3m_dmat *m, int row0, int n, float *out, void *stream);
 // which attention a decode step runs for a head group of nq query heads (2 matrix cores over the K/V
-// window in LDS, 1 VALU over the window, 0 VALU reading the cache; kv_lds: the window fits in LDS);
+// window in LDS, for hd a multiple of 16; 1 VALU over the window; 0 VALU reading the cache; kv_lds: the
+// window fits in LDS);
 int    l3m_attention_mode(int kv_lds, int hd, int nq, int ctx);
 // one head group's attention in that mode, exactly as the decode step runs it (l3m_attend, ops.c:58-73, for
 // each query head; GQA head h reads kv head h / (nq / nkv)): q [nq][hd] f32, kc and vc [nkv][ctx][hd] bf16
@@ -177,7 +178,8 @@ int    l3m_phase_stamps(int mode, int pos, int layer, unsigned long long *out);
 // greedy tokens are checked against the logits they came from).
 int    l3m_logits_at(const l3m_model *m, int pos, float *out);
 // Prompt positions the last generate call ran as one batched prefill (0: token by token). Prompts of at
-// least L3M_PREFILL_MIN (default 8) tokens on q8_0 and q4_0 bodies are prefilled unless L3M_PREFILL=0.
+// least L3M_PREFILL_MIN (default 8) tokens on q8_0 and q4_0 bodies (and mxfp4 bodies whose blocks widen
+// exactly to q8_0) are prefilled unless L3M_PREFILL=0.
 int    l3m_prefill_positions(const l3m_model *m);
 // The attention mode the decode step of m runs (l3m_attention_mode's codes).
 int    l3m_decode_attention(const l3m_model *m);
