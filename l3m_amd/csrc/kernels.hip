@@ -1645,16 +1645,18 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     else if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
     else attend_group<false, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
     phase(gi, 6, pos, layer);
-    // this step's k and v rows (bf16, engine.c:247-248) into the cache, for the kv heads this group writes;
-    // the flag after the block waits for them
-    for (int i = tid; i < 2 * nkd; i += NTE) {
-        const int kv = i < nkd ? 0 : 1, jj = i - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
-        if (G.write_kv >> kvl & 1u)
-            gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + (jj - kvl * hd)] = cur[i];
-    }
+    // this step's k and v rows (bf16, engine.c:247-248) into the cache, for the kv heads this group writes,
+    // by the wavefronts past those that prepare the attention output next (they go straight to the prep);
+    // the flag after the block waits for the stores
+    const int kq = kpad(nqd), skip = (kq + 255) >> 8 < NWE ? 64 * ((kq + 255) >> 8) : 0;
+    if (tid >= skip)
+        for (int i = tid - skip; i < 2 * nkd; i += NTE - skip) {
+            const int kv = i < nkd ? 0 : 1, jj = i - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
+            if (G.write_kv >> kvl & 1u)
+                gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + (jj - kvl * hd)] = cur[i];
+        }
 
     // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
-    const int kq = kpad(nqd);
     prep_owned<AT>(4 * tid < nqd ? ((const float4 *)att)[tid] : make_float4(0.f, 0.f, 0.f, 0.f), act2, kq);
     phase(gi, 7, pos, layer);
     mv<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
