@@ -2569,7 +2569,17 @@ __host__ __device__ inline int pf_split(int nb) {
     const int s = (nb + PF_BATCH - 1) / PF_BATCH;
     return s < 1 ? 1 : s > NWE ? NWE : s;
 }
-__global__ void __launch_bounds__(NTE) k_pf_gemm(l3m_dmat W, const uint8_t *act, int astride, int P, float *y, int ystride, int add) {
+// The qkv matrix's epilogue (PfQkv): RoPE on the q and k rows (pairs (2i, 2i+1) of each head rotated by
+// the angle i of position t from the host table, ops.c:29-40), q into y, the k and v rows rounded to bf16
+// into the cache (engine.c:247-248). A lane's four rows are two whole pairs.
+struct PfQkv {
+    const float *rope;
+    uint16_t *kc, *vc;
+    int layer, ctx, nq, nk, hd, n_kv;
+};
+template <bool QKV>
+__global__ void __launch_bounds__(NTE) k_pf_gemm(l3m_dmat W, const uint8_t *act, int astride, int P, float *y, int ystride, int add,
+                                                 PfQkv E) {
     __shared__ f32x4 part[NWE][64];
     const int lane = tidx() & 63, wave = wave_id(), S = blockDim.x >> 6, tile = blockIdx.x, tg = blockIdx.y;
     const int nb = W.nb, kp = 32 * nb, quarter = lane >> 4, col = lane & 15;
@@ -2615,6 +2625,31 @@ __global__ void __launch_bounds__(NTE) k_pf_gemm(l3m_dmat W, const uint8_t *act,
             const f32x4 p = part[w][lane];
             acc[0] += p[0]; acc[1] += p[1]; acc[2] += p[2]; acc[3] += p[3];
         }
+        if constexpr (QKV) {
+            const int r0 = tile * 16 + 4 * quarter;   // even: rows r0 .. r0 + 3 are pairs (r0, r0 + 1), (r0 + 2, r0 + 3)
+            const float2 *cs = (const float2 *)(E.rope + (size_t)t * E.hd);
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+                const int e = r0 + i;
+                if (e < E.nq + E.nk) {
+                    const int j = (e < E.nq ? e : e - E.nq) % E.hd;
+                    const float2 c = cs[j >> 1];
+                    const float a = acc[i], b = acc[i + 1];
+                    acc[i] = a * c.x - b * c.y;
+                    acc[i + 1] = a * c.y + b * c.x;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = r0 + i;
+                if (r < E.nq) y[(size_t)t * ystride + r] = acc[i];
+                else if (r < W.rows) {
+                    const int kv = r < E.nq + E.nk ? 0 : 1, rr = r - E.nq - kv * E.nk, h = rr / E.hd, j = rr - h * E.hd;
+                    (kv ? E.vc : E.kc)[(((size_t)E.layer * E.n_kv + h) * E.ctx + t) * E.hd + j] = f32_bf16(acc[i]);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = tile * 16 + 4 * quarter + i;
@@ -2626,45 +2661,45 @@ __global__ void __launch_bounds__(NTE) k_pf_gemm(l3m_dmat W, const uint8_t *act,
     }
 }
 
-// RoPE on the q and k rows of every token (ops.c:29-40, angles of position t from the host table), then
-// the k and v rows rounded to bf16 into the cache (engine.c:247-248); q stays in qkv for the attention.
-__global__ void __launch_bounds__(256) k_pf_rope_kv(float *qkv, int P, int n_heads, int n_kv, int hd, int ctx, int layer,
-                                                    const float *rope, uint16_t *kc, uint16_t *vc) {
-    const int t = blockIdx.x, nq = n_heads * hd, nk = n_kv * hd, width = nq + 2 * nk;
-    float *row = qkv + (size_t)t * width;
-    const float2 *cs = (const float2 *)(rope + (size_t)t * hd);
-    for (int i = tidx(); i < (nq + nk) / 2; i += blockDim.x) {   // pairs (2i, 2i+1) of q, then of k
-        const int e = 2 * i, j = (e < nq ? e : e - nq) % hd;
-        const float2 c = cs[j >> 1];
-        const float a = row[e], b = row[e + 1];
-        row[e] = a * c.x - b * c.y;
-        row[e + 1] = a * c.y + b * c.x;
-    }
-    __syncthreads();
-    for (int i = tidx(); i < 2 * nk; i += blockDim.x) {
-        const int kv = i < nk ? 0 : 1, r = i - kv * nk, h = r / hd, j = r - h * hd;
-        (kv ? vc : kc)[(((size_t)layer * n_kv + h) * ctx + t) * hd + j] = f32_bf16(row[nq + i]);
-    }
-}
-
 // Attention of token t, head h over positions 0..t (ops.c:42-73): one wavefront per (t, h), positions in
 // chunks of 64 (a lane per position) with a running maximum and sum; then each lane sums its output
 // dims over the chunk's weights. q from qkv (after RoPE), K and V from the cache as bf16.
 __global__ void __launch_bounds__(64) k_pf_attend(const float *qkv, int P, int n_heads, int n_kv, int hd, int ctx, int layer,
-                                                  float scale, const uint16_t *kc, const uint16_t *vc, float *att) {
-    __shared__ float qs[256], ps[64];
+                                                  float scale, const uint16_t *kc, const uint16_t *vc, float *att, uint8_t *act,
+                                                  int astride) {
+    constexpr int VMAX = 32;                          // V rows a lane loads per 64-position chunk (h8 <= 32)
+    __shared__ float qs[256], ps[64], part[64 * 8];
     const int t = blockIdx.x, h = blockIdx.y, lane = tidx(), hpk = n_heads / n_kv, kv = h / hpk;
-    const int width = n_heads * hd + 2 * n_kv * hd;
+    const int width = n_heads * hd + 2 * n_kv * hd, h8 = hd >> 3;
+    // P.V: lane = jg * h8 + dg takes dims [8 dg, 8 dg + 8) at positions jg, jg + JG, ... of a chunk
+    const int JG = 64 / h8, jg = lane / h8, dg = lane - jg * h8;
+    const bool vlane = jg < JG;
     for (int d = lane; d < hd; d += 64) qs[d] = qkv[(size_t)t * width + h * hd + d];
     __syncthreads();
     const uint16_t *K = kc + ((size_t)layer * n_kv + kv) * ctx * hd, *V = vc + ((size_t)layer * n_kv + kv) * ctx * hd;
     float m = -INFINITY, l = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};   // output dims lane, lane + 64, ... (hd <= 256)
     for (int p0 = 0; p0 <= t; p0 += 64) {
-        const int p = p0 + lane;
+        const int p = p0 + lane, n = t - p0 + 1 < 64 ? t - p0 + 1 : 64;
+        // the V rows this lane multiplies, requested before the scores so their latency overlaps them
+        uint4 vv[VMAX];
+#pragma unroll
+        for (int u = 0; u < VMAX; u++) {
+            const int j = jg + u * JG;
+            vv[u] = (u * JG < 64) ? ((const uint4 *)(V + (size_t)(p0 + (vlane && j < n ? j : 0)) * hd))[dg] : make_uint4(0u, 0u, 0u, 0u);
+        }
         float sc = -INFINITY;
         if (p <= t) {
+            // the lane's K row in 16-byte words, eight loads in flight before their products
+            const uint4 *kr = (const uint4 *)(K + (size_t)p * hd);
             float dot = 0.f;
-            for (int d = 0; d < hd; d++) dot += qs[d] * bf16_f32(K[(size_t)p * hd + d]);
+            for (int v0 = 0; v0 < h8; v0 += 8) {
+                uint4 kk[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) kk[u] = kr[v0 + u < h8 ? v0 + u : h8 - 1];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (v0 + u < h8) dot = dot8_bf16(qs + 8 * (v0 + u), kk[u], dot);
+            }
             sc = dot * scale;
         }
         const float cm = lanes_max<64>(sc), nm = fmaxf(m, cm);
@@ -2672,18 +2707,61 @@ __global__ void __launch_bounds__(64) k_pf_attend(const float *qkv, int P, int n
         l = l * rescale + lanes_sum<64>(w);
         ps[lane] = w;
         __syncthreads();
-        const int n = t - p0 + 1 < 64 ? t - p0 + 1 : 64;
+        // each lane's 8 dims over its positions, then the JG partial sums of a dim added in jg order
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < VMAX; u++) {
+            const int j = jg + u * JG;
+            if (u * JG < 64 && vlane && j < n) {
+                const float pj = ps[j];
+                const uint4 x = vv[u];
+                acc[0] += pj * bf16_f32(x.x & 0xFFFF); acc[1] += pj * bf16_f32(x.x >> 16);
+                acc[2] += pj * bf16_f32(x.y & 0xFFFF); acc[3] += pj * bf16_f32(x.y >> 16);
+                acc[4] += pj * bf16_f32(x.z & 0xFFFF); acc[5] += pj * bf16_f32(x.z >> 16);
+                acc[6] += pj * bf16_f32(x.w & 0xFFFF); acc[7] += pj * bf16_f32(x.w >> 16);
+            }
+        }
+        if (vlane) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) part[jg * hd + 8 * dg + e] = acc[e];
+        }
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int d = lane + 64 * i;
             if (d < hd) {
-                float acc = o[i] * rescale;
-                for (int j = 0; j < n; j++) acc += ps[j] * bf16_f32(V[(size_t)(p0 + j) * hd + d]);
-                o[i] = acc;
+                float sum = 0.f;
+                for (int g = 0; g < JG; g++) sum += part[g * hd + d];
+                o[i] = o[i] * rescale + sum;
             }
         }
         m = nm;
         __syncthreads();
+    }
+    if (act) {
+        // hd a multiple of 32: the head's 32-blocks of the output prepared here, as k_pf_prep would (per block
+        // amax, inv = 127 / amax, q = rint(x * inv), the scale amax / 127 and the sum of q), into act[t]
+        uint8_t *row = act + (size_t)t * astride;
+        const int nb = (n_heads * hd) >> 5;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (64 * i >= hd) break;                  // uniform; a group of 32 lanes is a whole block or past hd
+            const int d = lane + 64 * i;
+            const float x = d < hd ? o[i] / l : 0.f;
+            const float am = lanes_max<32>(fabsf(x));
+            const float inv = am > 0.f ? 127.0f / am : 0.f;
+            const int q = (int)rintf(x * inv);
+            const float qs32 = lanes_sum<32>((float)q);   // |sum| <= 32 * 127: exact in float
+            if (d < hd) {
+                const int blk = (h * hd + d) >> 5;
+                row[h * hd + d] = (uint8_t)(q & 255);
+                if ((lane & 31) == 0) {
+                    ((float *)(row + 32 * nb))[blk] = am / 127.0f;
+                    ((int *)(row + 36 * nb))[blk] = (int)qs32;
+                }
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -3199,25 +3277,29 @@ int l3m_prefill(const l3m_dmodel *M, const l3m_pflayer *L, const l3m_pfbuf *B, i
     if (P > M->ctx || !l3m_prefill_fits(M->dim, M->ffn, M->n_heads * M->hd, M->hd)) return fail_msg("prefill: shape out of range");
     hipStream_t st = as_stream(stream);
     const int dim = M->dim, hd = M->hd, nq = M->n_heads * hd, width = nq + 2 * M->n_kv * hd;
-    auto gemm = [&](const l3m_dmat &W, float *y, int ystride, int add) {
-        hipLaunchKernelGGL(k_pf_gemm, dim3(W.tiles, (P + 15) / 16), dim3(64 * pf_split(W.nb)), 0, st, W, (const uint8_t *)B->act, B->astride, P, y,
-                           ystride, add);
+    const PfQkv none{}, qkv_out{M->rope, M->kc, M->vc, 0, M->ctx, nq, M->n_kv * hd, hd, M->n_kv};
+    auto gemm = [&](const l3m_dmat &W, float *y, int ystride, int add, const PfQkv *E) {
+        const dim3 grid(W.tiles, (P + 15) / 16), block(64 * pf_split(W.nb));
+        if (E) hipLaunchKernelGGL(k_pf_gemm<true>, grid, block, 0, st, W, (const uint8_t *)B->act, B->astride, P, y, ystride, add, *E);
+        else hipLaunchKernelGGL(k_pf_gemm<false>, grid, block, 0, st, W, (const uint8_t *)B->act, B->astride, P, y, ystride, add, none);
     };
     hipLaunchKernelGGL(k_pf_embed, dim3(P), dim3(NTE), 0, st, M->embed, (const int32_t *)M->tokens, dim, B->x);
     for (int l = 0; l < M->n_layers; l++) {
         const l3m_pflayer &W = L[l];
         hipLaunchKernelGGL(k_pf_norm_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->x, W.attn_norm, dim, M->eps, B->act, B->astride);
-        gemm(W.qkv, B->qkv, width, 0);
-        hipLaunchKernelGGL(k_pf_rope_kv, dim3(P), dim3(256), 0, st, B->qkv, P, M->n_heads, M->n_kv, hd, M->ctx, l, M->rope, M->kc, M->vc);
+        PfQkv E = qkv_out;                            // q (after RoPE) into qkv, k and v into the cache
+        E.layer = l;
+        gemm(W.qkv, B->qkv, width, 0, &E);
+        if (l == M->n_layers - 1) break;              // the last layer's K/V rows are all its prompt positions leave
+        const bool fuse = hd % 32 == 0;               // whole blocks per head: the attention prepares its output
         hipLaunchKernelGGL(k_pf_attend, dim3(P, M->n_heads), dim3(64), 0, st, (const float *)B->qkv, P, M->n_heads, M->n_kv, hd, M->ctx, l,
-                           M->att_scale, (const uint16_t *)M->kc, (const uint16_t *)M->vc, B->att);
-        if (l == M->n_layers - 1) break;              // the last layer's residual feeds only the head
-        hipLaunchKernelGGL(k_pf_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->att, nq, nq, B->act, B->astride);
-        gemm(W.wo, B->x, dim, 1);
+                           M->att_scale, (const uint16_t *)M->kc, (const uint16_t *)M->vc, B->att, fuse ? B->act : nullptr, B->astride);
+        if (!fuse) hipLaunchKernelGGL(k_pf_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->att, nq, nq, B->act, B->astride);
+        gemm(W.wo, B->x, dim, 1, nullptr);
         hipLaunchKernelGGL(k_pf_norm_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->x, W.ffn_norm, dim, M->eps, B->act, B->astride);
-        gemm(W.gu, B->gu, 2 * M->ffn, 0);
+        gemm(W.gu, B->gu, 2 * M->ffn, 0, nullptr);
         hipLaunchKernelGGL(k_pf_silu_prep, dim3(P), dim3(NTE), 0, st, (const float *)B->gu, M->ffn, B->act, B->astride);
-        gemm(W.down, B->x, dim, 1);
+        gemm(W.down, B->x, dim, 1, nullptr);
     }
     CKL("prefill");
     return 0;

@@ -5,7 +5,9 @@ that fills the K/V cache; decoding then starts at the last prompt token. The log
 must meet the engine bar of test_gpu_engine.py against the oracle (the reference's token-by-token order)
 and against the GPU's own token-by-token path (L3M_PREFILL=0): equal argmax, KL < 0.01 nats, max-abs
 within 2% of max|logit| (the int8 activation noise floor of the quantized paths). Prompts of 40 and 100
-tokens cover one and two 64-token groups of the GEMM and the attention's 64-position chunks. q4_0 and
+tokens cover three and seven 16-token groups of the GEMM and one and two of the attention's 64-position
+chunks; head dims of 32 and 64 prepare the attention output inside the attention kernel, hd 48 in one of
+its own. q4_0 and
 mxfp4 bodies run the same int8 GEMM on q8_0 copies of their matrices with the same values (an mxfp4 block's
 scale 2^(e-128) is an f16 and its doubled e2m1 codes are int8).
 """
@@ -18,6 +20,8 @@ pytestmark = pytest.mark.gpu
 GQA = A.Config("pf_gqa", dim=192, n_layers=3, n_heads=6, n_kv_heads=2, ffn_dim=512, vocab=512, ctx=128, dtype="q8_0")
 MHA = A.Config("pf_mha", dim=256, n_layers=2, n_heads=4, n_kv_heads=4, ffn_dim=640, vocab=512, ctx=128, dtype="q4_0")
 MX = A.Config("pf_mx", dim=192, n_layers=2, n_heads=6, n_kv_heads=3, ffn_dim=512, vocab=512, ctx=128, dtype="mxfp4")
+# hd 48: the attention output's blocks span heads, so it is prepared by a kernel of its own
+HD48 = A.Config("pf_hd48", dim=192, n_layers=3, n_heads=4, n_kv_heads=2, ffn_dim=512, vocab=512, ctx=128, dtype="q8_0")
 
 
 def kl(lr, lf):
@@ -45,7 +49,7 @@ def close(a, b):
 
 
 @pytest.mark.parametrize("n_prompt", [40, 100])
-@pytest.mark.parametrize("cfg", [GQA, MHA, MX], ids=["q8_0-gqa", "q4_0-mha", "mxfp4-gqa"])
+@pytest.mark.parametrize("cfg", [GQA, MHA, MX, HD48], ids=["q8_0-gqa", "q4_0-mha", "mxfp4-gqa", "q8_0-hd48"])
 def test_prefill_logits(models, oracle, monkeypatch, cfg, n_prompt):
     print(f"case {cfg.name} prompt {n_prompt}", flush=True)
     path = models.get(cfg, cfg.dtype, seed=9, std=0.05, norm_jitter=0.1)
