@@ -2067,9 +2067,22 @@ __device__ __forceinline__ int keep_waiting(unsigned spin, unsigned long long t0
 }
 
 // Wavefront 0 polls flags[0..n) (n <= 64, one lane each) until every one is >= target; the result
-// reaches every thread through ok_lds. SLEEP: s_sleep between polls (64 clocks each).
-template <int SLEEP>
+// reaches every thread through ok_lds. SLEEP: s_sleep between polls (64 clocks each). ALL: every wavefront
+// polls for itself and goes on as soon as it sees the flags, with no barrier (the hand-overs inside the
+// body XCD: measured 2.4% faster decode on stories110M); a wavefront that gives up leaves, and the others
+// see the abort word at their next poll.
+template <int SLEEP, bool ALL = false>
 __device__ bool wait_flags(const unsigned *flags, int n, unsigned target, unsigned *abort_flag, unsigned long long limit, int *ok_lds) {
+    if constexpr (ALL) {
+        const int lane = tidx() & 63;
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        for (unsigned spin = 0;; spin++) {
+            const unsigned v = lane < n ? ld_flag(flags + lane) : target;
+            if (__all(v >= target)) return true;
+            if (!keep_waiting(spin, t0, abort_flag, limit)) return false;
+            __builtin_amdgcn_s_sleep(SLEEP);
+        }
+    }
     const int tid = tidx();
     if (tid < 64) {
         int ok = 1;
@@ -2277,7 +2290,7 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
             if (tok < 0) return false;
             if (g == 0 && tidx() == 0) gw(M.tokens)[pos] = tok;
         } else {
-            if (epoch > 0 && !wait_flags<1>(sync + SY_FFN, M.n_chunks, epoch, abort_flag, R.spin_limit, &ok_lds)) return false;
+            if (epoch > 0 && !wait_flags<1, true>(sync + SY_FFN, M.n_chunks, epoch, abort_flag, R.spin_limit, &ok_lds)) return false;
             if (l == 0) tok = __hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         phase(g, 1, pos, l);
@@ -2307,7 +2320,7 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
         ffn_static(wt.st, M, Lw);
         ffn_issue<DT>(wt, C);
         const unsigned epoch = (unsigned)(s * nl + l);
-        if (!wait_flags<1>(sync + SY_ATTN, M.n_groups, epoch + 1, sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
+        if (!wait_flags<1, true>(sync + SY_ATTN, M.n_groups, epoch + 1, sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
         phase(64 + ci, 1, pos, l);
         ffn_block<DT, true, G2>(M, Lw, C, ci, wt, smem, l, pos);
         set_flag<false>(sync + SY_FFN + ci, epoch + 1);
