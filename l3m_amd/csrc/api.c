@@ -418,12 +418,10 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
                 rc |= upload_step_mat(m, &Cc->gate_up, dt, 16 * tiles, d->dim, rows);
                 Cc->bup = b_up_dev ? b_up_dev + Cc->f0 : NULL;
             } else {
-                for (int t = 0; t < tiles; t++)              // gate tile t, then up tile t
-                    for (int c = 0; c < 16; c++) {
-                        int r = t * 16 + c;
-                        rows[t * 32 + c] = r < Cc->nf ? frow(f, wg, Cc->f0 + r) : NULL;
-                        rows[t * 32 + 16 + c] = r < Cc->nf ? frow(f, wu, Cc->f0 + r) : NULL;
-                    }
+                for (int r = 0; r < 16 * tiles; r++) {       // gate row r, then up row r
+                    rows[2 * r] = r < Cc->nf ? frow(f, wg, Cc->f0 + r) : NULL;
+                    rows[2 * r + 1] = r < Cc->nf ? frow(f, wu, Cc->f0 + r) : NULL;
+                }
                 rc |= upload_step_mat(m, &Cc->gate_up, dt, 32 * tiles, d->dim, rows);
             }
             for (int r = 0; r < d->dim; r++) rows[r] = col_slice(frow(f, wd, r), dt, Cc->f0);

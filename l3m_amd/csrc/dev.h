@@ -25,7 +25,7 @@ typedef struct {
 
 // One chunk of a layer's FFN block: ffn rows [f0, f0 + nf), nf a multiple of 32.
 typedef struct {
-    l3m_dmat gate_up;            // 2 * ceil16(nf) rows: gate tile t, up tile t, ... x dim
+    l3m_dmat gate_up;            // 2 * nf rows: gate row r, up row r, ... x dim (GPT-2: the up rows only)
     l3m_dmat down;               // dim rows x the chunk's nf Wdown columns
     int      f0, nf;
     unsigned lds[5];             // LDS byte offsets of the FFN block's regions (l3m_chunk_layout)

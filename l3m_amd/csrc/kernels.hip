@@ -1695,24 +1695,33 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
     __syncthreads();
     phase(64 + ci, 4, pos, layer);
-    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float, bool lead) {
-        if constexpr (G2) y += i < C.nf ? C.bup[i] : 0.f;   // the up rows only, with b_up
-        if (lead) gu[i] = y;
+    // gate row k and up row k are rows 2k and 2k + 1 (row i ^ 1 is the partner rows_sum4 hands over):
+    // the lane of gate row k forms h_k = up * silu(gate) (ops.c:49-51) there, into gu[k]
+    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float partner, bool lead) {
+        if constexpr (G2) {
+            y += i < C.nf ? C.bup[i] : 0.f;           // the up rows only, with b_up
+            if (lead) gu[i] = y;
+        } else {
+            if (lead && !(i & 1)) gu[i >> 1] = silu_mul(partner, y);
+        }
     });
     __syncthreads();
     phase(64 + ci, 5, pos, layer);
-    // h = up * silu(gate) (ops.c:49-51) for the owned 4 rows (gate tile t and up tile t interleave), prepared
+    // h of the owned 4 rows, prepared
     const int kf = kpad(C.nf);
     float4 hv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * tid < C.nf) {
-        float hh[4];
+        if constexpr (G2) {
+            float hh[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int i = 4 * tid + e, gi = (2 * (i >> 4)) * 16 + (i & 15);
-            if constexpr (G2) hh[e] = i < C.nf ? gelu_tanh(gu[i]) : 0.f;   // GELU(up) (engine.c:263-264)
-            else hh[e] = silu_mul(gu[gi + 16], gu[gi]);
+            for (int e = 0; e < 4; e++) {
+                const int i = 4 * tid + e;
+                hh[e] = i < C.nf ? gelu_tanh(gu[i]) : 0.f;   // GELU(up) (engine.c:263-264)
+            }
+            hv = make_float4(hh[0], hh[1], hh[2], hh[3]);
+        } else {
+            hv = ((const float4 *)gu)[tid];
         }
-        hv = make_float4(hh[0], hh[1], hh[2], hh[3]);
     }
     prep_owned<AT>(hv, act2, kf);
     phase(64 + ci, 6, pos, layer);
