@@ -44,6 +44,41 @@ def test_python_binding_covers_the_header():
     assert not missing
 
 
+def split_args(args):
+    """A C parameter list split at its top-level commas (a function-pointer parameter stays whole)."""
+    out, depth, cur = [], 0, ""
+    for ch in args:
+        depth += ch == "("
+        depth -= ch == ")"
+        if ch == "," and depth == 0:
+            out.append(cur.strip())
+            cur = ""
+        else:
+            cur += ch
+    if cur.strip() not in ("", "void"):
+        out.append(cur.strip())
+    return out
+
+
+def test_python_signatures_match_the_header():
+    """Each ctypes signature has the header's number of parameters, pointers where the header has
+    pointers and scalars where it has scalars (a missing parameter would turn a device pointer into a
+    32-bit int on the call)."""
+    text = re.sub(r"/\*.*?\*/", "", re.sub(r"//[^\n]*", "", HEADER.read_text()), flags=re.S)
+    decls = re.findall(r"\b(l3m_\w+)\s*\(((?:[^;{()]|\([^()]*\))*)\)\s*;", text)
+    checked, bad = 0, []
+    for name, args in decls:
+        if name not in A._SIG:
+            continue
+        params, (_, codes) = split_args(args), A._SIG[name]
+        kinds = ["p" if "*" in a or "(" in a else "s" for a in params]
+        want = ["s" if c in (C.c_int, C.c_int32, C.c_uint16, C.c_uint64, C.c_size_t, C.c_float, C.c_double) else "p" for c in codes]
+        checked += 1
+        if kinds != want:
+            bad.append((name, params, want))
+    assert checked > 50 and not bad, bad
+
+
 def test_model_api_matches_the_reference_struct_layouts():
     """l3m_opts and l3m_perf have the reference's field order and sizes (src/l3m.h:10-29)."""
     assert [f[0] for f in A.Opts._fields_] == ["cpus", "n_cpus", "ctx", "reference", "force", "verbose", "cold"]
