@@ -896,10 +896,13 @@ struct ProGeom {
 };
 // groups = NTE / n4 (at least 1), per = ceil(nparts / groups) (at least 1): computed on the host
 // (l3m_model_layout) so that no workgroup divides by them at run time.
+// As many groups of dim / 4 threads as the workgroup holds, each summing per parts, and no group more than
+// the parts need (a group past the last part would only load copies of it).
 __host__ __device__ inline void pro_shape(int dim, int nparts, int &groups, int &per) {
     groups = NTE / (dim >> 2) < 1 ? 1 : NTE / (dim >> 2);
     per = (nparts + groups - 1) / groups;
     if (per < 1) per = 1;
+    groups = nparts > 0 ? (nparts + per - 1) / per : 1;
 }
 // which 0: over the n_chunks FFN partials (attention and head prologues), 1: over the n_groups ones.
 __device__ __forceinline__ ProGeom pro_geom(const l3m_dmodel &M, int which) {
