@@ -790,18 +790,20 @@ __device__ void block_argmax(float &v, int &i, float *sv, int *si) {
 }
 
 // Matvec results res[pair * 16 + row] summed per row: four quarter sums of the blocks, each in block
-// order, added pairwise ((q0 + q1) + (q2 + q3)). Rows of more than 4 blocks take 4 adjacent lanes (one
-// quarter each); shorter rows one lane (all four quarters), which gives the same sums in a quarter of the
-// passes. f(i, y, partner, lead) runs in every lane for rows i < rows, partner being row i ^ 1's value
-// and lead true in one lane per row.
+// order, added pairwise ((q0 + q1) + (q2 + q3)). Rows of more than 4 blocks take 4 lanes, one per quarter:
+// a wavefront takes the 16 rows of one tile, row r in lanes r, r + 16, r + 32, r + 48, and quarter q
+// holds blocks q, q + 4, q + 8, ..., so the 32 lanes the LDS serves at once (quarters q and q + 1) read
+// 32 different banks (block b lies 16 b floats into the tile). Rows of at most 4 blocks take one lane
+// (all four quarters: block q, if any), which gives the same sums in a quarter of the passes.
+// f(i, y, partner, lead) runs in every lane for rows i < rows, partner being row i ^ 1's value and lead
+// true in one lane per row.
 template <class F>
 __device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, int rows, F f) {
     const int nb = m.nb;
     // Reads are unconditional (row and block clamped into range) and issued together; the sums then take
     // only the values in range, in block order.
     if (nb <= 4) {
-        // each quarter holds at most one block: quarter q has block (q * nb) / 4 when that is below
-        // ((q + 1) * nb) / 4
+        // each quarter holds at most one block: quarter q has block q when q < nb
         for (int base = 0; base < rows; base += NTE) {
             const int i = base + tidx(), ic = i < rows ? i : rows - 1;
             const float *p = res + (size_t)(ic >> 4) * nb * 16 + (ic & 15);
@@ -810,28 +812,29 @@ __device__ __forceinline__ void rows_sum4(const l3m_dmat &m, const float *res, i
             for (int b = 0; b < 4; b++) v[b] = p[(b < nb ? b : nb - 1) * 16];
             float s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int lo = q * nb >> 2, hi = (q + 1) * nb >> 2;
-                const float vq = lo == 0 ? v[0] : lo == 1 ? v[1] : lo == 2 ? v[2] : v[3];
-                if (i < rows && lo < hi) s[q] += vq;
-            }
+            for (int q = 0; q < 4; q++)
+                if (i < rows && q < nb) s[q] += v[q];
             const float y = (s[0] + s[1]) + (s[2] + s[3]);
             const float partner = dppf<QP_X1>(y);     // row i ^ 1 is the neighbouring lane
             if (i < rows) f(i, y, partner, true);
         }
         return;
     }
-    const int q = tidx() & 3, b0 = q * nb >> 2, b1 = (q + 1) * nb >> 2;
+    const int lane = tidx() & 63, q = lane >> 4;
     for (int base = 0; base < rows; base += NTE / 4) {
-        const int i = base + (tidx() >> 2);
+        const int i = base + 16 * wave_id() + (lane & 15);
         float y = 0.f;
         if (i < rows) {
             const float *p = res + (size_t)(i >> 4) * nb * 16 + (i & 15);
 #pragma unroll 4
-            for (int b = b0; b < b1; b++) y += p[b * 16];
+            for (int b = q; b < nb; b += 4) y += p[b * 16];
         }
-        y = lanes_sum<4>(y);
-        const float partner = dppf<ROW_HALF_MIRROR>(y);
+        float lo, hi;
+        swap16(y, lo, hi);                            // q0 + q1, q2 + q3
+        y = lo + hi;
+        swap32(y, lo, hi);                            // (q0 + q1) + (q2 + q3), in all four lanes
+        y = lo + hi;
+        const float partner = dppf<QP_X1>(y);        // row i ^ 1 is the neighbouring lane
         if (i < rows) f(i, y, partner, q == 0);
     }
 }
