@@ -673,13 +673,15 @@ __device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m
     }
     // a wavefront stops at its first slot past the end (a scalar branch); in its last slot the up to 3
     // pairs past the end (loads repeat the last pair) write into the padding of res (res_bytes)
+    float *rp = res + wave * 64 + lane;              // res[p0 * 16 + lane] = rp[slot * NWE * 64]
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         const int p0 = (wave + (s0 + s) * NWE) * 4;
         if (p0 >= n) break;
-        res[p0 * 16 + lane] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b);
-        b += step;                                    // step < nb
-        b -= b >= nb ? nb : 0;
+        rp[(s0 + s) * NWE * 64] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b);
+        // b + step - nb when that is not negative, else b + step (step < nb): one unsigned minimum
+        const unsigned t = (unsigned)b + (unsigned)step;
+        b = (int)__builtin_elementwise_min(t, t - (unsigned)nb);
     }
 }
 
