@@ -663,6 +663,7 @@ __device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m
     const int x0 = (tidx() >> 4) + 4 * NWE * s0;      // the lane's pair in slot 0
     int b = x0 - (int)(((float)x0 + 0.5f) * inb) * nb;
     const int step = __builtin_amdgcn_readfirstlane(4 * NWE - (int)(((float)(4 * NWE) + 0.5f) * inb) * nb);
+    const unsigned stepm = (unsigned)__builtin_amdgcn_readfirstlane(step - nb);
     // Pin the loaded registers here: otherwise the compiler hoists their first use (the f16 scale
     // conversion) up to the loads, and every wavefront stalls on its first load at entry.
 #pragma unroll
@@ -680,8 +681,7 @@ __device__ __forceinline__ void pref_compute(Pref<DT, NS> &pf, const l3m_dmat &m
         if (p0 >= n) break;
         rp[(s0 + s) * NWE * 64] = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b);
         // b + step - nb when that is not negative, else b + step (step < nb): one unsigned minimum
-        const unsigned t = (unsigned)b + (unsigned)step;
-        b = (int)__builtin_elementwise_min(t, t - (unsigned)nb);
+        b = (int)__builtin_elementwise_min((unsigned)b + (unsigned)step, (unsigned)b + stepm);
     }
 }
 
@@ -755,6 +755,57 @@ __device__ __forceinline__ float strided_sum(float v, int n) {
     if (n <= 16) { swap16(v, lo, hi); v = lo + hi; }
     swap32(v, lo, hi);
     return lo + hi;
+}
+
+// A matrix of nb = 1, 2 or 4 blocks per row, its rows summed where the slots computed them: a slot's 4
+// pairs are then whole rows of 16 (nb 4: the 4 blocks of one tile; nb 2: two tiles; nb 1: four), so the
+// quarter sums of rows_sum4 meet in registers (permlane swaps, the same values added in the same order)
+// and f(i, y, lead) takes each row from the slot that computed it, with no LDS round trip or barrier.
+template <int DT, int NS, class F>
+__device__ __forceinline__ void slots_rows(Pref<DT, NS> &pf, const l3m_dmat &m, int s0, const uint8_t *act, int kp, int rows, F f) {
+    const int wave = wave_id(), lane = tidx() & 63, nb = m.nb, n = m.tiles * nb, sub = lane >> 4, row = lane & 15;
+    const int b = sub & (nb - 1), sh = nb >> 1 == 2 ? 2 : nb >> 1;   // the lane's block, log2(nb)
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        asm volatile("" : "+v"(pf.sc[s]));
+#pragma unroll
+        for (int v = 0; v < qbytes(DT) / 16; v++) asm volatile("" : "+v"(pf.w[s][v].x), "+v"(pf.w[s][v].y), "+v"(pf.w[s][v].z), "+v"(pf.w[s][v].w));
+    }
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int p0 = (wave + (s0 + s) * NWE) * 4;
+        if (p0 >= n) break;
+        // rows_sum4 for nb <= 4: quarter q = 0.f + block q (when q < nb), then (q0 + q1) + (q2 + q3)
+        const float v = 0.f + block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b);
+        float lo, hi, y;
+        if (nb == 4) {
+            swap16(v, lo, hi);
+            y = lo + hi;
+            swap32(y, lo, hi);
+            y = lo + hi;
+        } else if (nb == 2) {
+            swap16(v, lo, hi);
+            y = (lo + hi) + (0.f + 0.f);
+        } else {
+            y = (v + 0.f) + (0.f + 0.f);
+        }
+        const int i = ((p0 + sub) >> sh) * 16 + row;   // pairs past the end give i >= rows
+        if (i < rows) f(i, y, b == 0);
+    }
+}
+template <int DT, int NS, class F>
+__device__ __forceinline__ void mv_rows(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int kp, float *res, int rows, F f) {
+    if (m.nb == 1 || m.nb == 2 || m.nb == 4) {
+        slots_rows<DT, NS>(pf, m, 0, act, kp, rows, f);
+        for (int s0 = NS; s0 * NWE * 4 < m.tiles * m.nb; s0 += NS) {
+            pref_load<DT, NS>(pf, m, s0);
+            slots_rows<DT, NS>(pf, m, s0, act, kp, rows, f);
+        }
+        return;
+    }
+    mv<DT, NS>(pf, m, act, kp, res);
+    __syncthreads();
+    rows_sum4(m, res, rows, [&](int i, float y, float, bool lead) { f(i, y, lead); });
 }
 
 // Scratch for workgroup reductions (norm_prep): the wavefront results go to one of two 16-float slots of
@@ -1667,14 +1718,21 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
     prep_owned<AT>(4 * tid < nqd ? ((const float4 *)att)[tid] : make_float4(0.f, 0.f, 0.f, 0.f), act2, kq);
     phase(gi, 7, pos, layer);
-    mv<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
-    __syncthreads();
-    phase(gi, 8, pos, layer);
     float *po = M.po + (size_t)gi * dim;
-    rows_sum4(G.wo, work, dim, [&](int i, float y, float, bool lead) {
-        if constexpr (G2) y += gi == 0 ? Lw.bo[i] : 0.f;   // bo once, with group 0's partial
-        if (lead) gw(po)[i] = y;
-    });
+    if constexpr (G2) {
+        mv<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, act2, kq, work);
+        __syncthreads();
+        phase(gi, 8, pos, layer);
+        rows_sum4(G.wo, work, dim, [&](int i, float y, float, bool lead) {
+            y += gi == 0 ? Lw.bo[i] : 0.f;            // bo once, with group 0's partial
+            if (lead) gw(po)[i] = y;
+        });
+    } else {
+        mv_rows<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, act2, kq, work, dim, [&](int i, float y, bool lead) {
+            if (lead) gw(po)[i] = y;
+        });
+        phase(gi, 8, pos, layer);
+    }
     phase(gi, 9, pos, layer);
 }
 
@@ -1733,14 +1791,21 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     }
     prep_owned<AT>(hv, act2, kf);
     phase(64 + ci, 6, pos, layer);
-    mv<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, act2, kf, work);
-    __syncthreads();
-    phase(64 + ci, 7, pos, layer);
     float *pd = M.pd + (size_t)ci * dim;
-    rows_sum4(C.down, work, dim, [&](int i, float y, float, bool lead) {
-        if constexpr (G2) y += ci == 0 ? Lw.bdown[i] : 0.f;   // b_down once, with chunk 0's partial
-        if (lead) gw(pd)[i] = y;
-    });
+    if constexpr (G2) {
+        mv<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, act2, kf, work);
+        __syncthreads();
+        phase(64 + ci, 7, pos, layer);
+        rows_sum4(C.down, work, dim, [&](int i, float y, float, bool lead) {
+            y += ci == 0 ? Lw.bdown[i] : 0.f;         // b_down once, with chunk 0's partial
+            if (lead) gw(pd)[i] = y;
+        });
+    } else {
+        mv_rows<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, act2, kf, work, dim, [&](int i, float y, bool lead) {
+            if (lead) gw(pd)[i] = y;
+        });
+        phase(64 + ci, 7, pos, layer);
+    }
     phase(64 + ci, 8, pos, layer);
 }
 
