@@ -653,6 +653,26 @@ __device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, i
     }
 }
 
+// The tile form of a matrix: wavefront w takes tiles w, w + NWE, ... in turn, each in slots of 4 blocks
+// of its 16 rows (lane quarter sub = lane / 16 takes blocks sub, sub + 4, ...), NS slots per batch.
+// pref_load_tile loads slots j0 .. j0 + NS - 1 of tile t: 4 consecutive pairs per slot, as pref_load;
+// blocks past nb and tiles past the end load the last valid pair (not used).
+template <int DT, int NS>
+__device__ __forceinline__ void pref_load_tile(Pref<DT, NS> &pf, const l3m_dmat &m, int t, int j0) {
+    constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
+    const int sub = (tidx() >> 4) & 3, row = tidx() & 15, nb = m.nb, tc = t < m.tiles ? t : m.tiles - 1;
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int b = 4 * (j0 + s) + sub;
+        const size_t slot = ((size_t)tc * nb + (b < nb ? b : nb - 1)) * 16 + row;
+#pragma unroll
+        for (int v = 0; v < NV; v++) pf.w[s][v] = ldg16(m.q, slot * NV + v);
+        if constexpr (SBY == 2) pf.sc[s] = gp<uint16_t>(m.s)[slot];
+        if constexpr (SBY == 1) pf.sc[s] = gp<uint8_t>(m.s)[slot];
+        if constexpr (SBY == 0) pf.sc[s] = 0;
+    }
+}
+
 // res[pair * 16 + row] for this lane's slots. The lane's pair advances by 4 * NWE from slot to slot, so
 // its block (pair % nb) advances by (4 * NWE) % nb, with one wrap.
 template <int DT, int NS>
@@ -755,6 +775,59 @@ __device__ __forceinline__ float strided_sum(float v, int n) {
     if (n <= 16) { swap16(v, lo, hi); v = lo + hi; }
     swap32(v, lo, hi);
     return lo + hi;
+}
+
+// The matvec of m in the tile form (the first batch of the wavefront's first tile loaded by
+// pref_load_tile beforehand): lane (sub, row) adds its blocks sub, sub + 4, ... as they come out of its
+// slots, the four quarter sums meet by permlane swaps, and f(i, y, partner, lead) runs for the tile's 16
+// rows: the values and order of additions of mv and rows_sum4, with no LDS round trip or barrier.
+template <int DT, int NS, class F>
+__device__ __forceinline__ void tile_rows(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int kp, int rows, F f) {
+    const int wave = wave_id(), lane = tidx() & 63, sub = lane >> 4, row = lane & 15, nb = m.nb, spt = (nb + 3) >> 2;
+    float y = 0.f;
+    auto batch = [&](int j0) {
+        // pin the loaded registers here, as pref_compute does
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            asm volatile("" : "+v"(pf.sc[s]));
+#pragma unroll
+            for (int v = 0; v < qbytes(DT) / 16; v++)
+                asm volatile("" : "+v"(pf.w[s][v].x), "+v"(pf.w[s][v].y), "+v"(pf.w[s][v].z), "+v"(pf.w[s][v].w));
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            if (j0 + s >= spt) break;
+            const int b = 4 * (j0 + s) + sub;
+            const float v = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b < nb ? b : nb - 1);
+            if (b < nb) y += v;
+        }
+    };
+    auto finish = [&](int t) {
+        float lo, hi;
+        swap16(y, lo, hi);                            // q0 + q1, q2 + q3
+        y = lo + hi;
+        swap32(y, lo, hi);                            // (q0 + q1) + (q2 + q3), in all four lanes
+        y = lo + hi;
+        const float partner = dppf<QP_X1>(y);        // row i ^ 1 is the neighbouring lane
+        const int i = t * 16 + row;
+        if (i < rows) f(i, y, partner, sub == 0);
+        y = 0.f;
+    };
+    if (wave < m.tiles) {
+        batch(0);
+        for (int j0 = NS; j0 < spt; j0 += NS) {
+            pref_load_tile<DT, NS>(pf, m, wave, j0);
+            batch(j0);
+        }
+        finish(wave);
+        for (int t = wave + NWE; t < m.tiles; t += NWE) {
+            for (int j0 = 0; j0 < spt; j0 += NS) {
+                pref_load_tile<DT, NS>(pf, m, t, j0);
+                batch(j0);
+            }
+            finish(t);
+        }
+    }
 }
 
 // A matrix of nb = 1, 2 or 4 blocks per row, its rows summed where the slots computed them: a slot's 4
@@ -1605,16 +1678,34 @@ __device__ __forceinline__ void ffn_static(ProStatic &st, const l3m_dmodel &M, c
     pro_static(st, M.dim >> 2, Lw.ffn_norm, nullptr, 0);
 }
 
+// The wide matrices (q/k/v rows, gate/up rows, the head) take the tile form (tile_rows) in the quantized
+// dtypes, whose slots hold a whole row of the benchmark shapes (up to 20-24 blocks); bf16 and f32 slots
+// hold 2-3 times fewer blocks, and those take mv and rows_sum4.
+template <int DT> constexpr bool tiled() { return quantized(DT); }
+template <int DT, int NS> __device__ __forceinline__ void wide_issue(Pref<DT, NS> &pf, const l3m_dmat &m) {
+    if constexpr (tiled<DT>()) pref_load_tile<DT, NS>(pf, m, wave_id(), 0);
+    else pref_load<DT, NS>(pf, m, 0);
+}
+template <int DT, int NS, class F>
+__device__ __forceinline__ void wide_rows(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int kp, float *res, int rows, F f) {
+    if constexpr (tiled<DT>()) {
+        tile_rows<DT, NS>(pf, m, act, kp, rows, f);
+    } else {
+        mv<DT, NS>(pf, m, act, kp, res);
+        __syncthreads();
+        rows_sum4(m, res, rows, f);
+    }
+}
 template <int DT> __device__ __forceinline__ void attn_issue(AttnW<DT> &w, const l3m_dgroup &G) {
-    pref_load<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, 0);
+    wide_issue<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv);
     pref_load<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, 0);
 }
 template <int DT> __device__ __forceinline__ void ffn_issue(FfnW<DT> &w, const l3m_dchunk &C) {
-    pref_load<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, 0);
+    wide_issue<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up);
     pref_load<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, 0);
 }
 template <int DT> __device__ __forceinline__ void head_issue(HeadW<DT> &w, const l3m_dmat &V) {
-    pref_load<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, 0);
+    wide_issue<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V);
 }
 
 // The persistent path's K/V window copy for the attention block of group G at (layer, pos): rows
@@ -1662,9 +1753,6 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     else norm_prep<AT>(x, w.st.nw, dim, kp, M.eps, act, red);
     phase(gi, 3, pos, layer);
 
-    mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, act, kp, work);
-    __syncthreads();
-    phase(gi, 4, pos, layer);
     // q, k rows: RoPE on pairs (2i, 2i+1) of each head by the angle i (ops.c:29-40); k, v rows rounded
     // to bf16 as the cache holds them (engine.c:247-248), into cur, row pos of the LDS window and, for the
     // heads this group writes, the cache
@@ -1673,7 +1761,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // the matrix-core attention (LDS window, hd a multiple of 16, q parts fit beside vred's 2 NWE sums)
     const bool mfma_att = M.kv_lds && mfma_fits(hd, G.nq, M.ctx);
     __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
-    rows_sum4(G.qkv, work, nqd + 2 * nkd, [&](int i, float y, float partner, bool lead) {
+    auto qkv_row = [&](int i, float y, float partner, bool lead) {
         if constexpr (G2) y += G.bqkv[i];            // the GPT-2 variant's q, k, v biases; no RoPE
         if (!G2 && i < nqd + nkd) {
             const int local = i < nqd ? i : i - nqd, head = (int)(((float)local + 0.5f) * inv_hd);
@@ -1694,7 +1782,9 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
                     kvb[((size_t)(kv * G.nkv + kvl) * M.ctx + pos) * kv_row(hd) + (jj - kvl * hd)] = hb;
             }
         }
-    });
+    };
+    wide_rows<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, act, kp, work, nqd + 2 * nkd, qkv_row);
+    phase(gi, 4, pos, layer);
     // the window's copy (issued long before) is complete; this step's rows go to the cache after the
     // attention, so their store acknowledgements stay off the path to it
     if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1758,19 +1848,18 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     if constexpr (G2) ln_prep<AT>(x, Lw.ffn_norm, Lw.ffn_norm_b, dim, kp, M.eps, act, red);
     else norm_prep<AT>(x, w.st.nw, dim, kp, M.eps, act, red);
     phase(64 + ci, 3, pos, layer);
-    mv<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, act, kp, work);
-    __syncthreads();
-    phase(64 + ci, 4, pos, layer);
     // gate row k and up row k are rows 2k and 2k + 1 (row i ^ 1 is the partner rows_sum4 hands over):
     // the lane of gate row k forms h_k = up * silu(gate) (ops.c:49-51) there, into gu[k]
-    rows_sum4(C.gate_up, work, C.gate_up.rows, [&](int i, float y, float partner, bool lead) {
+    auto gu_row = [&](int i, float y, float partner, bool lead) {
         if constexpr (G2) {
             y += i < C.nf ? C.bup[i] : 0.f;           // the up rows only, with b_up
             if (lead) gu[i] = y;
         } else {
             if (lead && !(i & 1)) gu[i >> 1] = silu_mul(partner, y);
         }
-    });
+    };
+    wide_rows<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, act, kp, work, C.gate_up.rows, gu_row);
+    phase(64 + ci, 4, pos, layer);
     __syncthreads();
     phase(64 + ci, 5, pos, layer);
     // h of the owned 4 rows, prepared
@@ -1848,19 +1937,18 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
     }
     if constexpr (G2) ln_prep<DT>(x, M.norm, M.norm_b, dim, kp, M.eps, act, red);
     else norm_prep<DT>(x, w.st.nw, dim, kp, M.eps, act, red);
-    mv<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work);
-    __syncthreads();
     // each row's logit from the lane that sums it: stored, and kept if it beats the lane's earlier rows
     float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab + (size_t)t0 * 16;
     v = -INFINITY;
     idx = 0x7FFFFFFF;
-    rows_sum4(V, work, V.rows, [&](int i, float yy, float, bool lead) {
+    auto logit_row = [&](int i, float yy, float, bool lead) {
         if (lead) {
             gw(lg)[i] = yy;
             if (keep) keep[i] = yy;                   // kept in LDS for sampling
             better(v, idx, yy, t0 * 16 + i);
         }
-    });
+    };
+    wide_rows<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work, V.rows, logit_row);
     block_argmax(v, idx, scr, (int *)scr + 16);
 }
 
