@@ -621,6 +621,12 @@ template <int DT> constexpr int nslot_a() { return DT == L3M_F32 ? 1 : DT == L3M
 template <int DT> constexpr int nslot_b() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 1 : 3; }
 // The attention block keeps its Wo slots live through the attention; q8_0 gives one up to stay in registers.
 template <int DT> constexpr int nslot_wo() { return DT == L3M_Q8_0 || DT == L3M_Q4_0 ? 2 : nslot_b<DT>(); }
+// The wide matrices (q/k/v rows, gate/up rows, the head) take the tile form (tile_rows) in the quantized
+// dtypes, whose slot batch holds a whole row of the benchmark shapes (up to 24 blocks); bf16 and f32 take
+// mv and rows_sum4 (bf16 in the tile form, with a third slot, measured 3% slower on stories15M). The
+// head's slots: one row's in the tile form.
+template <int DT> constexpr bool tiled() { return quantized(DT); }
+template <int DT> constexpr int nslot_h() { return tiled<DT>() ? nslot_a<DT>() : nslot_a<DT>() + nslot_b<DT>(); }
 
 template <int DT, int NS>
 struct Pref {
@@ -1668,7 +1674,7 @@ template <int DT> constexpr int a_dtype() { return DT == L3M_Q4_0 ? L3M_Q8_0 : D
 #endif
 template <int DT> struct AttnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_wo<DT>()> b; ProStatic st; };
 template <int DT> struct FfnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_b<DT>()> b; ProStatic st; };
-template <int DT> struct HeadW { Pref<DT, nslot_a<DT>() + nslot_b<DT>()> a; ProStatic st; };
+template <int DT> struct HeadW { Pref<DT, nslot_h<DT>()> a; ProStatic st; };
 
 // A block's static prologue inputs (ProStatic), issued ahead of its weights.
 __device__ __forceinline__ void attn_static(ProStatic &st, const l3m_dmodel &M, const l3m_dlayer &Lw, int pos) {
@@ -1678,10 +1684,6 @@ __device__ __forceinline__ void ffn_static(ProStatic &st, const l3m_dmodel &M, c
     pro_static(st, M.dim >> 2, Lw.ffn_norm, nullptr, 0);
 }
 
-// The wide matrices (q/k/v rows, gate/up rows, the head) take the tile form (tile_rows) in the quantized
-// dtypes, whose slots hold a whole row of the benchmark shapes (up to 20-24 blocks); bf16 and f32 slots
-// hold 2-3 times fewer blocks, and those take mv and rows_sum4.
-template <int DT> constexpr bool tiled() { return quantized(DT); }
 template <int DT, int NS> __device__ __forceinline__ void wide_issue(Pref<DT, NS> &pf, const l3m_dmat &m) {
     if constexpr (tiled<DT>()) pref_load_tile<DT, NS>(pf, m, wave_id(), 0);
     else pref_load<DT, NS>(pf, m, 0);
@@ -1705,7 +1707,7 @@ template <int DT> __device__ __forceinline__ void ffn_issue(FfnW<DT> &w, const l
     pref_load<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, 0);
 }
 template <int DT> __device__ __forceinline__ void head_issue(HeadW<DT> &w, const l3m_dmat &V) {
-    wide_issue<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V);
+    wide_issue<DT, nslot_h<DT>()>(w.a, V);
 }
 
 // The persistent path's K/V window copy for the attention block of group G at (layer, pos): rows
@@ -1948,7 +1950,7 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
             better(v, idx, yy, t0 * 16 + i);
         }
     };
-    wide_rows<DT, nslot_a<DT>() + nslot_b<DT>()>(w.a, V, act, kp, work, V.rows, logit_row);
+    wide_rows<DT, nslot_h<DT>()>(w.a, V, act, kp, work, V.rows, logit_row);
     block_argmax(v, idx, scr, (int *)scr + 16);
 }
 
