@@ -26,6 +26,9 @@ __host__ __device__ constexpr int qbytes(int dt) { return dt == L3M_F32 ? 128 : 
 __host__ __device__ constexpr int sbytes(int dt) { return dt == L3M_Q8_0 || dt == L3M_Q4_0 ? 2 : dt == L3M_MXFP4 ? 1 : 0; }
 __host__ __device__ constexpr bool quantized(int dt) { return dt >= L3M_Q8_0; }
 __host__ __device__ inline int kpad(int k) { return (k + 31) & ~31; }
+// The prepared input of the wide matrices (q/k/v, gate/up, head) is padded to whole slots of 4 blocks with
+// zero values, scales and sums, so the tile form reads the 4 blocks of every slot unconditionally.
+__host__ __device__ inline int kwide(int k) { return (k + 127) & ~127; }
 // A prepared activation (l3m_vec_prepare's values, pack.c:101-123) in the form the matvec of a dtype reads:
 //   q8_0   per 32-block the 32 int8 values q
 //   q4_0   per 32-block 16 bytes of high nibbles h = q >> 4 and 16 of low nibbles l = q & 15, dword k of each
@@ -268,52 +271,15 @@ __device__ void prep_act(uint8_t *act, const float *xs, int kp) {
 
 // One row-block: acc += (x.scale[b] * d) * (integer dot - offset * x.sum[b]) for the quantized dtypes
 // (kernels_scalar.c:30-75), or the bf16 / f32 dot (kernels_scalar.c:9-28).
+// The quantized dtypes from the block's own pointers: xq its values, xsp its scale, xsum its sum.
+template <int DT>
+__device__ __forceinline__ float block_fma_at(float acc, const uint4 *w, uint32_t sc, const uint8_t *xq, const float *xsp, const int *xsum);
 template <int DT>
 __device__ __forceinline__ float block_fma(float acc, const uint4 *w, uint32_t sc, const uint8_t *act, int kp, int b) {
     if constexpr (quantized(DT)) {
         const int nb = kp >> 5;
-        const float xs = ((const float *)(act + act_qbytes(DT) * nb))[b];
-        if constexpr (DT == L3M_Q8_0) {
-            const int4 *xv = (const int4 *)(act + b * 32);
-            const int4 x0 = xv[0], x1 = xv[1];
-            int dot = 0;
-            dot = dot4(w[0].x, x0.x, dot); dot = dot4(w[0].y, x0.y, dot);
-            dot = dot4(w[0].z, x0.z, dot); dot = dot4(w[0].w, x0.w, dot);
-            dot = dot4(w[1].x, x1.x, dot); dot = dot4(w[1].y, x1.y, dot);
-            dot = dot4(w[1].z, x1.z, dot); dot = dot4(w[1].w, x1.w, dot);
-            return fmaf(xs * f16_f32(sc), (float)dot, acc);
-        } else if constexpr (DT == L3M_Q4_0) {
-            // sum (n - 8) q over the block with q = 16 h + l: 16 * sum (n - 8) h (signed 4-bit dots, the
-            // codes' top bits flipped make n - 8) + sum n l (unsigned 4-bit dots) - 8 * sum l
-            const uint4 *xv = (const uint4 *)(act + b * 32);
-            const uint4 h = xv[0], l = xv[1];
-            const int lsum = ((const int *)(act + 32 * nb + 4 * nb))[b];
-            int dh = 0, dl = 0;
-            dh = __builtin_amdgcn_sdot8((int)(w[0].x ^ 0x88888888u), (int)h.x, dh, false);
-            dh = __builtin_amdgcn_sdot8((int)(w[0].y ^ 0x88888888u), (int)h.y, dh, false);
-            dh = __builtin_amdgcn_sdot8((int)(w[0].z ^ 0x88888888u), (int)h.z, dh, false);
-            dh = __builtin_amdgcn_sdot8((int)(w[0].w ^ 0x88888888u), (int)h.w, dh, false);
-            dl = (int)__builtin_amdgcn_udot8(w[0].x, l.x, (unsigned)dl, false);
-            dl = (int)__builtin_amdgcn_udot8(w[0].y, l.y, (unsigned)dl, false);
-            dl = (int)__builtin_amdgcn_udot8(w[0].z, l.z, (unsigned)dl, false);
-            dl = (int)__builtin_amdgcn_udot8(w[0].w, l.w, (unsigned)dl, false);
-            return fmaf(xs * f16_f32(sc), (float)(16 * dh + dl - 8 * lsum), acc);
-        } else {
-            // each code byte's two e2m1 values, doubled, as f16 (exact), dotted with the (q[j], q[j + 16])
-            // pairs in f32: every partial sum is an integer below 2^24, so the dot is exact
-            const uint4 *xv = (const uint4 *)(act + b * 64);
-            float dot = 0.f;
-            const uint32_t v[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint4 x = xv[j];
-                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 0), x.x, dot);
-                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 1), x.y, dot);
-                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 2), x.z, dot);
-                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 3), x.w, dot);
-            }
-            return fmaf(xs * e8m0_half(sc), dot, acc);
-        }
+        return block_fma_at<DT>(acc, w, sc, act + (size_t)act_qbytes(DT) * b, (const float *)(act + act_qbytes(DT) * nb) + b,
+                                (const int *)(act + act_qbytes(DT) * nb + 4 * nb) + b);
     } else if constexpr (DT == L3M_BF16) {
         const uint4 *xv = (const uint4 *)(act + b * 64);
 #pragma unroll
@@ -332,6 +298,54 @@ __device__ __forceinline__ float block_fma(float acc, const uint4 *w, uint32_t s
             acc = fmaf(__uint_as_float(w[v].z), x.z, acc); acc = fmaf(__uint_as_float(w[v].w), x.w, acc);
         }
         return acc;
+    }
+}
+template <int DT>
+__device__ __forceinline__ float block_fma_at(float acc, const uint4 *w, uint32_t sc, const uint8_t *xq, const float *xsp, const int *xsum) {
+    static_assert(quantized(DT), "block_fma_at: quantized dtypes");
+    {
+        const float xs = *xsp;
+        if constexpr (DT == L3M_Q8_0) {
+            const int4 *xv = (const int4 *)xq;
+            const int4 x0 = xv[0], x1 = xv[1];
+            int dot = 0;
+            dot = dot4(w[0].x, x0.x, dot); dot = dot4(w[0].y, x0.y, dot);
+            dot = dot4(w[0].z, x0.z, dot); dot = dot4(w[0].w, x0.w, dot);
+            dot = dot4(w[1].x, x1.x, dot); dot = dot4(w[1].y, x1.y, dot);
+            dot = dot4(w[1].z, x1.z, dot); dot = dot4(w[1].w, x1.w, dot);
+            return fmaf(xs * f16_f32(sc), (float)dot, acc);
+        } else if constexpr (DT == L3M_Q4_0) {
+            // sum (n - 8) q over the block with q = 16 h + l: 16 * sum (n - 8) h (signed 4-bit dots, the
+            // codes' top bits flipped make n - 8) + sum n l (unsigned 4-bit dots) - 8 * sum l
+            const uint4 *xv = (const uint4 *)xq;
+            const uint4 h = xv[0], l = xv[1];
+            const int lsum = *xsum;
+            int dh = 0, dl = 0;
+            dh = __builtin_amdgcn_sdot8((int)(w[0].x ^ 0x88888888u), (int)h.x, dh, false);
+            dh = __builtin_amdgcn_sdot8((int)(w[0].y ^ 0x88888888u), (int)h.y, dh, false);
+            dh = __builtin_amdgcn_sdot8((int)(w[0].z ^ 0x88888888u), (int)h.z, dh, false);
+            dh = __builtin_amdgcn_sdot8((int)(w[0].w ^ 0x88888888u), (int)h.w, dh, false);
+            dl = (int)__builtin_amdgcn_udot8(w[0].x, l.x, (unsigned)dl, false);
+            dl = (int)__builtin_amdgcn_udot8(w[0].y, l.y, (unsigned)dl, false);
+            dl = (int)__builtin_amdgcn_udot8(w[0].z, l.z, (unsigned)dl, false);
+            dl = (int)__builtin_amdgcn_udot8(w[0].w, l.w, (unsigned)dl, false);
+            return fmaf(xs * f16_f32(sc), (float)(16 * dh + dl - 8 * lsum), acc);
+        } else {
+            // each code byte's two e2m1 values, doubled, as f16 (exact), dotted with the (q[j], q[j + 16])
+            // pairs in f32: every partial sum is an integer below 2^24, so the dot is exact
+            const uint4 *xv = (const uint4 *)xq;
+            float dot = 0.f;
+            const uint32_t v[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint4 x = xv[j];
+                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 0), x.x, dot);
+                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 1), x.y, dot);
+                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 2), x.z, dot);
+                dot = fdot2h(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v[j], 2.0f, 3), x.w, dot);
+            }
+            return fmaf(xs * e8m0_half(sc), dot, acc);
+        }
     }
 }
 
@@ -784,12 +798,20 @@ __device__ __forceinline__ float strided_sum(float v, int n) {
 }
 
 // The matvec of m in the tile form (the first batch of the wavefront's first tile loaded by
-// pref_load_tile beforehand): lane (sub, row) adds its blocks sub, sub + 4, ... as they come out of its
-// slots, the four quarter sums meet by permlane swaps, and f(i, y, partner, lead) runs for the tile's 16
-// rows: the values and order of additions of mv and rows_sum4, with no LDS round trip or barrier.
+// pref_load_tile beforehand): lane (sub, row) accumulates its blocks sub, sub + 4, ... in block order as
+// they come out of its slots (block_fma's fma into the running sum), the four quarter sums meet by
+// permlane swaps ((q0 + q1) + (q2 + q3)), and f(i, y, partner, lead) runs for the tile's 16 rows, with
+// no LDS round trip or barrier. The block offsets are constants per slot (no index arithmetic).
 template <int DT, int NS, class F>
 __device__ __forceinline__ void tile_rows(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int kp, int rows, F f) {
     const int wave = wave_id(), lane = tidx() & 63, sub = lane >> 4, row = lane & 15, nb = m.nb, spt = (nb + 3) >> 2;
+    constexpr int QB = act_qbytes(DT);
+    // the lane's block sub (values, scale, sum) of act's na blocks (kp = kwide(k): whole slots, the blocks
+    // past nb zero with scale 0); slot s adds 4 s blocks, a constant offset
+    const int na = kp >> 5;
+    const uint8_t *xq = act + QB * sub;
+    const float *xsp = (const float *)(act + QB * na) + sub;
+    const int *xsum = (const int *)(act + QB * na + 4 * na) + sub;
     float y = 0.f;
     auto batch = [&](int j0) {
         // pin the loaded registers here, as pref_compute does
@@ -803,9 +825,9 @@ __device__ __forceinline__ void tile_rows(Pref<DT, NS> &pf, const l3m_dmat &m, c
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             if (j0 + s >= spt) break;
-            const int b = 4 * (j0 + s) + sub;
-            const float v = block_fma<DT>(0.f, pf.w[s], pf.sc[s], act, kp, b < nb ? b : nb - 1);
-            if (b < nb) y += v;
+            // blocks past nb: weights of block nb - 1 (pref_load_tile) times zero values with scale 0
+            const int o = 4 * (j0 + s);
+            y = block_fma_at<DT>(y, pf.w[s], pf.sc[s], xq + QB * o, xsp + o, xsum + o);
         }
     };
     auto finish = [&](int t) {
@@ -1314,7 +1336,7 @@ __host__ __device__ inline LdsA lds_a(int dt, int dim, int ctx, int hd, const l3
     LdsA L;
     size_t o = 0;
     const size_t pq = (size_t)g.qkv.tiles * g.qkv.nb, pw = (size_t)g.wo.tiles * g.wo.nb;
-    L.act = o;  o += align16(act_size(dt, dim));
+    L.act = o;  o += align16(act_size(dt, kwide(dim)));
     L.work = o; o += work_bytes(res_bytes(pq), res_bytes(pw));
     L.q = o;    o += align16(4 * (size_t)g.nq * hd);
     L.cur = o;  o += align16(4 * (size_t)g.nkv * hd);              // this step's k, v rows: bf16 [2][nkv][hd]
@@ -1339,7 +1361,7 @@ __host__ __device__ inline LdsB lds_b(int dt, int dim, const l3m_dchunk &c) {
     LdsB L;
     size_t o = 0;
     const size_t pg = (size_t)c.gate_up.tiles * c.gate_up.nb, pw = (size_t)c.down.tiles * c.down.nb;
-    L.act = o;  o += align16(act_size(dt, dim));
+    L.act = o;  o += align16(act_size(dt, kwide(dim)));
     L.work = o; o += work_bytes(res_bytes(pg), res_bytes(pw));
     L.gu = o;   o += align16(64 * (size_t)c.gate_up.tiles);
     L.act2 = o; o += align16(act_size(dt, c.nf));
@@ -1356,7 +1378,7 @@ struct LdsH { size_t act, work, scr, lgv, total; };
 __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg) {
     LdsH L;
     size_t o = 0;
-    L.act = o;  o += align16(act_size(dt, dim));
+    L.act = o;  o += align16(act_size(dt, kwide(dim)));
     L.work = o; o += work_bytes(res_bytes((size_t)tiles_per_wg * nb), 0);
     L.scr = o;  o += 4 * 64;
     L.lgv = o;  o += align16(4 * 16 * (size_t)tiles_per_wg);   // the slice's logits, kept for sampling
@@ -1725,7 +1747,7 @@ __device__ __forceinline__ void attn_kv_window(const l3m_dmodel &M, const l3m_dg
 template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dgroup &G, int layer, int pos,
                                            int tok, int gi, AttnW<DT> &w, uint8_t *smem) {
-    const int tid = tidx(), dim = M.dim, hd = M.hd, kp = kpad(dim);
+    const int tid = tidx(), dim = M.dim, hd = M.hd, kp = kwide(dim);
     const LdsA L = lds_of(G);
     float *work = (float *)(smem + L.work), *qh = (float *)(smem + L.q), *cs = (float *)(smem + L.cs);
     float *vred = (float *)(smem + L.vred), *att = (float *)(smem + L.att);
@@ -1833,7 +1855,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
 template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dchunk &C, int ci, FfnW<DT> &w,
                                           uint8_t *smem, int layer = 0, int pos = 0) {
-    const int tid = tidx(), dim = M.dim, kp = kpad(dim);
+    const int tid = tidx(), dim = M.dim, kp = kwide(dim);
     const LdsB L = lds_of(C);
     float *work = (float *)(smem + L.work), *gu = (float *)(smem + L.gu);
     uint8_t *act = smem + L.act, *act2 = smem + L.act2;
@@ -1916,7 +1938,7 @@ __device__ __forceinline__ l3m_dmat head_slice(const l3m_dmodel &M, int t0, int 
 template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &V, int t0, int tpw, int pos, HeadW<DT> &w,
                                            uint8_t *smem, float &v, int &idx, float *keep = nullptr) {
-    const int tid = tidx(), dim = M.dim, kp = kpad(dim);
+    const int tid = tidx(), dim = M.dim, kp = kwide(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
     float *work = (float *)(smem + L.work), *scr = (float *)(smem + L.scr);
     uint8_t *act = smem + L.act;
