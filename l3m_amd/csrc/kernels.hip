@@ -1744,6 +1744,19 @@ __device__ __forceinline__ void attn_kv_window(const l3m_dmodel &M, const l3m_dg
 // The attention block of head group gi (engine.c:236-258) at `layer`, position pos: x = xb + the FFN
 // partials (layer 0: the embedding row of tokens[pos]), RMSNorm, prep, the group's q/k/v rows, RoPE,
 // bf16 K/V into the cache, attention, prep, the group's Wo columns -> po[gi]. Group 0 keeps x in xa.
+// This step's k and v rows (bf16, engine.c:247-248, in cur) into the cache, for the kv heads group G
+// writes: element i0, i0 + step, ... of the 2 nkv hd.
+__device__ __forceinline__ void kv_rows_store(const l3m_dmodel &M, const l3m_dgroup &G, int layer, int pos, const uint16_t *cur, int i0,
+                                              int step) {
+    const int hd = M.hd, nkd = G.nkv * hd;
+    const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
+    for (int i = i0; i < 2 * nkd; i += step) {
+        const int kv = i < nkd ? 0 : 1, jj = i - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
+        if (G.write_kv >> kvl & 1u)
+            gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + (jj - kvl * hd)] = cur[i];
+    }
+}
+
 template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dgroup &G, int layer, int pos,
                                            int tok, int gi, AttnW<DT> &w, uint8_t *smem) {
@@ -1821,13 +1834,9 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // this step's k and v rows (bf16, engine.c:247-248) into the cache, for the kv heads this group writes,
     // by the wavefronts past those that prepare the attention output next (they go straight to the prep);
     // the flag after the block waits for the stores
+    // (the persistent path stores them after the block's flag instead, kv_rows_store)
     const int kq = kpad(nqd), skip = (kq + 255) >> 8 < NWE ? 64 * ((kq + 255) >> 8) : 0;
-    if (tid >= skip)
-        for (int i = tid - skip; i < 2 * nkd; i += NTE - skip) {
-            const int kv = i < nkd ? 0 : 1, jj = i - kv * nkd, kvl = (int)(((float)jj + 0.5f) * inv_hd);
-            if (G.write_kv >> kvl & 1u)
-                gw(kv ? M.vc : M.kc)[(((size_t)layer * M.n_kv + G.kv0 + kvl) * M.ctx + pos) * hd + (jj - kvl * hd)] = cur[i];
-        }
+    if (!PRE && tid >= skip) kv_rows_store(M, G, layer, pos, cur, tid - skip, NTE - skip);
 
     // the group's attention output, prepared, through its Wo columns -> the partial residual po[group]
     prep_owned<AT>(4 * tid < nqd ? ((const float4 *)att)[tid] : make_float4(0.f, 0.f, 0.f, 0.f), act2, kq);
@@ -2490,6 +2499,9 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
         phase(g, 1, pos, l);
         attn_block<DT, true, G2>(M, Lw, G, l, pos, tok, g, wt, smem);
         set_flag<false>(sync + SY_ATTN + g, epoch + 1);
+        // the K/V rows while the FFN runs: off the block's path (the next read of them is the window copy
+        // of the next position's step, behind this workgroup's later flag waits)
+        kv_rows_store(M, G, l, pos, (const uint16_t *)(smem + lds_of(G).cur), tidx(), NTE);
         phase(g, 10, pos, l);
     }
     return true;
