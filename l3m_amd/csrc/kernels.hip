@@ -2732,7 +2732,7 @@ __global__ void __launch_bounds__(NTE) k_where(int *out) {
 }
 
 // ------------------------------------------------------------------ batched prompt prefill
-// The prompt positions before the last one, all at once (SURVEY §8(f) row 1): per layer, the same
+// The prompt positions before the last one, all at once: per layer, the same
 // operations as the decode step (engine.c:230-275) on P tokens, with the matrices as int8 GEMMs on the
 // matrix cores. The decode path then runs from the last prompt position on, over the K/V rows these
 // kernels wrote. Weights are q8_0 lane-tile planes of the full matrices (q4_0 widened exactly); the

@@ -378,3 +378,33 @@ def test_persistent_kernel_equals_graph_path(models, monkeypatch, key):
             out[persist] = (first, second, m.logits)
     assert out["1"][0] == out["0"][0] and out["1"][1] == out["0"][1]
     np.testing.assert_array_equal(out["1"][2], out["0"][2])
+
+
+# Rows of 32 blocks (more than one batch of a lane's weight slots: q8_0 holds 5 slots of 4 blocks, q4_0 6)
+# and 24 tiles of q/k/v rows per head group (more tiles than wavefronts), for the tile form of the wide
+# matrices; hd 128 on the matrix-core attention.
+WIDE = A.Config("wide", dim=1024, n_layers=2, n_heads=8, n_kv_heads=2, ffn_dim=2816, vocab=4096, ctx=128, dtype="q8_0")
+
+
+@pytest.mark.parametrize("dtype", ["q8_0", "q4_0"])
+def test_wide_rows_take_several_slot_batches(oracle, models, monkeypatch, dtype):
+    """Tokens and logits against the oracle where a wavefront's rows need a second batch of slots and
+    more tiles than one per wavefront, and the persistent kernel bit-identical to the graph path there."""
+    path = models.get(WIDE, dtype, seed=5, std=0.05, norm_jitter=0.2)
+    ids = A.prompt(5, WIDE.vocab, 4)
+    om = oracle.load(path)
+    want = om.generate(ids, 24)
+    lo = om.logits()
+    out = {}
+    for persist in ("1", "0"):
+        monkeypatch.setenv("L3M_PERSIST", persist)
+        print(f"wide {dtype} persist {persist}", flush=True)
+        with A.Model(path) as m:
+            assert m.persistent == (persist == "1")
+            out[persist] = (m.generate(ids, 24), m.logits)
+    got, lg = out["1"]
+    assert got == want
+    assert int(np.argmax(lg)) == int(np.argmax(lo)) and kl(lo, lg) < 0.01
+    assert np.abs(lg - lo).max() <= SPREAD[dtype] * np.abs(lo).max()
+    assert out["0"][0] == got
+    np.testing.assert_array_equal(out["0"][1], lg)
