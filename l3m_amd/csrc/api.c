@@ -16,7 +16,6 @@
 #define HEAD_WGS 256           // workgroups of the head kernel
 #define MAX_PARTS 64           // partial residual vectors a step kernel adds (head groups, FFN chunks)
 #define BODY_CUS 32            // the CUs of one MI355X XCD (256 in 8), where the persistent kernel keeps the body
-#define PRO_BATCH 4            // partial residuals one prologue thread loads in one batch (FILL_PER of the kernels)
 #define EVICT_BYTES (512u << 20)   // --cold: read before each forward pass, twice the 256 MiB Infinity Cache
 
 struct l3m_model {
@@ -314,19 +313,24 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     if (d->n_heads % nq) nq = d->n_heads;
     d->n_groups = d->n_heads / nq;
     // FFN chunk (rows, a multiple of 32): at most the most rows whose gate/up rows (up rows only for GPT-2)
-    // and Wdown columns fit the weight slots a workgroup holds in flight (one pass of loads covers the
-    // chunk); within that, the fewest rows, from 64, that keep the head groups and chunks on the CUs of one
-    // XCD (where the persistent kernel keeps the body) and each prologue thread to one batch of partial
-    // loads: less FFN work per CU, measured faster (stories42M at ctx 1024 7,444 -> 7,817 tok/s, SmolLM2
-    // q8_0 +1.5%). Then larger (more passes of loads) while the body would not fit one XCD.
+    // take at most one 16-row tile per wavefront and, with the Wdown columns, fit the weight slots a
+    // workgroup holds in flight (one pass of loads covers the chunk). bf16 and f32 (whose gate/up pairs
+    // are spread over every wavefront's slots) take that: fewer chunks, fewer partials for every attention
+    // prologue, at the same FFN time (stories15M bf16 +1.5% at 96 rows against 64). The quantized dtypes
+    // (one tile per wavefront) take the fewest rows, from 64, that keep the head groups and chunks on the
+    // CUs of one XCD and each prologue thread to one batch of partial loads (stories42M q8_0 at ctx 1024
+    // -1.1% at 128 rows against 64; stories110M and SmolLM2 land on 128 and 96 either way). Then larger
+    // (more passes of loads) while the body would not fit one XCD.
     int sdt = m->reference ? L3M_F32 : m->mx_wide ? L3M_Q8_0 : m->dtype, cap_a = 64 * l3m_step_slots(sdt, 0), cap_b = 64 * l3m_step_slots(sdt, 1);
     int nbd = (d->dim + 31) / 32, chunk = 32, gu = gpt2 ? 1 : 2;
     for (int c = 256; c >= 32; c -= 32)
-        if (gu * c / 16 * nbd <= cap_a && (d->dim + 15) / 16 * (c / 32) <= cap_b) { chunk = c; break; }
-    const int pro_groups = 4096 / d->dim > 1 ? 4096 / d->dim : 1;   // the prologue's thread groups (1024 / (dim / 4))
-    for (int c = 64; c < chunk; c += 32) {
-        const int nc = (d->ffn + c - 1) / c;
-        if (d->n_groups + nc <= BODY_CUS && nc <= PRO_BATCH * pro_groups && nc <= MAX_PARTS) { chunk = c; break; }
+        if (gu * c <= 16 * 16 && gu * c / 16 * nbd <= cap_a && (d->dim + 15) / 16 * (c / 32) <= cap_b) { chunk = c; break; }
+    if (sdt != L3M_BF16 && sdt != L3M_F32) {
+        const int pro_groups = 4096 / d->dim > 1 ? 4096 / d->dim : 1;   // the prologue's thread groups (1024 / (dim / 4))
+        for (int c = 64; c < chunk; c += 32) {
+            const int nc = (d->ffn + c - 1) / c;
+            if (d->n_groups + nc <= BODY_CUS && nc <= 4 * pro_groups && nc <= MAX_PARTS) { chunk = c; break; }
+        }
     }
     const char *ck_ = getenv("L3M_FFN_CHUNK");      // rows per FFN chunk (a multiple of 32), for measurement
     if (ck_ && atoi(ck_) >= 32 && atoi(ck_) % 32 == 0) chunk = atoi(ck_);
