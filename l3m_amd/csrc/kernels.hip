@@ -2283,7 +2283,7 @@ __device__ bool wait_flags(const unsigned *flags, int n, unsigned target, unsign
             const unsigned v = lane < n ? ld_flag(flags + lane) : target;
             if (__all(v >= target)) return true;
             if (!keep_waiting(spin, t0, abort_flag, limit)) return false;
-            __builtin_amdgcn_s_sleep(SLEEP);
+            if constexpr (SLEEP > 0) __builtin_amdgcn_s_sleep(SLEEP);
         }
     }
     const int tid = tidx();
@@ -2493,7 +2493,7 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
             if (tok < 0) return false;
             if (g == 0 && tidx() == 0) gw(M.tokens)[pos] = tok;
         } else {
-            if (epoch > 0 && !wait_flags<1, true>(sync + SY_FFN, M.n_chunks, epoch, abort_flag, R.spin_limit, &ok_lds)) return false;
+            if (epoch > 0 && !wait_flags<0, true>(sync + SY_FFN, M.n_chunks, epoch, abort_flag, R.spin_limit, &ok_lds)) return false;
             if (l == 0) tok = __hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         phase(g, 1, pos, l);
@@ -2526,7 +2526,7 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
         ffn_static(wt.st, M, Lw);
         ffn_issue<DT>(wt, C);
         const unsigned epoch = (unsigned)(s * nl + l);
-        if (!wait_flags<1, true>(sync + SY_ATTN, M.n_groups, epoch + 1, sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
+        if (!wait_flags<0, true>(sync + SY_ATTN, M.n_groups, epoch + 1, sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
         phase(64 + ci, 1, pos, l);
         ffn_block<DT, true, G2>(M, Lw, C, ci, wt, smem, l, pos);
         set_flag<false>(sync + SY_FFN + ci, epoch + 1);
