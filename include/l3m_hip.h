@@ -181,8 +181,11 @@ int    l3m_logits_at(const l3m_model *m, int pos, float *out);
 // least L3M_PREFILL_MIN (default 8) tokens on q8_0 and q4_0 bodies (and mxfp4 bodies whose blocks widen
 // exactly to q8_0) are prefilled unless L3M_PREFILL=0.
 int    l3m_prefill_positions(const l3m_model *m);
-// The attention mode the decode step of m runs (l3m_attention_mode's codes).
+// The attention mode the decode step of m runs at positions inside its K/V window (l3m_attention_mode's
+// codes); and the window's size in positions: ctx when every position fits in LDS, else the most (a
+// multiple of 32) that fit, 0 when none. Steps at positions from l3m_decode_window on read the cache (mode 0).
 int    l3m_decode_attention(const l3m_model *m);
+int    l3m_decode_window(const l3m_model *m);
 // K and V rows [pos0, pos0 + n) of kv head kvh in layer `layer` of m's cache (bf16 as the step writes them,
 // engine.c:247-248), into k and v [n][hd]; -1 when out of range.
 int    l3m_kv_rows(const l3m_model *m, int layer, int kvh, int pos0, int n, uint16_t *k, uint16_t *v);

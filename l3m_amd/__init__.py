@@ -72,6 +72,7 @@ l3m_prefill_positions i p       | l3m_probe_stream i z i i i *d   | l3m_probe_ex
 l3m_probe_graph_node i i i *d
 l3m_k_dequant i M i i p p       | l3m_attention_mode i i i i i   | l3m_k_attend_decode i i p p p p i i i i i p
 l3m_dev_evict i p z p           | l3m_decode_attention i p       | l3m_kv_rows i p i i i i p p
+l3m_decode_window i p
 l3m_time_read d ** i z i         | l3m_hip_attend_noalloc i p p p p i i i | l3m_phase_stamps i i i i p
 """
 _SIG = {}
@@ -195,6 +196,11 @@ class Model:
     def attention_mode(self):
         """The decode step's attention: 2 matrix cores over the LDS window, 1 VALU over it, 0 from the cache."""
         return self._lib.l3m_decode_attention(self._handle())
+
+    @property
+    def window(self):
+        """Positions the decode step's LDS K/V window holds (ctx when all fit); past it attention reads the cache."""
+        return self._lib.l3m_decode_window(self._handle())
 
     def kv_rows(self, layer, kvh, pos0, n, hd):
         """bf16 K and V rows [pos0, pos0 + n) of one kv head of one layer's cache, as uint16 [n, hd] each."""

@@ -448,6 +448,20 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
             return fail(m, "prefill weight upload failed");
         }
     }
+    // The K/V window: every position of the context when it fits in LDS beside the rest of the attention
+    // block, else the most positions (a multiple of 32) that fit; a step at a position past it reads K and V
+    // from the cache. The offsets of l3m_group_layout do not depend on the window (it is the last region).
+    int kv_win = d->ctx;
+    for (;;) {
+        unsigned need = 0;
+        for (int gi = 0; gi < d->n_groups; gi++) {
+            const unsigned la = l3m_lds_attn(d->body_dtype, d->dim, kv_win, d->hd, &groups[gi], 1);
+            if (la > need) need = la;
+        }
+        lds_a = need;
+        if (need <= l3m_dev_lds_max() || kv_win <= 32) break;
+        kv_win = kv_win == d->ctx ? (d->ctx - 1) & ~31 : kv_win - 32;
+    }
     free(groups); free(chunks); free(rows);
     const l3m_tensor *embed = l3m_map_tensor(f, "embed");
     double body = m->weight_bytes;
@@ -469,7 +483,8 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     d->head_tiles_per_wg = (d->head.tiles + HEAD_WGS - 1) / HEAD_WGS;
     d->head_grid = (d->head.tiles + d->head_tiles_per_wg - 1) / d->head_tiles_per_wg;
     unsigned lds_max = l3m_dev_lds_max();
-    d->kv_lds = lds_a <= lds_max;                // the K, V window in LDS when it fits beside the rest
+    d->kv_lds = lds_a <= lds_max;                // the K, V window in LDS when 32 positions fit beside the rest
+    d->kv_win = d->kv_lds ? kv_win : 0;
     d->lds_a = d->kv_lds ? lds_a : lds_a0; d->lds_b = lds_b;
     d->lds_h = l3m_lds_head(d->head.dtype, d->dim, d->head.nb, d->head_tiles_per_wg);
     if (d->lds_a > lds_max || d->lds_b > lds_max || d->lds_h > lds_max || d->head_tiles_per_wg > 64)
@@ -568,9 +583,9 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
         snprintf(m->desc, sizeof m->desc, "%s: %s, %d layers, %.1f MiB on 1 gpu (hip)%s", base, l3m_dtype_name(m->dtype), d->n_layers,
                  m->weight_bytes / MiB, m->mx_wide ? ", blocks widened exactly to q8_0" : "");
     if (o.verbose)
-        fprintf(stderr, "l3m: %s, ctx %d, %s; %d head groups, %d ffn chunks, head %d x %d tiles, lds %u/%u/%u, kv in lds %d; "
+        fprintf(stderr, "l3m: %s, ctx %d, %s; %d head groups, %d ffn chunks, head %d x %d tiles, lds %u/%u/%u, kv in lds %d (%d positions); "
                 "persistent %d (grid %d, body on xcd %d, head %d x %d tiles, lds %u)\n", m->desc, d->ctx, l3m_dev_name(), d->n_groups,
-                d->n_chunks, d->head_grid, d->head_tiles_per_wg, d->lds_a, d->lds_b, d->lds_h, d->kv_lds, m->persist, m->grid, m->body_xcc,
+                d->n_chunks, d->head_grid, d->head_tiles_per_wg, d->lds_a, d->lds_b, d->lds_h, d->kv_lds, d->kv_win, m->persist, m->grid, m->body_xcc,
                 m->n_head, m->head_tpw, m->lds_decode);
     return m;
 }
@@ -793,8 +808,10 @@ int l3m_decode_persistent(const l3m_model *m) { return m->persist; }
 int l3m_prefill_positions(const l3m_model *m) { return m->prefilled; }
 
 int l3m_decode_attention(const l3m_model *m) {
-    return l3m_attention_mode(m->dm.kv_lds, m->dm.hd, m->dm.n_heads / m->dm.n_groups, m->dm.ctx);
+    return l3m_attention_mode(m->dm.kv_lds, m->dm.hd, m->dm.n_heads / m->dm.n_groups, m->dm.kv_win);
 }
+
+int l3m_decode_window(const l3m_model *m) { return m->dm.kv_win; }
 
 int l3m_kv_rows(const l3m_model *m, int layer, int kvh, int pos0, int n, uint16_t *k, uint16_t *v) {
     const l3m_dmodel *d = &m->dm;

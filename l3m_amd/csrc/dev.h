@@ -43,7 +43,9 @@ typedef struct {
 typedef struct {
     int          dim, hd, n_heads, n_kv, kv_dim, ffn, vocab, ctx, n_layers, nslots;
     int          n_groups, n_chunks, head_grid, head_tiles_per_wg, body_dtype;
-    int          kv_lds;         // attention copies the K, V rows of its kv heads into LDS (they fit)
+    int          kv_lds;         // attention copies the K, V rows of its kv heads into LDS (a window exists)
+    int          kv_win;         // positions the LDS window holds (ctx, or the multiple of 32 that fits);
+                                 // steps at pos >= kv_win read K and V from the cache
     float        eps;
     float        att_scale;      // 1 / sqrt(hd)
     int          hpk;            // query heads per kv head

@@ -1396,7 +1396,7 @@ __host__ __device__ inline LdsH lds_h(int dt, int dim, int nb, int tiles_per_wg)
 template <bool COH>
 __device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int kv0, int nkv, int pos, bool vt) {
     const int wave = wave_id(), lane = tidx() & 63, hd = M.hd, rs = kv_row(hd);
-    const size_t cwin = (size_t)M.ctx * hd, lwin = (size_t)M.ctx * rs;      // per head: cache, LDS window
+    const size_t cwin = (size_t)M.ctx * hd, lwin = (size_t)M.kv_win * rs;   // per head: cache, LDS window
     // one row per instruction (the window's rows are padded apart, so a copy cannot span rows): hd / 8
     // lanes of 16 bytes each
     for (int head = 0; head < (vt ? nkv : 2 * nkv); head++) {
@@ -1410,7 +1410,7 @@ __device__ void kv_window_dma(uint16_t *kvb, const l3m_dmodel &M, int layer, int
                                                  COH ? 16 : 0);   // 16: sc1
     }
     if (!vt) return;
-    const int vr = vt_row(M.ctx), tend = (pos + 32) & ~31;   // the step of position pos ends at tend
+    const int vr = vt_row(M.kv_win), tend = (pos + 32) & ~31;   // the step of position pos ends at tend (<= kv_win)
     for (int j = 0; j < nkv; j++) {
         const uint16_t *src = M.vc + ((size_t)layer * M.n_kv + kv0 + j) * cwin;
         uint16_t *dst = kvb + (size_t)nkv * lwin + (size_t)j * hd * vr;
@@ -1454,7 +1454,7 @@ __device__ void attend_group(const l3m_dmodel &M, const l3m_dgroup &G, int layer
     const int lane = tidx() & 63, wave = wave_id(), j = lane & (LP - 1), gl = lane >> lg, n = pos + 1;
     const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
     const int rs = WIN ? kv_row(hd) : hd;             // row stride: LDS window or cache
-    const size_t win = (size_t)M.ctx * rs;
+    const size_t win = (size_t)(WIN ? M.kv_win : M.ctx) * rs;
     // W = 2^wl wavefronts per head: the fewest that keep each at ATT_IT rounds or less, at most 2^att_wl
     const int sh = ATT_LOG_IT + 6 - lg;               // ATT_IT * PPW = 2^sh positions per wavefront
     const int need = (n + (1 << sh) - 1) >> sh;
@@ -1597,7 +1597,7 @@ __device__ __forceinline__ void split3(float x, __bf16 &h, __bf16 &m, __bf16 &l)
 // sc: 10 * ceil32(ctx) bytes of LDS; vred: 2 * NWE floats; qp: [3][nq * hd] bf16. Ends with a barrier.
 __device__ void attend_mfma(const l3m_dmodel &M, const l3m_dgroup &G, int pos, const __bf16 *qp, const uint16_t *kvb, float *sc,
                             float *vred, float *att) {
-    const int hd = M.hd, rs = kv_row(hd), vr = vt_row(M.ctx), ctx = M.ctx, n = pos + 1;
+    const int hd = M.hd, rs = kv_row(hd), vr = vt_row(M.kv_win), ctx = M.kv_win, n = pos + 1;   // ctx: the window's
     const int lane = tidx() & 63, wave = wave_id(), li = lane & 15, lg = lane >> 4;
     const float scale = M.att_scale, ihpk = __builtin_amdgcn_rcpf((float)M.hpk);
     const size_t win = (size_t)ctx * rs;
@@ -1736,9 +1736,9 @@ template <int DT> __device__ __forceinline__ void head_issue(HeadW<DT> &w, const
 // 0..pos-1 were written in earlier steps, so it can run while the block waits for its inputs.
 template <int DT>
 __device__ __forceinline__ void attn_kv_window(const l3m_dmodel &M, const l3m_dgroup &G, int layer, int pos, uint8_t *smem) {
-    if (!M.kv_lds) return;
+    if (!M.kv_lds || pos >= M.kv_win) return;
     const LdsA L = lds_of(G);
-    kv_window_dma<true>((uint16_t *)(smem + L.kvb), M, layer, G.kv0, G.nkv, pos, mfma_fits(M.hd, G.nq, M.ctx));
+    kv_window_dma<true>((uint16_t *)(smem + L.kvb), M, layer, G.kv0, G.nkv, pos, mfma_fits(M.hd, G.nq, M.kv_win));
 }
 
 // The attention block of head group gi (engine.c:236-258) at `layer`, position pos: x = xb + the FFN
@@ -1784,7 +1784,8 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     // K, V rows 0..pos-1 (no dependence on this step). Issued after the prologue is consumed: a copy of
     // data-dependent length ahead of it would make the compiler wait for every load in flight there.
     // The persistent path issues it before it waits for the block's inputs (attn_kv_window).
-    if (!PRE && M.kv_lds) kv_window_dma<false>(kvb, M, layer, G.kv0, G.nkv, pos, mfma_fits(hd, G.nq, M.ctx));
+    const bool kwin = M.kv_lds && pos < M.kv_win;    // rows 0..pos fit the LDS window at this step
+    if (!PRE && kwin) kv_window_dma<false>(kvb, M, layer, G.kv0, G.nkv, pos, mfma_fits(hd, G.nq, M.kv_win));
     constexpr int AT = a_dtype<DT>();                // the activations take the form the step matrices read
     if constexpr (G2) ln_prep<AT>(x, Lw.attn_norm, Lw.attn_norm_b, dim, kp, M.eps, act, red);
     else norm_prep<AT>(x, w.st.nw, dim, kp, M.eps, act, red);
@@ -1796,7 +1797,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     const int nqd = G.nq * hd, nkd = G.nkv * hd;
     const float inv_hd = 1.0f / (float)hd;            // i / hd by an exact float reciprocal (i, hd < 2^12)
     // the matrix-core attention (LDS window, hd a multiple of 16, q parts fit beside vred's 2 NWE sums)
-    const bool mfma_att = M.kv_lds && mfma_fits(hd, G.nq, M.ctx);
+    const bool mfma_att = kwin && mfma_fits(hd, G.nq, M.kv_win);
     __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
     auto qkv_row = [&](int i, float y, float partner, bool lead) {
         if constexpr (G2) y += G.bqkv[i];            // the GPT-2 variant's q, k, v biases; no RoPE
@@ -1814,9 +1815,9 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
                 const uint16_t hb = f32_bf16(y);
                 cur[kv * nkd + jj] = hb;
                 if (mfma_att && kv)                   // V^T
-                    kvb[(size_t)G.nkv * M.ctx * kv_row(hd) + (size_t)jj * vt_row(M.ctx) + pos] = hb;
-                else if (M.kv_lds)
-                    kvb[((size_t)(kv * G.nkv + kvl) * M.ctx + pos) * kv_row(hd) + (jj - kvl * hd)] = hb;
+                    kvb[(size_t)G.nkv * M.kv_win * kv_row(hd) + (size_t)jj * vt_row(M.kv_win) + pos] = hb;
+                else if (kwin)
+                    kvb[((size_t)(kv * G.nkv + kvl) * M.kv_win + pos) * kv_row(hd) + (jj - kvl * hd)] = hb;
             }
         }
     };
@@ -1824,11 +1825,11 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
     phase(gi, 4, pos, layer);
     // the window's copy (issued long before) is complete; this step's rows go to the cache after the
     // attention, so their store acknowledgements stay off the path to it
-    if (M.kv_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (kwin) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     phase(gi, 5, pos, layer);
     if (mfma_att) attend_mfma(M, G, pos, qp, kvb, work, vred, att);
-    else if (M.kv_lds) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
+    else if (kwin) attend_group<true, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
     else attend_group<false, PRE>(M, G, layer, pos, qh, cur, kvb, vred, att);
     phase(gi, 6, pos, layer);
     // this step's k and v rows (bf16, engine.c:247-248) into the cache, for the kv heads this group writes,
@@ -2133,7 +2134,7 @@ __global__ void __launch_bounds__(NTE) k_attend_decode(float *out, const float *
     uint16_t *cur = (uint16_t *)(smem + L.cur), *kvb = (uint16_t *)(smem + L.kvb);
     __bf16 *qp = (__bf16 *)(vred + 2 * NWE);
     l3m_dmodel M{};
-    M.hd = hd; M.ctx = ctx; M.n_kv = nkv; M.hpk = nq / nkv; M.att_scale = 1.0f / sqrtf((float)hd); M.kv_lds = MODE != 0;
+    M.hd = hd; M.ctx = ctx; M.n_kv = nkv; M.hpk = nq / nkv; M.att_scale = 1.0f / sqrtf((float)hd); M.kv_lds = MODE != 0; M.kv_win = MODE != 0 ? ctx : 0;
     M.kc = (uint16_t *)kc; M.vc = (uint16_t *)vc;
     l3m_dgroup G{};
     G.q0 = 0; G.nq = nq; G.kv0 = 0; G.nkv = nkv; G.att_wl = att_wl;

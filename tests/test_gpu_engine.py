@@ -84,8 +84,8 @@ def test_greedy_tokens_match_reference(golden_cases, oracle, i):
 
 
 # The attention each golden configuration's decode step runs (l3m_attention_mode): stories15M (hd 48),
-# stories42M (ctx 512), stories110M and SmolLM2 (hd 64) take the matrix cores over the LDS window (its V
-# transposed). The cache-reading form has its own long-context test.
+# stories42M, stories110M and SmolLM2 (hd 64) take the matrix cores over the LDS window (its V
+# transposed). The cache-reading form, past a window shorter than ctx, has its own long-context test.
 GOLDEN_ATTENTION = {"stories15M": 2, "stories42M": 2, "stories110M": 2, "smollm2": 2}
 
 
@@ -229,14 +229,17 @@ def assert_follows_oracle(got, steps, what):
 @pytest.mark.parametrize("cfg,ctx,n_new", [(A.CONFIGS["stories42M"], 1024, 600), (dataclasses.replace(SMALL, name="tiny2k", ctx=2048), 2048, 1500)],
                          ids=["stories42M-ctx1024", "tiny-ctx2048"])
 def test_long_context_follows_oracle(models, oracle, cfg, ctx, n_new):
-    """Decoding far past the positions whose K/V window fits in LDS (attention reads the cache): every step
+    """Decoding far past the positions whose K/V window fits in LDS (the steps before the window's end attend
+    over it, those past it read the cache, in one generate call): every step
     of a long greedy run, teacher-forcing the oracle along the GPU's own tokens, and the logits of the last
     positions at the engine bar. stories42M runs at its configured ctx 1024 (engine.c:22, 435 cap the default
     at 512)."""
     path = models.get(cfg, cfg.dtype, seed=11, std=0.05 if cfg.dim < 256 else 0.02, norm_jitter=0.1 if cfg.dim < 256 else 0.0)
     ids = A.prompt(11, cfg.vocab, 4)
     m = A.Model(path, ctx=ctx)
-    assert m.ctx == ctx and m.attention_mode == 0
+    # the window holds the first positions (matrix-core attention there), the cache serves the rest
+    assert m.ctx == ctx and 32 <= m.window < ctx and m.window % 32 == 0 and m.attention_mode == 2, (m.window, m.attention_mode)
+    print(f"window {m.window} positions of {ctx}", flush=True)
     got = m.generate(ids, n_new)
     assert len(got) == n_new
     om = oracle.load(path, ctx=ctx)
