@@ -314,24 +314,15 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     d->n_groups = d->n_heads / nq;
     // FFN chunk (rows, a multiple of 32): at most the most rows whose gate/up rows (up rows only for GPT-2)
     // take at most one 16-row tile per wavefront and, with the Wdown columns, fit the weight slots a
-    // workgroup holds in flight (one pass of loads covers the chunk). bf16 and f32 (whose gate/up pairs
-    // are spread over every wavefront's slots) take that: fewer chunks, fewer partials for every attention
-    // prologue, at the same FFN time (stories15M bf16 +1.5% at 96 rows against 64). The quantized dtypes
-    // (one tile per wavefront) take the fewest rows, from 64, that keep the head groups and chunks on the
-    // CUs of one XCD and each prologue thread to one batch of partial loads (stories42M q8_0 at ctx 1024
-    // -1.1% at 128 rows against 64; stories110M and SmolLM2 land on 128 and 96 either way). Then larger
-    // (more passes of loads) while the body would not fit one XCD.
+    // workgroup holds in flight (one pass of loads covers the chunk). Every dtype takes the most rows that
+    // do: fewer chunks, fewer partials for every attention prologue, at the same FFN time (stories15M bf16
+    // +1.5% at 96 rows against 64, stories42M q8_0 at ctx 1024 +3.2% at 128 rows against 64; stories110M
+    // q4_0 within 0.3% from 64 to 128 rows, 16% slower at 160). Then larger (more passes of loads) while
+    // the body would not fit one XCD.
     int sdt = m->reference ? L3M_F32 : m->mx_wide ? L3M_Q8_0 : m->dtype, cap_a = 64 * l3m_step_slots(sdt, 0), cap_b = 64 * l3m_step_slots(sdt, 1);
     int nbd = (d->dim + 31) / 32, chunk = 32, gu = gpt2 ? 1 : 2;
     for (int c = 256; c >= 32; c -= 32)
         if (gu * c <= 16 * 16 && gu * c / 16 * nbd <= cap_a && (d->dim + 15) / 16 * (c / 32) <= cap_b) { chunk = c; break; }
-    if (sdt != L3M_BF16 && sdt != L3M_F32) {
-        const int pro_groups = 4096 / d->dim > 1 ? 4096 / d->dim : 1;   // the prologue's thread groups (1024 / (dim / 4))
-        for (int c = 64; c < chunk; c += 32) {
-            const int nc = (d->ffn + c - 1) / c;
-            if (d->n_groups + nc <= BODY_CUS && nc <= 4 * pro_groups && nc <= MAX_PARTS) { chunk = c; break; }
-        }
-    }
     const char *ck_ = getenv("L3M_FFN_CHUNK");      // rows per FFN chunk (a multiple of 32), for measurement
     if (ck_ && atoi(ck_) >= 32 && atoi(ck_) % 32 == 0) chunk = atoi(ck_);
     while ((d->ffn + chunk - 1) / chunk > MAX_PARTS || (d->n_groups + (d->ffn + chunk - 1) / chunk > BODY_CUS && chunk < d->ffn)) chunk += 32;
