@@ -383,6 +383,28 @@ def test_persistent_kernel_equals_graph_path(models, monkeypatch, key):
     np.testing.assert_array_equal(out["1"][2], out["0"][2])
 
 
+@pytest.mark.parametrize("cfg,ctx", [(A.CONFIGS["stories42M"], 1024), (dataclasses.replace(SMALL, name="tiny2k", ctx=2048), 2048)],
+                         ids=["stories42M-ctx1024", "tiny-ctx2048"])
+def test_window_end_persistent_equals_graph_path(models, monkeypatch, cfg, ctx):
+    """Across the end of the K/V window (steps before it attend over the LDS window, steps from it on read
+    the cache) the persistent kernel and the one-graph-per-step path run the same blocks: tokens and the
+    last logits bit-identical, 40 steps past the window's end."""
+    path = models.get(cfg, cfg.dtype, seed=11, std=0.05 if cfg.dim < 256 else 0.02, norm_jitter=0.1 if cfg.dim < 256 else 0.0)
+    ids = A.prompt(11, cfg.vocab, 4)
+    out = {}
+    for persist in ("1", "0"):
+        monkeypatch.setenv("L3M_PERSIST", persist)
+        with A.Model(path, ctx=ctx) as m:
+            assert m.persistent == (persist == "1")
+            win = m.window
+            assert 32 <= win < ctx and win % 32 == 0, win
+            n = win - len(ids) + 41
+            print(f"{cfg.name} ctx {ctx} persist {persist}: window {win}, {n} steps", flush=True)
+            out[persist] = (m.generate(ids, n), m.logits)
+    assert out["1"][0] == out["0"][0]
+    np.testing.assert_array_equal(out["1"][1], out["0"][1])
+
+
 # Rows of 32 blocks (more than one batch of a lane's weight slots: q8_0 holds 5 slots of 4 blocks, q4_0 6)
 # and 24 tiles of q/k/v rows per head group (more tiles than wavefronts), for the tile form of the wide
 # matrices; hd 128 on the matrix-core attention.
