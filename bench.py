@@ -407,9 +407,7 @@ def phase_report(A, d, name, dtype, pos, layer):
         def med(vals):
             return round(float(np.median(vals)) - z, 3)
         rep["head_chain_us"] = {
-            "ffn_chunks_see_every_chunk": med([t[0, c, 10] for c in chunks]),
-            "final_residual_stored_and_flagged": med([t[0, c, 11] for c in chunks]),
-            "head_workgroups_see_it": med([t[0, h, 1] for h in heads]),
+            "head_workgroups_see_every_flag": med([t[0, h, 1] for h in heads]),
             "head_blocks_end": med([t[0, h, 2] for h in heads]),
             "head_keys_stored": med([t[0, h, 3] for h in heads]),
             "next_position_attention_wakes": med([t[1, g, 1] for g in groups]),

@@ -489,7 +489,6 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     d->xb = dalloc(m, (size_t)d->dim * 4);
     d->po = dalloc(m, (size_t)d->n_groups * d->dim * 4);
     d->pd = dalloc(m, (size_t)d->n_chunks * d->dim * 4);
-    d->xf = dalloc(m, (size_t)d->dim * 4);
     if (m->pf) {
         int mk = d->dim > d->n_heads * d->hd ? d->dim : d->n_heads * d->hd;
         if (d->ffn > mk) mk = d->ffn;
@@ -555,7 +554,7 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     free(rope);
     m->tok_host = calloc((size_t)d->ctx + 1, sizeof *m->tok_host);
     m->logits = calloc((size_t)d->vocab, sizeof *m->logits);
-    if (!d->pos || !d->tokens || !d->xa || !d->xb || !d->po || !d->pd || !d->xf || !d->samp || !d->logits || !d->part_val || !d->part_idx || !d->done ||
+    if (!d->pos || !d->tokens || !d->xa || !d->xb || !d->po || !d->pd || !d->samp || !d->logits || !d->part_val || !d->part_idx || !d->done ||
         !d->kc || !d->vc || !d->rope || !d->norm || !m->tok_host || !m->logits || !m->sync || !m->layers_dev || !m->run_dev || !m->run_host ||
         !m->dm_dev || l3m_dev_upload(m->dm_dev, d, sizeof *d))
         return fail(m, "device allocation failed");

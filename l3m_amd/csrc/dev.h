@@ -57,7 +57,6 @@ typedef struct {
     float       *xa, *xb;        // residual stream entering the attention block / the FFN block
     float       *po;             // [n_groups][dim] attention-block partials (Wo column slices)
     float       *pd;             // [n_chunks][dim] FFN partials (Wdown column slices)
-    float       *xf;             // [dim] the final residual (persistent kernel: summed once per step for the head)
     float       *logits;         // [nslots][vocab], slot = pos % nslots
     float       *part_val;       // [head_grid] argmax partials
     int         *part_idx;

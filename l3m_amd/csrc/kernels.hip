@@ -84,6 +84,9 @@ __device__ __forceinline__ void stcoh16(void *p, size_t i, float4 x) {
     const u32x4 v = {__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w)};
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), buf(p), (uint32_t)(16 * i), 0, SC1);
 }
+__device__ __forceinline__ void stcoh4(void *p, size_t i, float x) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), buf(p), (uint32_t)(4 * i), 0, SC1);
+}
 template <bool COH> __device__ __forceinline__ uint4 ld16(const void *p, size_t i) { return COH ? ldcoh16(p, i) : ldg16(p, i); }
 template <bool COH> __device__ __forceinline__ float4 ld16f(const void *p, size_t i) {
     if constexpr (COH) {
@@ -1169,37 +1172,6 @@ __device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, const P
 
 __device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
 
-// x[4f, 4f+4) as pro_finish forms it from the same inputs, for one thread: base and the parts grouped
-// and added in the same order (a group that leaves some of its FILL_PER slots unused adds +0.0 for
-// them, which turns a -0.0 sum into +0.0), read with device-coherent loads.
-__device__ __forceinline__ float4 parts_sum_at(const float *base, const float *parts, const ProGeom &G, int f) {
-    constexpr int B = 16;                             // parts loaded at once; the rest one at a time
-    const int nparts = G.nparts, dim = 4 * G.n4;
-    const size_t stride = (size_t)(dim >> 2);
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 p[B];
-#pragma unroll
-    for (int k = 0; k < B; k++) p[k] = k < nparts ? ld16f<true>(parts, (size_t)k * stride + f) : zero;
-    float4 x = zero, v = ld16f<true>(base, f);
-    int g = 0;
-    auto close = [&]() {
-        const int c = nparts - g * G.per < G.per ? nparts - g * G.per : G.per;
-        if (c < FILL_PER) v = add4(v, zero);
-        x = g == 0 ? v : add4(x, v);
-    };
-    auto take = [&](int k, float4 pk) {
-        if (k == (g + 1) * G.per) { close(); v = zero; g++; }
-        v = add4(v, pk);
-    };
-#pragma unroll
-    for (int k = 0; k < B; k++)
-        if (k < nparts) take(k, p[k]);
-    for (int k = B; k < nparts; k++) take(k, ld16f<true>(parts, (size_t)k * stride + f));
-    close();
-    for (int e = g + 1; e < G.groups; e++) x = add4(x, zero);
-    return x;
-}
-
 // act = the prepared activation (pack.c:101-123) of the values v[4f, 4f+4) held by thread f, f < kp/4
 // (zero beyond k): the reference's per-32-block int8 quantization (8 lanes per block), bf16 or f32.
 // Ends with a barrier.
@@ -1864,7 +1836,9 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
 // chunk's gate and up rows, SiLU(gate) * up, prep, its Wdown columns -> pd[ci]. Chunk 0 keeps x in xb.
 template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer &Lw, const l3m_dchunk &C, int ci, FfnW<DT> &w,
-                                          uint8_t *smem, int layer = 0, int pos = 0) {
+                                          uint8_t *smem, int layer = 0, int pos = 0, bool through = false) {
+    // through: the last layer of a persistent step with logits, whose x (chunk 0) and partials the head
+    // workgroups on other XCDs read, stored through to memory
     const int tid = tidx(), dim = M.dim, kp = kwide(dim);
     const LdsB L = lds_of(C);
     float *work = (float *)(smem + L.work), *gu = (float *)(smem + L.gu);
@@ -1877,6 +1851,7 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
     pro_load<PRE>(P, M.xa, M.po, PG, M.embed, false, 0);     // x += proj (engine.c:259)
     if constexpr (!PRE) ffn_issue<DT>(w, C);
     const float4 x = pro_finish<PRE>(P, M.po, PG, false, (float4 *)work, ci == 0 ? M.xb : nullptr, nullptr, w.st.cs, 0);
+    if (through && ci == 0 && tid < (dim >> 2)) stcoh16(M.xb, tid, x);
     phase(64 + ci, 2, pos, layer);
     constexpr int AT = a_dtype<DT>();                // the activations take the form the step matrices read
     if constexpr (G2) ln_prep<AT>(x, Lw.ffn_norm, Lw.ffn_norm_b, dim, kp, M.eps, act, red);
@@ -1921,11 +1896,17 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
         phase(64 + ci, 7, pos, layer);
         rows_sum4(C.down, work, dim, [&](int i, float y, float, bool lead) {
             y += ci == 0 ? Lw.bdown[i] : 0.f;         // b_down once, with chunk 0's partial
-            if (lead) gw(pd)[i] = y;
+            if (lead) {
+                if (through) stcoh4(pd, i, y);
+                else gw(pd)[i] = y;
+            }
         });
     } else {
         mv_rows<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, act2, kf, work, dim, [&](int i, float y, bool lead) {
-            if (lead) gw(pd)[i] = y;
+            if (lead) {
+                if (through) stcoh4(pd, i, y);
+                else gw(pd)[i] = y;
+            }
         });
         phase(64 + ci, 7, pos, layer);
     }
@@ -1948,7 +1929,7 @@ __device__ __forceinline__ l3m_dmat head_slice(const l3m_dmodel &M, int t0, int 
 template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &V, int t0, int tpw, int pos, HeadW<DT> &w,
                                            uint8_t *smem, float &v, int &idx, float *keep = nullptr) {
-    const int tid = tidx(), dim = M.dim, kp = kwide(dim);
+    const int dim = M.dim, kp = kwide(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
     float *work = (float *)(smem + L.work), *scr = (float *)(smem + L.scr);
     uint8_t *act = smem + L.act;
@@ -1956,11 +1937,12 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
 
     float4 x;
     if constexpr (PRE) {
-        // the persistent path sums the final residual once per step (reduce_final) into xf; the norm
-        // weights came with the head's weights (head_issue)
-        const int n4 = dim >> 2, own = tid < n4 ? tid : n4 - 1;
-        const float4 xv = ld16f<true>(M.xf, own);
-        x = tid < n4 ? xv : make_float4(0.f, 0.f, 0.f, 0.f);
+        // the persistent path: x and the last layer's FFN partials, stored through by the chunks, read
+        // from memory (coherent loads); the norm weights came with the head's weights (head_issue)
+        Pro P;
+        const ProGeom PG = pro_geom(M, 0);
+        pro_load<true>(P, M.xb, M.pd, PG, M.embed, false, 0);   // x += down (engine.c:275), last layer
+        x = pro_finish<true>(P, M.pd, PG, false, (float4 *)work, nullptr, nullptr, w.st.cs, 0);
     } else {
         Pro P;
         const ProGeom PG = pro_geom(M, 0);
@@ -2234,18 +2216,18 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
 // launch (the host zeroes R.sync first): attention group g sets attn[g] = s*L + l + 1 after layer l of
 // step s, FFN chunk c sets ffn[c] likewise. A layer's blocks wait for all flags of the block before them.
 //
-// Hand-over to and from the head (other XCDs, so through memory): after the last layer of a step with
-// logits, FFN chunk c waits for every chunk's partial, sums its slice of the final residual into xf with
-// write-through stores and sets xf_flag[c] = s + 1; head workgroups wait for all of them, compute their
-// tiles' logits and argmax, and store one 64-bit key per workgroup (the step's tag, the value in an
-// order-preserving code, the index); the attention groups of the next step wait for every key with that
-// tag and take the maximum. The chunks do the final sum so that the attention groups are free after
-// their last block: they issue the next step's first weights while the head runs, and those loads are
-// complete by the time they poll for the token (a wavefront's loads return in order).
+// Hand-over to and from the head (other XCDs, so through memory): in the last layer of a step with
+// logits, the FFN chunks store x (chunk 0) and their partials through to memory and set their flags
+// device-wide; head workgroups wait for those flags, sum the final residual themselves (the prologue's
+// order of additions, coherent loads), compute their tiles' logits and argmax, and store one 64-bit key
+// per workgroup (the step's tag, the value in an order-preserving code, the index); the attention groups
+// of the next step wait for every key with that tag and take the maximum. The attention groups are free
+// after their last block: they issue the next step's first weights while the head runs, and those loads
+// are complete by the time they poll for the token (a wavefront's loads return in order).
 //
 // Every wait is bounded: past R.spin_limit ticks of the 100 MHz clock the waiter raises the abort flag
 // and every workgroup leaves at its next wait, so the grid always drains.
-enum { SY_ATTN = 0, SY_FFN = 64, SY_XF = 128, SY_ABORT = L3M_SYNC_ABORT, SY_TOKEN = 208, SY_TICKET = 224, SY_HEAD_TICKET = 240,
+enum { SY_ATTN = 0, SY_FFN = 64, SY_ABORT = L3M_SYNC_ABORT, SY_TOKEN = 208, SY_TICKET = 224, SY_HEAD_TICKET = 240,
        SY_SLOTS = 256 };
 constexpr int SY_SUMS = SY_SLOTS + 2 * L3M_MAX_HEAD_WGS;   // slice totals (sampling) follow the keys
 static_assert(L3M_SYNC_WORDS == SY_SUMS + 2 * L3M_MAX_HEAD_WGS && L3M_MAX_HEAD_WGS == 256, "keys and totals follow the flag words");
@@ -2452,17 +2434,6 @@ template <class T> __device__ __forceinline__ const T *per_iteration(const T *p)
 }
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// FFN chunk c's share of the final residual (the head's input): x = xb + the last layer's FFN partials,
-// in pro_finish's order of additions, for float4 elements [c * per, (c + 1) * per), stored through to
-// memory for the head workgroups.
-__device__ __noinline__ void reduce_final(const l3m_dmodel *Mp, int c) {
-    c = uniform(c);
-    const l3m_dmodel M = fixed(Mp);
-    const int n4 = M.dim >> 2, per = (n4 + M.n_chunks - 1) / M.n_chunks;
-    const int f = c * per + tidx();
-    if (tidx() < per && f < n4) stcoh16(M.xf, f, parts_sum_at(M.xb, M.pd, pro_geom(M, 0), f));
-}
-
 // The roles, each in a function of its own (so each gets its own register allocation and nothing of one
 // role stays live in another). They return false when the run is being abandoned.
 template <int DT, bool G2>
@@ -2529,20 +2500,11 @@ __device__ __noinline__ bool ffn_role(const l3m_dmodel *Mp, const l3m_dlayer *la
         const unsigned epoch = (unsigned)(s * nl + l);
         if (!wait_flags<0, true>(sync + SY_ATTN, M.n_groups, epoch + 1, sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
         phase(64 + ci, 1, pos, l);
-        ffn_block<DT, true, G2>(M, Lw, C, ci, wt, smem, l, pos);
-        set_flag<false>(sync + SY_FFN + ci, epoch + 1);
+        const bool through = l == nl - 1 && pos >= R.head_from;   // the head reads this layer's partials
+        ffn_block<DT, true, G2>(M, Lw, C, ci, wt, smem, l, pos, through);
+        if (through) set_flag<true>(sync + SY_FFN + ci, epoch + 1);
+        else set_flag<false>(sync + SY_FFN + ci, epoch + 1);
         phase(64 + ci, 9, pos, l);
-    }
-    const l3m_run R = fixed(per_iteration(Rp));
-    if (R.pos0 + s >= R.head_from) {
-        unsigned *sync = R.sync;
-        if (!wait_flags<1>(sync + SY_FFN, fixed(Mp).n_chunks, (unsigned)((s + 1) * nl), sync + SY_ABORT, R.spin_limit, &ok_lds))
-            return false;
-        phase_arm(R.pos0 + s, nl - 1, nl);
-        phase(64 + ci, 10, R.pos0 + s, nl - 1);
-        reduce_final(Mp, ci);
-        set_flag<true>(sync + SY_XF + ci, (unsigned)s + 1);
-        phase(64 + ci, 11, R.pos0 + s, nl - 1);
     }
     return true;
 }
@@ -2665,7 +2627,9 @@ __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, 
         pro_static(wt.st, M.dim >> 2, M.norm, nullptr, 0);
         head_issue<DT>(wt, V);
     }
-    if (!wait_flags<4>(R.sync + SY_XF, M.n_chunks, (unsigned)s + 1, R.sync + SY_ABORT, R.spin_limit, &ok_lds)) return false;
+    // the last layer's FFN flags, set once its partials are stored through (epoch (s + 1) L)
+    if (!wait_flags<4>(R.sync + SY_FFN, M.n_chunks, (unsigned)((s + 1) * M.n_layers), R.sync + SY_ABORT, R.spin_limit, &ok_lds))
+        return false;
     phase(128 + h, 1, pos, M.n_layers - 1);
     const float temp = R.temp;
     float *keep = temp > 0 ? (float *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).lgv) : nullptr;
