@@ -455,6 +455,8 @@ def main():
     ap.add_argument("--phases", default="", help="only per-phase timing of CONFIG:DTYPE:POS:LAYER (e.g. stories110M:q4_0:64:5), "
                                                 "with l3m_amd/libl3m_hip_phases.so, one JSON line")
     ap.add_argument("--only-decode", action="store_true", help="the headline decode only (for profiling runs)")
+    ap.add_argument("--matvec-only", action="store_true", help="only the matvec microbench, one JSON line (profiling runs "
+                                                               "of the matvec kernels: no decode, no persistent launch)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the plain copy kernel once over this many MiB (counter calibration under rocprofv3)")
     a = ap.parse_args()
@@ -473,6 +475,9 @@ def main():
         return
     if a.probes:
         print(json.dumps({"probes": probes(A)}), flush=True)
+        return
+    if a.matvec_only:
+        print(json.dumps({"matvec": matvec_bench(A, [s for s in a.matvec.split(",") if s], cpu_seconds=a.cpu_matvec_seconds)}), flush=True)
         return
     cfg = A.CONFIGS[a.config]
     dtype = a.dtype or cfg.dtype

@@ -75,9 +75,14 @@ typedef struct {                 // src/kernels.h:35-40
     void (*attend)(float *out, const float *q, const uint16_t *k, const uint16_t *v, int pos, int head_dim, int stride);
 } l3m_kernels;
 
-extern const l3m_kernels l3m_kernels_hip;          // name "hip"; joins TABLES / best() (kernels.h:42, dispatch.c:15-21)
-int                l3m_kernels_usable(const l3m_kernels *k);   // src/kernels.h:46, dispatch.c:23-26
-const l3m_kernels *l3m_kernels_pick(void);                     // src/kernels.h:45, dispatch.c:28-36: NULL without a GPU
+extern const l3m_kernels l3m_kernels_hip;          // name "hip"; joins the tables of src/kernels.h:42
+// 1 when a gfx950 GPU is usable from this process, else 0 (the reason in l3m_dev_error). The reference's
+// dispatcher asks it before it selects l3m_kernels_hip (dispatch.c:23-36 with two added lines: in
+// l3m_kernels_usable, `if (k == &l3m_kernels_hip) return l3m_hip_kernels_usable();`; in l3m_kernels_pick,
+// `if (want && !strcmp(want, "hip") && l3m_hip_kernels_usable()) return &l3m_kernels_hip;`), and otherwise
+// falls back to its own CPU table with its own message. This library defines no l3m_kernels_pick or
+// l3m_kernels_usable of its own, so it never shadows the dispatcher's.
+int                l3m_hip_kernels_usable(void);
 const char        *l3m_hip_last_error(void);                   // the table's sticky error (its functions return void)
 // No counterpart in the reference: l3m_kernels_hip.attend for callers that cannot allocate device memory
 // (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments
@@ -138,6 +143,26 @@ int    l3m_attention_mode(int kv_lds, int hd, int nq, int ctx);
 // holding rows 0..pos, out [nq][hd].
 int    l3m_k_attend_decode(int mode, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int nq, int nkv, int hd,
                            int ctx, int pos, void *stream);
+// One of the decode step's matvecs alone, on device pointers: form 0 the wide form of the q/k/v and
+// gate/up rows, 1 the Wo columns, 2 the Wdown columns, for a body of dtype `dtype` (m stored as the step
+// stores it: q4_0 as q8_0 blocks of the same values); 3 the head of dtype `dtype`, tpw tiles per workgroup
+// as the head workgroups take them. x: k f32 values (the step's normalized input), prepared in the kernel
+// as the step prepares it; y: m->rows floats. The same device code as the step (tile_rows, slots_rows,
+// mv with rows_sum4).
+int    l3m_k_step_mv(int dtype, int form, const l3m_dmat *m, const float *x, int k, float *y, int tpw, void *stream);
+// The same on a loaded model's own matrices (host x and y): which 0 the q/k/v rows of head group `index`
+// of layer `layer` ([q rows of its nq heads | k rows of its kv heads | v rows]), 1 its Wo columns (k = nq
+// hd), 2 the gate/up rows of FFN chunk `index` (gate row r, up row r; rows past the chunk zero), 3 its
+// Wdown columns (k = the chunk's rows), 4 the head (vocab rows). -1 on a bad index or a device error.
+int    l3m_step_matvec(const l3m_model *m, int which, int layer, int index, const float *x, float *y);
+// out[5]: head groups, FFN chunks, query heads per group, rows per chunk (the last chunk takes the rest),
+// head tiles per head workgroup. Group g holds query heads [g nq, (g + 1) nq) and kv heads
+// [g nq / hpk, ((g + 1) nq - 1) / hpk]; chunk c holds FFN rows [c rows, min((c + 1) rows, ffn)).
+void   l3m_step_layout(const l3m_model *m, int *out);
+// Host: q4_0 or mxfp4 file rows as the q8_0 file rows of the same values the step matrices hold (q4_0:
+// byte n - 8, the same f16 scale; mxfp4: the doubled e2m1 codes, d = 2^(e - 128)); dst rows * k / 32
+// blocks of 34 bytes, NULL source rows zero. -1 when an mxfp4 block does not widen exactly.
+int    l3m_widen_rows(int src_dtype, int rows, int k, const void *const *src, void *dst);
 // One streaming read of bytes (16-byte multiple) at buf: with bytes above the Infinity Cache's size it
 // evicts every cached weight (the --cold eviction, engine.c:330-338).
 int    l3m_dev_evict(const void *buf, size_t bytes, void *stream);
@@ -163,6 +188,11 @@ int    l3m_decode_timer(int mode, double *us, int *launches);
 void   l3m_decode_work(const l3m_model *m, double *out);
 double l3m_kernel_bytes(const l3m_model *m, int kind, int pos);   // weight bytes one launch of that kernel reads
 double l3m_weight_bytes(const l3m_model *m);                       // weight bytes streamed per token
+// The persistent decode kernel's longest wait, in ticks of the 100 MHz clock; ticks < 0 restores the default
+// (1 s). Past it a waiting workgroup raises the abort word, every workgroup leaves at its next wait, and
+// l3m_generate returns -1 ("a wait between phases timed out"). A test hook for that path (no counterpart in
+// the reference, whose barrier waits without bound, pool.c:111-123).
+void   l3m_decode_spin_limit(l3m_model *m, long long ticks);
 // 1 when decode runs as one persistent cooperative kernel per chunk of steps (L3M_PERSIST=0 at load
 // selects the one-graph-per-step path), 0 otherwise.
 int    l3m_decode_persistent(const l3m_model *m);

@@ -42,7 +42,7 @@ GenSpec = _struct("GenSpec", [("arch", C.c_char_p)] + [(n, C.c_int) for n in "di
                   + [("seed", C.c_uint64), ("std", C.c_float), ("norm_jitter", C.c_float), ("bos", C.c_int), ("eos", C.c_int)])
 
 # Signature table: one line per exported function, "name result arg...", in the type codes below.
-_CODES = {"v": None, "i": C.c_int, "I": C.c_int32, "w": C.c_uint16, "q": C.c_uint64, "z": C.c_size_t, "f": C.c_float,
+_CODES = {"v": None, "i": C.c_int, "I": C.c_int32, "w": C.c_uint16, "q": C.c_uint64, "l": C.c_longlong, "z": C.c_size_t, "f": C.c_float,
           "d": C.c_double, "p": C.c_void_p, "s": C.c_char_p, "*i": C.POINTER(C.c_int), "*I": _i32, "*f": _f,
           "*d": C.POINTER(C.c_double),
           "**": C.POINTER(C.c_void_p), "O": C.POINTER(Opts), "P": C.POINTER(Perf), "M": C.POINTER(DMat),
@@ -52,7 +52,7 @@ l3m_load p s O                  | l3m_free v p                   | l3m_logits *f
 l3m_generate i p *I i i f q cb p | l3m_vocab i p                 | l3m_ctx i p
 l3m_describe s p                | l3m_encode i p s i *I i        | l3m_decode p p I *i
 l3m_bos i p                     | l3m_eos i p                    | l3m_perf_read i p P
-l3m_parse_cpus i s *i i         | l3m_kernels_usable i p         | l3m_kernels_pick p
+l3m_parse_cpus i s *i i         | l3m_hip_kernels_usable i
 l3m_hip_last_error s            | l3m_dev_init i                 | l3m_dev_error s
 l3m_dev_clear_error v           | l3m_dev_name s                 | l3m_dev_alloc p z
 l3m_dev_free v p                | l3m_dev_upload i p p z         | l3m_dev_download i p p z
@@ -73,6 +73,8 @@ l3m_probe_graph_node i i i *d
 l3m_k_dequant i M i i p p       | l3m_attention_mode i i i i i   | l3m_k_attend_decode i i p p p p i i i i i p
 l3m_dev_evict i p z p           | l3m_decode_attention i p       | l3m_kv_rows i p i i i i p p
 l3m_decode_window i p
+l3m_k_step_mv i i i M p i p i p  | l3m_step_matvec i p i i i *f *f | l3m_step_layout v p *i
+l3m_widen_rows i i i i ** p | l3m_decode_spin_limit v p l
 l3m_time_read d ** i z i         | l3m_hip_attend_noalloc i p p p p i i i | l3m_phase_stamps i i i i p
 """
 _SIG = {}
@@ -220,6 +222,22 @@ class Model:
         if self._lib.l3m_logits_at(self._handle(), pos, out.ctypes.data_as(_f)) != 0:
             raise ValueError(f"no logits kept for position {pos}")
         return out
+
+    def step_layout(self):
+        """The decode step's geometry: head groups, FFN chunks, query heads per group, rows per chunk, head
+        tiles per head workgroup (l3m_step_layout)."""
+        out = (C.c_int * 5)()
+        self._lib.l3m_step_layout(self._handle(), out)
+        return dict(zip(("groups", "chunks", "nq", "chunk", "head_tpw"), out))
+
+    def step_matvec(self, which, layer, index, x, rows):
+        """One matvec of the decode step on its own stored matrix and in its own form (l3m_step_matvec):
+        which 0 q/k/v of group index, 1 its Wo, 2 gate/up of chunk index, 3 its Wdown, 4 the head."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(rows, np.float32)
+        if self._lib.l3m_step_matvec(self._handle(), which, layer, index, x.ctypes.data_as(_f), y.ctypes.data_as(_f)) != 0:
+            raise RuntimeError(f"l3m_step_matvec({which}, {layer}, {index}) failed")
+        return y
 
     def encode(self, text, bos=True):
         raw = text.encode()

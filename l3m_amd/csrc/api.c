@@ -17,6 +17,7 @@
 #define MAX_PARTS 64           // partial residual vectors a step kernel adds (head groups, FFN chunks)
 #define BODY_CUS 32            // the CUs of one MI355X XCD (256 in 8), where the persistent kernel keeps the body
 #define EVICT_BYTES (512u << 20)   // --cold: read before each forward pass, twice the 256 MiB Infinity Cache
+#define SPIN_LIMIT 100000000ull    // a wait of the persistent kernel gives up after 1 s (100 MHz ticks)
 
 struct l3m_model {
     l3m_mapped   f;
@@ -36,6 +37,7 @@ struct l3m_model {
     unsigned     lds_decode;
     unsigned    *sync;         // L3M_SYNC_WORDS flag and key words of the persistent kernel
     double       work[3];      // persistent launches so far: steps, steps with the head, K/V rows read
+    unsigned long long spin_limit;   // the persistent kernel's longest wait, 100 MHz ticks (1 s)
     int32_t     *tok_host;     // [ctx + 1]
     float       *logits;       // [vocab], host copy of the last fed position's logits
     int          logits_pos;   // position whose logits l3m_logits returns, -1 before any generate
@@ -135,22 +137,22 @@ static int mxfp4_body_widens(const l3m_mapped *f, int n_layers) {
     return 1;
 }
 
-// Uploads q4_0 or mxfp4 rows as q8_0 rows of the same values (exact; -1 if an mxfp4 block is not).
-// weight_bytes counts the source's bytes.
-static int upload_widened(l3m_model *m, l3m_dmat *out, int src_dtype, int rows, int k, const void *const *src) {
-    if ((src_dtype != L3M_Q4_0 && src_dtype != L3M_MXFP4) || k % 32) return -1;
-    size_t nb = (size_t)k / 32;
-    l3m_block_q8_0 *buf = malloc((size_t)rows * nb * sizeof *buf);
-    const void **wide = malloc((size_t)rows * sizeof *wide);
-    if (!buf || !wide) { free(buf); free(wide); return -1; }
+// q4_0 or mxfp4 file rows as q8_0 file rows of the same values (exact): q4_0 byte n - 8 with the same
+// scale; mxfp4 the doubled e2m1 codes with d = 2^(e - 128). dst holds rows * (k / 32) q8_0 blocks; a NULL
+// source row leaves its blocks zero. -1 when an mxfp4 block's scale is no f16 and its codes are not all
+// zero (it does not widen exactly), or the dtype or k do not apply.
+int l3m_widen_rows(int src_dtype, int rows, int k, const void *const *src, void *dst) {
+    if ((src_dtype != L3M_Q4_0 && src_dtype != L3M_MXFP4) || k % 32 || rows < 0) return -1;
+    const size_t nb = (size_t)k / 32;
+    l3m_block_q8_0 *buf = dst;
+    memset(buf, 0, (size_t)rows * nb * sizeof *buf);
     for (int r = 0; r < rows; r++) {
-        wide[r] = NULL;
         if (!src[r]) continue;
         l3m_block_q8_0 *o = buf + (size_t)r * nb;
         if (src_dtype == L3M_MXFP4) {
             const l3m_block_mxfp4 *in = (const l3m_block_mxfp4 *)src[r];
             for (size_t b = 0; b < nb; b++)
-                if (mxfp4_q8(in + b, o + b)) { free(buf); free(wide); return -1; }
+                if (mxfp4_q8(in + b, o + b)) return -1;
         } else {
             const l3m_block_q4_0 *in = (const l3m_block_q4_0 *)src[r];
             for (size_t b = 0; b < nb; b++) {
@@ -161,8 +163,19 @@ static int upload_widened(l3m_model *m, l3m_dmat *out, int src_dtype, int rows, 
                 }
             }
         }
-        wide[r] = o;
     }
+    return 0;
+}
+
+// Uploads q4_0 or mxfp4 rows as q8_0 rows of the same values (l3m_widen_rows; -1 if an mxfp4 block does
+// not widen exactly). weight_bytes counts the source's bytes.
+static int upload_widened(l3m_model *m, l3m_dmat *out, int src_dtype, int rows, int k, const void *const *src) {
+    if ((src_dtype != L3M_Q4_0 && src_dtype != L3M_MXFP4) || k % 32) return -1;
+    size_t nb = (size_t)k / 32;
+    l3m_block_q8_0 *buf = malloc((size_t)rows * nb * sizeof *buf);
+    const void **wide = malloc((size_t)rows * sizeof *wide);
+    if (!buf || !wide || l3m_widen_rows(src_dtype, rows, k, src, buf)) { free(buf); free(wide); return -1; }
+    for (int r = 0; r < rows; r++) wide[r] = src[r] ? buf + (size_t)r * nb : NULL;
     const double before = m->weight_bytes;
     int rc = upload_mat(m, out, L3M_Q8_0, rows, k, wide);
     m->weight_bytes = before + (double)(l3m_lt_quant_size(src_dtype, rows, k) + l3m_lt_scale_size(src_dtype, rows, k));
@@ -268,8 +281,9 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     l3m_model *m = calloc(1, sizeof *m);
     if (!m) return NULL;
     m->logits_pos = -1;
+    m->spin_limit = SPIN_LIMIT;
     if (l3m_map_open(&m->f, path)) { free(m); return NULL; }      // a bad file is reported as such first
-    if (!l3m_kernels_pick()) {
+    if (!l3m_hip_kernels_usable()) {
         fprintf(stderr, "l3m: no usable HIP device: %s\n", l3m_dev_error() ? l3m_dev_error() : "unknown");
         l3m_map_close(&m->f);
         free(m);
@@ -599,8 +613,7 @@ static int decode_launch(l3m_model *m, int first, int last, int head_from) {
     // the sync words zeroed and the launch parameters copied on the stream, behind the previous launch
     // (whose results the host has read, so run_host is free), without a wait of their own
     if (l3m_dev_zero_async(m->sync, (size_t)L3M_SYNC_WORDS * 4)) return -1;
-    const l3m_run r = {first, last - first + 1, head_from, m->head_tpw, m->n_head, m->body_xcc, m->sync, 100000000ull,   // waits end after 1 s
-                       m->temp, 0};
+    const l3m_run r = {first, last - first + 1, head_from, m->head_tpw, m->n_head, m->body_xcc, m->sync, m->spin_limit, m->temp, 0};
     *m->run_host = r;
     if (l3m_dev_upload_async(m->run_dev, m->run_host, sizeof r)) return -1;
     if (l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, m->dm_dev, m->layers_dev, m->run_dev, m->grid, m->lds_decode, NULL)) return -1;
@@ -818,3 +831,54 @@ int l3m_logits_at(const l3m_model *m, int pos, float *out) {
 void l3m_decode_work(const l3m_model *m, double *out) {
     for (int i = 0; i < 3; i++) out[i] = m->work[i];
 }
+
+// The decode step's geometry: out[0] head groups, out[1] FFN chunks, out[2] query heads per group, out[3]
+// rows per chunk (the last chunk takes what is left), out[4] head tiles per head workgroup.
+void l3m_step_layout(const l3m_model *m, int *out) {
+    const l3m_dmodel *d = &m->dm;
+    out[0] = d->n_groups;
+    out[1] = d->n_chunks;
+    out[2] = d->n_heads / d->n_groups;
+    out[3] = (d->ffn + d->n_chunks - 1) / d->n_chunks;
+    out[4] = m->persist ? m->head_tpw : d->head_tiles_per_wg;
+}
+
+// One matvec of the decode step, on the matrix the step streams and through the form it runs (a parity
+// hook; l3m_k_step_mv): which 0 the q/k/v rows of head group `index` in layer `layer`, 1 its Wo columns, 2
+// the gate/up rows of FFN chunk `index` (gate row r, up row r), 3 its Wdown columns, 4 the head. x: the
+// normalized input (host, k floats: dim, or the group's nq * hd, or the chunk's rows), y: one float per row
+// of the matrix (host). 0 on success.
+int l3m_step_matvec(const l3m_model *m, int which, int layer, int index, const float *x, float *y) {
+    const l3m_dmodel *d = &m->dm;
+    if (which < 0 || which > 4 || (which < 4 && (layer < 0 || layer >= d->n_layers))) return -1;
+    if (d->gpt2 && (which == 1 || which == 3)) return -1;     // GPT-2 sums Wo and Wdown rows by rows_sum4
+    l3m_dmat mat;
+    int k = d->dim, form = 0, dtype = d->body_dtype;
+    if (which <= 1) {
+        l3m_dgroup G;
+        if (index < 0 || index >= d->n_groups || l3m_dev_download(&G, m->layers[layer].groups + index, sizeof G)) return -1;
+        mat = which ? G.wo : G.qkv;
+        if (which) { k = G.nq * d->hd; form = 1; }
+    } else if (which <= 3) {
+        l3m_dchunk C;
+        if (index < 0 || index >= d->n_chunks || l3m_dev_download(&C, m->layers[layer].chunks + index, sizeof C)) return -1;
+        mat = which == 3 ? C.down : C.gate_up;
+        if (which == 3) { k = C.nf; form = 2; }
+    } else {
+        mat = d->head;
+        form = 3;
+        dtype = d->head.dtype;
+    }
+    float *dx = l3m_dev_alloc((size_t)k * 4), *dy = l3m_dev_alloc((size_t)mat.rows * 4);
+    int layout[5];
+    l3m_step_layout(m, layout);
+    int rc = !dx || !dy || l3m_dev_upload(dx, x, (size_t)k * 4) || l3m_k_step_mv(dtype, form, &mat, dx, k, dy, layout[4], NULL) ||
+             l3m_dev_download(y, dy, (size_t)mat.rows * 4) ? -1 : 0;
+    l3m_dev_free(dx);
+    l3m_dev_free(dy);
+    return rc;
+}
+
+// The persistent kernel's longest wait, in ticks of the 100 MHz clock (ticks < 0: the default, 1 s). A test
+// hook: with 0 every wait that has to spin gives up at once, so a launch ends through the abort path.
+void l3m_decode_spin_limit(l3m_model *m, long long ticks) { m->spin_limit = ticks < 0 ? SPIN_LIMIT : (unsigned long long)ticks; }

@@ -2142,6 +2142,55 @@ __global__ void __launch_bounds__(NTE) k_attend_decode(float *out, const float *
     for (int i = tidx(); i < nqd; i += NTE) out[i] = att[i];
 }
 
+// One of the decode step's matvecs alone, exactly as the step runs it: FORM 0 the wide form of the q/k/v
+// rows and the gate/up rows (attn_block, ffn_block: tile_rows in the quantized dtypes, mv and rows_sum4 in
+// bf16 and f32, over an input padded to whole slots), 1 the Wo columns (attn_block: mv_rows with the Wo
+// slots), 2 the Wdown columns (ffn_block: mv_rows with its slots), 3 the head rows of tiles
+// [blockIdx * tpw, + tpw) per workgroup (head_block's slice). m is stored as the step stores it (a_dtype
+// for a body of dtype DT; the head in its own dtype DT). The weights are issued first and the int8 prep of
+// x (k f32 values, the step's normalized input) follows, as in the step; y[i] for every row i of m.
+template <int DT, int FORM>
+__global__ void __launch_bounds__(NTE) k_step_mv(l3m_dmat m, const float *x, int k, float *y, int tpw) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int AT = FORM == 3 ? DT : a_dtype<DT>();
+    constexpr int NS = FORM == 0 ? nslot_a<DT>() : FORM == 1 ? nslot_wo<DT>() : FORM == 2 ? nslot_b<DT>() : nslot_h<DT>();
+    constexpr bool WIDE = FORM == 0 || FORM == 3;
+    const int tid = tidx(), kp = WIDE ? kwide(k) : kpad(k);
+    uint8_t *act = smem;
+    float *work = (float *)(smem + align16(act_size(AT, kp)));
+    int t0 = 0;
+    if constexpr (FORM == 3) {                        // the workgroup's slice, as head_slice cuts it
+        t0 = blockIdx.x * tpw;
+        const int nt = t0 + tpw <= m.tiles ? tpw : m.tiles - t0;
+        m.q += (size_t)t0 * m.nb * 16 * qbytes(AT);
+        if (sbytes(AT)) m.s += (size_t)t0 * m.nb * 16 * sbytes(AT);
+        m.rows = nt * 16 < m.rows - t0 * 16 ? nt * 16 : m.rows - t0 * 16;
+        m.tiles = nt;
+    }
+    Pref<AT, NS> pf;
+    if constexpr (WIDE) wide_issue<AT, NS>(pf, m);
+    else pref_load<AT, NS>(pf, m, 0);
+    float e[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) e[j] = 4 * tid + j < k ? x[4 * tid + j] : 0.f;
+    prep_owned<AT>(make_float4(e[0], e[1], e[2], e[3]), act, kp);
+    float *out = y + (size_t)t0 * 16;
+    if constexpr (WIDE) {
+        wide_rows<AT, NS>(pf, m, act, kp, work, m.rows, [&](int i, float v, float, bool lead) {
+            if (lead) out[i] = v;
+        });
+    } else {
+        mv_rows<AT, NS>(pf, m, act, kp, work, m.rows, [&](int i, float v, bool lead) {
+            if (lead) out[i] = v;
+        });
+    }
+}
+// Dynamic LDS of k_step_mv: the prepared input, then the per-pair results of the general form.
+inline size_t step_mv_lds(int at, int form, int k, int tiles, int nb) {
+    const int kp = form == 0 || form == 3 ? kwide(k) : kpad(k);
+    return align16(act_size(at, kp)) + work_bytes(res_bytes((size_t)tiles * nb), 0);
+}
+
 // ------------------------------------------------------------------ the graph path: one kernel per block
 
 template <int DT, bool G2 = false>
@@ -3114,7 +3163,11 @@ template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t
     hipLaunchKernelGGL(k, dim3(M.head_grid), dim3(NTE), M.lds_h, st, M, advance);
 }
 // The persistent kernel needs every workgroup resident at once: a cooperative launch, which the runtime
-// refuses (instead of starting it) when the grid does not fit.
+// refuses (instead of starting it) when the grid does not fit. L3M_COOP=0 (read once, at l3m_dev_init)
+// launches the same grid as an ordinary dispatch instead, for profiling runs: with one workgroup per CU
+// (its LDS keeps a second one off each CU) on an otherwise idle GPU every workgroup is resident, and if
+// one were not, the bounded waits would end the launch with the abort flag (an error), not a hang.
+int g_coop = 1;
 // Optional timing of the decode launches: hipEvents around each launch on its stream, collected after
 // the host has waited for it (l3m_decode_timer).
 hipEvent_t g_dec_ev[2];
@@ -3128,7 +3181,13 @@ template <int DT, int HDT, bool G2> int launch_decode(const l3m_dmodel *M_dev, c
     const l3m_run *r = R_dev;
     void *args[] = {&m, &ly, &r};
     if (g_dec_timing) CK(hipEventRecord(g_dec_ev[0], st));
-    const hipError_t e = hipLaunchCooperativeKernel((const void *)k_decode<DT, HDT, G2>, dim3(grid), dim3(NTE), args, lds, st);
+    hipError_t e;
+    if (g_coop) {
+        e = hipLaunchCooperativeKernel((const void *)k_decode<DT, HDT, G2>, dim3(grid), dim3(NTE), args, lds, st);
+    } else {
+        hipLaunchKernelGGL((k_decode<DT, HDT, G2>), dim3(grid), dim3(NTE), lds, st, m, ly, r);
+        e = hipGetLastError();
+    }
     if (e != hipSuccess) return fail("decode launch", e);
     if (g_dec_timing) {
         CK(hipEventRecord(g_dec_ev[1], st));
@@ -3145,6 +3204,19 @@ template <int DT, int HDT, bool G2> int decode_fits(int grid, unsigned lds) {
     return per_cu >= 1 && grid <= per_cu * cus;
 }
 
+template <int DT> int launch_step_mv(int form, const l3m_dmat &m, const float *x, int k, float *y, int tpw, hipStream_t st) {
+    const int at = form == 3 ? DT : a_dtype<DT>();
+    if (m.dtype != at) return fail_msg("step_mv: the matrix is not stored in the dtype this form reads");
+    const int tpb = form == 3 ? tpw : m.tiles;
+    const size_t lds = step_mv_lds(at, form, k, tpb, m.nb);
+    if (lds > g_lds_max) return fail_msg("step_mv: the matrix's per-pair results do not fit in LDS");
+    const int grid = form == 3 ? (m.tiles + tpw - 1) / tpw : 1;
+    auto kern = form == 0 ? k_step_mv<DT, 0> : form == 1 ? k_step_mv<DT, 1> : form == 2 ? k_step_mv<DT, 2> : k_step_mv<DT, 3>;
+    lds_opt_in(kern, (unsigned)lds);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NTE), lds, st, m, x, k, y, tpw);
+    CKL("k_step_mv");
+    return 0;
+}
 }  // namespace
 
 // The only device memory l3m_hip_attend_noalloc uses: the staged q, K rows, V rows and the output of one
@@ -3192,6 +3264,8 @@ int l3m_dev_init(void) {
         return fail_msg(msg);
     }
     CK(hipSetDevice(0));
+    const char *coop = getenv("L3M_COOP");
+    g_coop = !(coop && !strcmp(coop, "0"));
     CK(hipGetSymbolAddress(&g_scratch_dev[0], HIP_SYMBOL(scratch)));
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, 0) == hipSuccess && lds > 0) g_lds_max = (unsigned)lds;
@@ -3397,6 +3471,23 @@ int l3m_phase_stamps(int mode, int pos, int layer, unsigned long long *out) {
 #endif
 }
 
+int l3m_k_step_mv(int dtype, int form, const l3m_dmat *m, const float *x, int k, float *y, int tpw, void *stream) {
+    if (l3m_dev_init()) return -1;
+    if (form < 0 || form > 3 || k < 1 || k > 4 * NTE || kpad(k) / 32 != m->nb || m->tiles < 1 || m->rows > 16 * m->tiles ||
+        (form == 3 && (tpw < 1 || tpw > 64)))
+        return fail_msg("step_mv: shape out of range");
+    int rc = -1;
+    switch (dtype) {
+    case L3M_F32: rc = launch_step_mv<L3M_F32>(form, *m, x, k, y, tpw, as_stream(stream)); break;
+    case L3M_BF16: rc = launch_step_mv<L3M_BF16>(form, *m, x, k, y, tpw, as_stream(stream)); break;
+    case L3M_Q8_0: rc = launch_step_mv<L3M_Q8_0>(form, *m, x, k, y, tpw, as_stream(stream)); break;
+    case L3M_Q4_0: rc = launch_step_mv<L3M_Q4_0>(form, *m, x, k, y, tpw, as_stream(stream)); break;
+    case L3M_MXFP4: rc = launch_step_mv<L3M_MXFP4>(form, *m, x, k, y, tpw, as_stream(stream)); break;
+    default: return fail_msg("step_mv: bad dtype");
+    }
+    return rc;
+}
+
 int l3m_k_attend_decode(int mode, float *out, const float *q, const uint16_t *kc, const uint16_t *vc, int nq, int nkv, int hd, int ctx,
                         int pos, void *stream) {
     if (l3m_dev_init()) return -1;
@@ -3563,7 +3654,13 @@ int l3m_decode_placement(int grid, unsigned lds, int *xcc) {
     CK(hipMalloc(&d, (size_t)grid * 4));
     lds_opt_in(k_where, lds);
     void *args[] = {&d};
-    hipError_t e = hipLaunchCooperativeKernel((const void *)k_where, dim3(grid), dim3(NTE), args, lds, g_stream);
+    hipError_t e;
+    if (g_coop) {
+        e = hipLaunchCooperativeKernel((const void *)k_where, dim3(grid), dim3(NTE), args, lds, g_stream);
+    } else {
+        hipLaunchKernelGGL(k_where, dim3(grid), dim3(NTE), lds, g_stream, d);
+        e = hipGetLastError();
+    }
     if (e == hipSuccess) e = hipMemcpyAsync(xcc, d, (size_t)grid * 4, hipMemcpyDeviceToHost, g_stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
     (void)hipFree(d);
@@ -3641,21 +3738,33 @@ int l3m_prefill_graph(l3m_pfgraphs *g, const l3m_dmodel *M, const l3m_pflayer *L
 }
 
 // Average microseconds per launch over `iters` launches, timed with events on the library stream.
+// Mean microseconds per launch over iters launches after one untimed one: each launch between its own
+// pair of events (launches still queued back to back), so the figure is the kernel's own duration plus
+// the event markers, not the launch rate of a queue of short kernels.
 static double time_launches(int iters, int (*launch)(void *ctx, int i), void *ctx) {
-    hipEvent_t a, b;
-    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { fail_msg("hipEventCreate"); return -1; }
-    double us = -1;
-    int rc = launch(ctx, 0);                                   // untimed first launch
-    if (!rc && hipEventRecord(a, g_stream) == hipSuccess) {
-        for (int i = 0; i < iters && !rc; i++) rc = launch(ctx, i);
-        float ms = 0;
-        if (!rc && hipEventRecord(b, g_stream) == hipSuccess && hipEventSynchronize(b) == hipSuccess &&
-            hipEventElapsedTime(&ms, a, b) == hipSuccess)
-            us = 1e3 * ms / iters;
+    enum { MAX_EV = 256 };
+    hipEvent_t ev[2 * MAX_EV];
+    int made = 0, rc = 0;
+    double us_total = 0;
+    for (; made < 2 * MAX_EV && made < 2 * iters; made++)
+        if (hipEventCreate(&ev[made]) != hipSuccess) { rc = fail_msg("hipEventCreate"); break; }
+    if (!rc) rc = launch(ctx, 0);                              // untimed first launch
+    for (int i0 = 0; i0 < iters && !rc; i0 += MAX_EV) {        // in batches of at most MAX_EV launches
+        const int n = iters - i0 < MAX_EV ? iters - i0 : MAX_EV;
+        for (int j = 0; j < n && !rc; j++) {
+            if (hipEventRecord(ev[2 * j], g_stream) != hipSuccess) { rc = fail_msg("hipEventRecord"); break; }
+            rc = launch(ctx, i0 + j);
+            if (!rc && hipEventRecord(ev[2 * j + 1], g_stream) != hipSuccess) rc = fail_msg("hipEventRecord");
+        }
+        if (!rc && hipEventSynchronize(ev[2 * n - 1]) != hipSuccess) rc = fail_msg("hipEventSynchronize");
+        for (int j = 0; j < n && !rc; j++) {
+            float ms = 0;
+            if (hipEventElapsedTime(&ms, ev[2 * j], ev[2 * j + 1]) != hipSuccess) rc = fail_msg("hipEventElapsedTime");
+            us_total += 1e3 * ms;
+        }
     }
-    (void)hipEventDestroy(a);
-    (void)hipEventDestroy(b);
-    return rc ? -1 : us;
+    for (int i = 0; i < made; i++) (void)hipEventDestroy(ev[i]);
+    return rc ? -1 : us_total / iters;
 }
 
 struct GemvCtx { const l3m_dmat *mats; int n; const void *act; int k; float *y; };

@@ -186,19 +186,25 @@ class _Table(C.Structure):
 class Reference:
     """fpedd/l3m built from source (oracle/_ref): its kernel tables and its l3m.h engine."""
     PATH = HERE / "_ref" / "libl3m_ref.so"
+    # the same library with its dispatcher able to pick l3m_kernels_hip (L3M_ISA=hip), linked against
+    # libl3m_hip.so (the Makefile's _ref/libl3m_ref_hip.so)
+    HIP_PATH = HERE / "_ref" / "libl3m_ref_hip.so"
 
     @classmethod
-    def available(cls):
-        return cls.PATH.exists()
+    def available(cls, path=None):
+        return (path or cls.PATH).exists()
 
-    def __init__(self):
-        if not self.available():
-            raise OSError(f"{self.PATH} missing: build it with `make -C oracle ref` where /root/reference exists")
-        lib = self.lib = C.CDLL(str(self.PATH))
+    def __init__(self, path=None):
+        path = path or self.PATH
+        if not path.exists():
+            raise OSError(f"{path} missing: build it with `make -C oracle ref` where /root/reference exists")
+        lib = self.lib = C.CDLL(str(path))
         # the reference's l3m.h entry points share the product's ctypes structs (same ABI); the rest are its
         # internal packing and prep functions (pack.c) and the kernel tables (kernels.h)
         api = {name: l3m_amd._SIG[name] for name in ("l3m_load", "l3m_free", "l3m_generate", "l3m_logits", "l3m_vocab",
-                                                      "l3m_describe", "l3m_perf_read", "l3m_kernels_usable")}
+                                                      "l3m_describe", "l3m_perf_read")}
+        api["l3m_kernels_usable"] = (C.c_int, [C.c_void_p])           # dispatch.c:23
+        api["l3m_kernels_pick"] = (C.c_void_p, [])                    # dispatch.c:28
         internal = {
             "l3m_tile_bytes": (C.c_size_t, [C.c_int, C.c_int]),
             "l3m_row_bytes": (C.c_size_t, [C.c_int, C.c_int]),
@@ -213,6 +219,11 @@ class Reference:
 
     def usable(self, name):
         return bool(self.lib.l3m_kernels_usable(C.addressof(self.tables[name])))
+
+    def pick(self):
+        """The dispatcher's choice (dispatch.c:28-36, L3M_ISA read at the call): the table's name and address."""
+        p = self.lib.l3m_kernels_pick()
+        return _Table.from_address(p).name.decode(), p
 
     def pack_tiles(self, dtype, rows, k):
         """File rows uint8 [n, row_bytes] (n a multiple of 16, None rows allowed as zeros) -> tile bytes."""

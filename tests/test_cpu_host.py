@@ -72,7 +72,8 @@ def test_python_signatures_match_the_header():
             continue
         params, (_, codes) = split_args(args), A._SIG[name]
         kinds = ["p" if "*" in a or "(" in a else "s" for a in params]
-        want = ["s" if c in (C.c_int, C.c_int32, C.c_uint16, C.c_uint64, C.c_size_t, C.c_float, C.c_double) else "p" for c in codes]
+        want = ["s" if c in (C.c_int, C.c_int32, C.c_uint16, C.c_uint64, C.c_longlong, C.c_size_t, C.c_float, C.c_double) else "p"
+            for c in codes]
         checked += 1
         if kinds != want:
             bad.append((name, params, want))
@@ -94,8 +95,9 @@ import sys, ctypes as C
 sys.path.insert(0, {str(ROOT)!r})
 import l3m_amd as A
 lib = A.lib()
-assert not lib.l3m_kernels_pick()
-assert lib.l3m_kernels_usable(C.addressof(C.c_char.in_dll(lib, "l3m_kernels_hip"))) == 0
+assert lib.l3m_hip_kernels_usable() == 0
+assert C.c_char.in_dll(lib, "l3m_kernels_hip")                  # the table is there; the GPU is not
+assert not hasattr(lib, "l3m_kernels_pick") and not hasattr(lib, "l3m_kernels_usable")   # dispatch.c's names
 p = A.write_model({str(tmp_path / 'm.l3m')!r}, A.Config("t", 64, 1, 2, 2, 96, 300, 32, "q8_0"))
 assert not lib.l3m_load(str(p).encode(), None)
 print("no-gpu ok")
@@ -104,6 +106,64 @@ print("no-gpu ok")
     assert r.returncode == 0, r.stderr
     assert "no-gpu ok" in r.stdout
     assert "no usable HIP device" in r.stderr
+
+
+@pytest.mark.skipif(not NO_GPU, reason="checks the behaviour on a host without a GPU")
+def test_reference_dispatcher_falls_back_without_gpu():
+    """The reference's own dispatcher, built with the "hip" table (oracle/_ref/libl3m_ref_hip.so): without a
+    GPU, L3M_ISA=hip is refused with the reference's message and its best CPU table is picked
+    (dispatch.c:28-36), and l3m_kernels_usable(&l3m_kernels_hip) is 0."""
+    from oracle.oracle import Reference
+    if not Reference.available(Reference.HIP_PATH):
+        pytest.skip("oracle/_ref/libl3m_ref_hip.so was not built (no reference sources)")
+    code = f"""
+import sys, ctypes as C
+sys.path.insert(0, {str(ROOT)!r})
+from oracle.oracle import Reference, _Table
+plain = Reference()
+best, _ = plain.pick()                               # L3M_ISA unset in that library's call
+import os
+os.environ["L3M_ISA"] = "hip"
+r = Reference(Reference.HIP_PATH)
+name, addr = r.pick()
+hip = _Table.in_dll(r.lib, "l3m_kernels_hip")
+print("picked", name, "best", best, "usable", r.lib.l3m_kernels_usable(C.addressof(hip)))
+"""
+    env = dict(os.environ)
+    env.pop("L3M_ISA", None)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0, r.stderr
+    _, picked, _, best, _, usable = r.stdout.split()
+    assert picked == best and best in ("avx512", "avx2") and usable == "0", r.stdout
+    assert f"l3m: L3M_ISA=hip not available here, using {best}" in r.stderr, r.stderr
+
+
+@pytest.mark.parametrize("dtype", [Q4_0, MXFP4], ids=["q4_0", "mxfp4"])
+def test_widened_rows_dequantize_bit_exact(oracle, dtype):
+    """The q8_0 rows a q4_0 (or f16-scaled mxfp4) body's step matrices are stored as (l3m_widen_rows, the
+    host conversion of the upload) hold exactly the file blocks' values (pack.c:55-62), zero rows stay zero,
+    and an mxfp4 block whose scale 2^(e-128) is no f16 is refused unless its codes are all zero."""
+    lib = A.lib()
+    n, k = 24, 1376
+    w = rows(dtype, n, k, seed=11 + dtype)
+    if dtype == MXFP4:
+        for i in range(n):                           # the f16 range of 2^(e - 128): 104 <= e <= 143
+            w[i, 0::17] = 104 + (i * 7 + np.arange(k // 32)) % 40
+    src = [w[i] if i < n - 2 else None for i in range(n)]
+    ptrs = (C.c_void_p * n)(*[None if r is None else r.ctypes.data for r in src])
+    out = np.zeros((n, k // 32 * 34), np.uint8)
+    assert lib.l3m_widen_rows(dtype, n, k, ptrs, out.ctypes.data) == 0
+    want = oracle.dequant(dtype, w[:n - 2], k)
+    got = oracle.dequant(Q8_0, out[:n - 2], k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert not out[n - 2:].any()                     # NULL rows: zero blocks, as the step's padding rows
+    if dtype == MXFP4:
+        bad = w[:1].copy()
+        bad[0, 0] = 200                              # 2^72: no f16
+        p1 = (C.c_void_p * 1)(bad.ctypes.data)
+        assert lib.l3m_widen_rows(dtype, 1, k, p1, out.ctypes.data) == -1
+        bad[0, 1:17] = 0                             # ... unless the block's codes are all zero
+        assert lib.l3m_widen_rows(dtype, 1, k, p1, out.ctypes.data) == 0
 
 
 def test_parse_cpus():

@@ -1,16 +1,28 @@
-"""The l3m.h boundary as a drop-in: fpedd/l3m's own CLI (src/main.c, unchanged), linked against
+"""The two drop-in boundaries, each through the reference's own code.
+
+The kernel table: fpedd/l3m's library built with its dispatcher able to pick the "hip" table
+(oracle/_ref/libl3m_ref_hip.so: dispatch.c with two added lines, linked against libl3m_hip.so). With
+L3M_ISA=hip its own l3m_kernels_pick() returns l3m_kernels_hip, whose gemv and attend match its scalar
+table on its own packed tiles and prepared vectors (tests/test_kernels.c:71-149 methodology and bars),
+and its engine, loaded with L3M_ISA=hip, runs every matvec and attention through the table.
+
+The l3m.h boundary: fpedd/l3m's own CLI (src/main.c, unchanged), linked against
 libl3m_hip.so instead of its own library (oracle/Makefile target _ref/l3m-on-hip), runs on the GPU and
 passes the reference's own `check` (fast path vs its fp32 reference path: argmax agrees and KL < 0.01
 after the prompt, main.c:275-291). Its `generate` prints the same greedy text as the same CLI on the
 reference's CPU engine (oracle/_ref/l3m) for a model whose greedy tokens have no near-tie in that range.
 Both binaries are built where the reference sources exist and travel with the tree.
 """
+import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from conftest import ROOT
+from weights import BF16, F32, MXFP4, Q4_0, Q8_0, rel_err, rows
 
 pytestmark = pytest.mark.gpu
 ON_HIP = ROOT / "oracle" / "_ref" / "l3m-on-hip"
@@ -19,7 +31,8 @@ ON_CPU = ROOT / "oracle" / "_ref" / "l3m"
 
 def run(binary, *args):
     print(f"dropin: {binary.name} {' '.join(map(str, args))}", flush=True)
-    r = subprocess.run([str(binary), *map(str, args)], capture_output=True, timeout=300)
+    env = {k: v for k, v in os.environ.items() if k != "L3M_ISA"}
+    r = subprocess.run([str(binary), *map(str, args)], capture_output=True, timeout=300, env=env)
     print(r.stderr.decode(errors="replace")[-400:], flush=True)
     return r
 
@@ -50,3 +63,87 @@ def test_reference_cli_generate_matches_cpu_engine(cli, models):
     assert gpu.returncode == 0 and cpu.returncode == 0
     assert b"(hip)" in gpu.stderr or b"hip" in gpu.stderr
     assert gpu.stdout == cpu.stdout                 # the prompt and 24 greedy tokens, as raw bytes
+
+
+TOL = {F32: 1e-3, BF16: 1e-3, Q8_0: 1e-3, Q4_0: 5e-3, MXFP4: 5e-3}
+
+
+@pytest.fixture(scope="module")
+def ref_hip(monkeypatch_module):
+    from oracle.oracle import Reference
+    if not Reference.available(Reference.HIP_PATH):
+        pytest.skip("oracle/_ref/libl3m_ref_hip.so was not built (no reference sources where the tree was built)")
+    monkeypatch_module.setenv("L3M_ISA", "hip")
+    return Reference(Reference.HIP_PATH)
+
+
+@pytest.fixture(scope="module")
+def monkeypatch_module():
+    mp = pytest.MonkeyPatch()
+    yield mp
+    mp.undo()
+
+
+def test_reference_dispatcher_picks_hip_table(ref_hip):
+    import l3m_amd as A
+    from oracle.oracle import _Table
+    name, addr = ref_hip.pick()
+    print(f"dispatcher: L3M_ISA=hip picked {name}", flush=True)
+    hip = _Table.in_dll(A.lib(), "l3m_kernels_hip")
+    assert name == "hip" and addr == C.addressof(hip)
+    assert ref_hip.lib.l3m_kernels_usable(C.addressof(hip)) == 1
+    assert ref_hip.usable("scalar")                   # the CPU tables stay as they were
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, Q8_0, Q4_0, MXFP4], ids=["f32", "bf16", "q8_0", "q4_0", "mxfp4"])
+def test_picked_table_matches_scalar_table(ref_hip, dtype):
+    """gemv through the table the reference's dispatcher picked, on tiles its l3m_pack_tile packed and the
+    vector its l3m_vec_prepare prepared, against its scalar table (test_kernels.c:71-122)."""
+    from oracle.oracle import _Table
+    table = _Table.from_address(ref_hip.pick()[1])
+    for k, ntiles in [(288, 3), (768, 2), (2048, 4)]:
+        n = ntiles * 16
+        w = rows(dtype, n, k, seed=3 * k + dtype)
+        tiles = ref_hip.pack_tiles(dtype, [w[i] if i < n - 2 else None for i in range(n)], k)
+        x = np.random.default_rng(k + 1).standard_normal(k).astype(np.float32)
+        v, keep = ref_hip.prepare(dtype, x)
+        y = np.zeros(n, np.float32)
+        table.gemv[dtype](y.ctypes.data_as(C.POINTER(C.c_float)), tiles.ctypes.data, ntiles, k, C.byref(v))
+        want = ref_hip.gemv("scalar", dtype, tiles, ntiles, k, x)
+        print(f"dispatcher: gemv dtype {dtype} k {k}: rel err {rel_err(y, want):.2e}", flush=True)
+        assert rel_err(y, want) < TOL[dtype], (k, rel_err(y, want))
+    rng = np.random.default_rng(dtype)
+    hd, pos, stride = 64, 77, 192
+    q = rng.standard_normal(hd).astype(np.float32)
+    kk = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBFFF
+    vv = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBFFF
+    out = np.zeros(hd, np.float32)
+    f, u16 = C.POINTER(C.c_float), C.POINTER(C.c_uint16)
+    table.attend(out.ctypes.data_as(f), q.ctypes.data_as(f), kk.ctypes.data_as(u16), vv.ctypes.data_as(u16), pos, hd, stride)
+    assert np.abs(out - ref_hip.attend("scalar", q, kk, vv, pos, hd, stride)).max() <= 1e-5
+
+
+def test_reference_engine_runs_on_picked_table(ref_hip, models, monkeypatch_module):
+    """The reference's engine loaded with L3M_ISA=hip describes itself as (hip) and generates through the
+    table; its logits after the prompt and its greedy tokens agree with the same engine on its scalar
+    table (max |logit difference| within 1e-3 of max |logit|, the matvec bar)."""
+    import l3m_amd as A
+    cfg = A.Config("dispatch", dim=64, n_layers=2, n_heads=4, n_kv_heads=2, ffn_dim=128, vocab=320, ctx=64, dtype="q8_0")
+    path = models.get(cfg)
+    prompt = A.prompt(5, cfg.vocab, 4)
+    on_hip = ref_hip.load(path, cpus=[0, 1])
+    assert on_hip.describe().endswith("(hip)"), on_hip.describe()
+    got = on_hip.generate(prompt, 12)
+    lg = on_hip.logits()
+    monkeypatch_module.setenv("L3M_ISA", "scalar")
+    try:
+        on_cpu = ref_hip.load(path, cpus=[0, 1])
+        assert on_cpu.describe().endswith("(scalar)"), on_cpu.describe()
+        want = on_cpu.generate(prompt, 12)
+        lw = on_cpu.logits()
+    finally:
+        monkeypatch_module.setenv("L3M_ISA", "hip")
+    err = float(np.abs(lg - lw).max() / np.abs(lw).max())
+    print(f"dispatcher: engine on hip {got}\ndispatcher: engine on scalar {want}\nlogit rel err {err:.2e}", flush=True)
+    assert err < 1e-3
+    assert got == want

@@ -433,3 +433,28 @@ def test_wide_rows_take_several_slot_batches(oracle, models, monkeypatch, dtype)
     assert np.abs(lg - lo).max() <= SPREAD[dtype] * np.abs(lo).max()
     assert out["0"][0] == got
     np.testing.assert_array_equal(out["0"][1], lg)
+
+
+def test_timed_out_wait_fails_cleanly_then_recovers(models, oracle, capfd):
+    """The persistent kernel's bounded waits (its replacement for pool.c:111-123's unbounded barrier): with
+    the spin limit set from the host to 0 ticks, every wait that has to spin gives up, raises the abort word
+    and every workgroup leaves, so l3m_generate returns -1 with the message; the next generate at the normal
+    limit gives the oracle's tokens."""
+    path = models.get(SMALL)
+    m = A.Model(path)
+    if not m.persistent:
+        pytest.skip("the graph path has no waits")
+    lib = A.lib()
+    prompt = A.prompt(9, SMALL.vocab, 4)
+    print("abort path: spin limit 0", flush=True)
+    lib.l3m_decode_spin_limit(m._handle(), 0)
+    with pytest.raises(ValueError):
+        m.generate(prompt, 16)
+    err = capfd.readouterr().err
+    assert "a wait between phases timed out" in err, err
+    lib.l3m_decode_spin_limit(m._handle(), -1)
+    print("abort path: default limit", flush=True)
+    got = m.generate(prompt, 16)
+    assert got == oracle.load(path).generate(prompt, 16)
+    assert m.generate(prompt, 16) == got
+    m.close()

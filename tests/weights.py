@@ -49,3 +49,25 @@ def extremes(dtype, r, k):
 
 def rel_err(got, want):
     return float(np.abs(np.float64(got) - np.float64(want)).max() / max(np.abs(np.float64(want)).max(), 1e-30))
+
+
+def read_tensors(path):
+    """The tensors of a .l3m v1 file (src/model.h:28-57): name -> (dtype, shape, bytes as uint8 [rows, row_bytes])
+    for matrices, (dtype, shape, bytes) otherwise, and the header's dims."""
+    import struct
+    raw = np.fromfile(path, np.uint8)
+    dims = struct.unpack_from("<7I", raw, 28)
+    n_tensors, = struct.unpack_from("<I", raw, 64)
+    toc, = struct.unpack_from("<Q", raw, 72)
+    out = {}
+    for i in range(n_tensors):
+        e = toc + 120 * i
+        name = bytes(raw[e:e + 64]).split(b"\0")[0].decode()
+        dtype, ndim = struct.unpack_from("<2I", raw, e + 64)
+        shape = struct.unpack_from("<4Q", raw, e + 72)[:ndim]
+        off, nbytes = struct.unpack_from("<2Q", raw, e + 104)
+        data = raw[off:off + nbytes]
+        if ndim == 2:
+            data = data.reshape(shape[0], -1)
+        out[name] = (dtype, shape, data)
+    return out, dict(zip(("dim", "n_layers", "n_heads", "n_kv_heads", "ffn_dim", "vocab", "ctx"), dims))
