@@ -273,7 +273,9 @@ def cpu_matvec_lib():
 
 def matvec_bench(A, dtypes, iters=50, cpu_seconds=0.2):
     """Warm: one matrix re-read; cold: round robin over copies totalling > 512 MiB (beyond the 256 MB
-    Infinity Cache). Beside each, the measured roofline (a streaming read of the same bytes, warm and cold)
+    Infinity Cache). Launches run back to back and each figure is their mean interval; where the warm
+    matvec or read is within 1.5x of an empty kernel's launch interval, warm_launch_bound marks it (those
+    warm figures are the launch rate). Beside each, the measured roofline (a streaming read of the same bytes, warm and cold)
     and the reference's own matvec table (tests/test_kernels.c:151-176's method) on one core and on all."""
     import numpy as np
     sys.path.insert(0, str(ROOT / "tests"))
@@ -281,7 +283,10 @@ def matvec_bench(A, dtypes, iters=50, cpu_seconds=0.2):
     lib, dev, cpu = A.lib(), A.Device(), cpu_matvec_lib() if cpu_seconds > 0 else None
     cores = host_cores()
     arr = (C.c_int * len(cores))(*cores)
-    out = {}
+    # back-to-back launches of an empty kernel: a warm figure within 1.5x of this interval is the launch
+    # rate of a short kernel, not its duration (the committed kernel trace has the durations)
+    interval = lib.l3m_time_launch_interval(200)
+    out = {"launch_interval_us": round(interval, 3)}
     for name in dtypes:
         dt = A.DTYPES[name]
         res = {}
@@ -311,7 +316,8 @@ def matvec_bench(A, dtypes, iters=50, cpu_seconds=0.2):
                  "cold_us": round(cold, 3), "cold_GBs": round(nbytes / cold * 1e-3, 1),
                  "cold_frac_of_peak": round(nbytes / cold * 1e-3 / PEAK_HBM_GBS, 3),
                  "read_warm_GBs": round(nbytes / rwarm * 1e-3, 1), "read_cold_GBs": round(nbytes / rcold * 1e-3, 1),
-                 "warm_frac_of_read": round(rwarm / warm, 3), "cold_frac_of_read": round(rcold / cold, 3)}
+                 "warm_frac_of_read": round(rwarm / warm, 3), "cold_frac_of_read": round(rcold / cold, 3),
+                 "warm_launch_bound": bool(min(warm, rwarm) < 1.5 * interval)}
             if cpu:
                 wc = np.ascontiguousarray(w)
                 r["cpu_1core_GBs"] = round(cpu.cb_gemv_gbs(dt, n, k, wc.ctypes.data, x.ctypes.data, arr, 1, cpu_seconds), 1)

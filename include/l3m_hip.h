@@ -174,6 +174,9 @@ double l3m_bench_decode(l3m_model *m, const int32_t *prompt, int n_prompt, int n
 // The same with temperature sampling on the device (seed + i for the i-th run of the context).
 double l3m_bench_decode_t(l3m_model *m, const int32_t *prompt, int n_prompt, int n_tokens, float temperature, uint64_t seed);
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);
+// Microseconds per launch of an empty kernel queued back to back: the launch interval, below which the
+// figures of l3m_time_gemv and l3m_time_read are the launch rate, not the kernel's.
+double l3m_time_launch_interval(int iters);
 // The measured roofline beside it: one streaming read of `bytes` (a 16-byte multiple; the last 16 bytes
 // are scratch) per launch, over bufs[i % n_bufs].
 double l3m_time_read(void *const *bufs, int n_bufs, size_t bytes, int iters);

@@ -37,6 +37,7 @@ struct l3m_model {
     unsigned     lds_decode;
     unsigned    *sync;         // L3M_SYNC_WORDS flag and key words of the persistent kernel
     double       work[3];      // persistent launches so far: steps, steps with the head, K/V rows read
+    int          chunk_rows;   // FFN rows per chunk (the last chunk takes the rest)
     unsigned long long spin_limit;   // the persistent kernel's longest wait, 100 MHz ticks (1 s)
     int32_t     *tok_host;     // [ctx + 1]
     float       *logits;       // [vocab], host copy of the last fed position's logits
@@ -341,6 +342,7 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     if (ck_ && atoi(ck_) >= 32 && atoi(ck_) % 32 == 0) chunk = atoi(ck_);
     while ((d->ffn + chunk - 1) / chunk > MAX_PARTS || (d->n_groups + (d->ffn + chunk - 1) / chunk > BODY_CUS && chunk < d->ffn)) chunk += 32;
     d->n_chunks = (d->ffn + chunk - 1) / chunk;
+    m->chunk_rows = chunk;
     d->body_dtype = sdt;
     if (d->n_groups > MAX_PARTS || d->n_chunks > MAX_PARTS) return fail(m, "too many head groups or FFN chunks for the GPU kernels");
     l3m_model_layout(d);
@@ -839,7 +841,7 @@ void l3m_step_layout(const l3m_model *m, int *out) {
     out[0] = d->n_groups;
     out[1] = d->n_chunks;
     out[2] = d->n_heads / d->n_groups;
-    out[3] = (d->ffn + d->n_chunks - 1) / d->n_chunks;
+    out[3] = m->chunk_rows;
     out[4] = m->persist ? m->head_tpw : d->head_tiles_per_wg;
 }
 

@@ -3738,39 +3738,41 @@ int l3m_prefill_graph(l3m_pfgraphs *g, const l3m_dmodel *M, const l3m_pflayer *L
 }
 
 // Average microseconds per launch over `iters` launches, timed with events on the library stream.
-// Mean microseconds per launch over iters launches after one untimed one: each launch between its own
-// pair of events (launches still queued back to back), so the figure is the kernel's own duration plus
-// the event markers, not the launch rate of a queue of short kernels.
+// Mean microseconds per launch of iters launches queued back to back, after one untimed launch: one pair
+// of events around them all (events around each launch would add their own markers' time to every
+// figure). For a kernel shorter than the launch interval (l3m_time_launch_interval) this is the launch rate.
 static double time_launches(int iters, int (*launch)(void *ctx, int i), void *ctx) {
-    enum { MAX_EV = 256 };
-    hipEvent_t ev[2 * MAX_EV];
-    int made = 0, rc = 0;
-    double us_total = 0;
-    for (; made < 2 * MAX_EV && made < 2 * iters; made++)
-        if (hipEventCreate(&ev[made]) != hipSuccess) { rc = fail_msg("hipEventCreate"); break; }
-    if (!rc) rc = launch(ctx, 0);                              // untimed first launch
-    for (int i0 = 0; i0 < iters && !rc; i0 += MAX_EV) {        // in batches of at most MAX_EV launches
-        const int n = iters - i0 < MAX_EV ? iters - i0 : MAX_EV;
-        for (int j = 0; j < n && !rc; j++) {
-            if (hipEventRecord(ev[2 * j], g_stream) != hipSuccess) { rc = fail_msg("hipEventRecord"); break; }
-            rc = launch(ctx, i0 + j);
-            if (!rc && hipEventRecord(ev[2 * j + 1], g_stream) != hipSuccess) rc = fail_msg("hipEventRecord");
-        }
-        if (!rc && hipEventSynchronize(ev[2 * n - 1]) != hipSuccess) rc = fail_msg("hipEventSynchronize");
-        for (int j = 0; j < n && !rc; j++) {
-            float ms = 0;
-            if (hipEventElapsedTime(&ms, ev[2 * j], ev[2 * j + 1]) != hipSuccess) rc = fail_msg("hipEventElapsedTime");
-            us_total += 1e3 * ms;
-        }
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { fail_msg("hipEventCreate"); return -1; }
+    double us = -1;
+    int rc = launch(ctx, 0);                                   // untimed first launch
+    if (!rc && hipEventRecord(a, g_stream) == hipSuccess) {
+        for (int i = 0; i < iters && !rc; i++) rc = launch(ctx, i);
+        float ms = 0;
+        if (!rc && hipEventRecord(b, g_stream) == hipSuccess && hipEventSynchronize(b) == hipSuccess &&
+            hipEventElapsedTime(&ms, a, b) == hipSuccess)
+            us = 1e3 * ms / iters;
     }
-    for (int i = 0; i < made; i++) (void)hipEventDestroy(ev[i]);
-    return rc ? -1 : us_total / iters;
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return rc ? -1 : us;
+}
+
+static int dummy_one(void *, int) {
+    hipLaunchKernelGGL(k_dummy, dim3(1), dim3(NT), 0, g_stream);
+    CKL("k_dummy");
+    return 0;
 }
 
 struct GemvCtx { const l3m_dmat *mats; int n; const void *act; int k; float *y; };
 static int gemv_one(void *c, int i) {
     GemvCtx *g = (GemvCtx *)c;
     return l3m_k_gemv(&g->mats[i % g->n], g->act, g->k, g->y, g_stream);
+}
+
+double l3m_time_launch_interval(int iters) {
+    if (l3m_dev_init() || iters < 1) return -1;
+    return time_launches(iters, dummy_one, nullptr);
 }
 
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters) {

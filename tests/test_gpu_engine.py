@@ -52,6 +52,17 @@ SPREAD = {"bf16": 1e-3, "f32": 1e-4, "q8_0": 0.02, "q4_0": 0.02, "mxfp4": 0.02}
 # A greedy step whose top-2 margin in the reference is under 0.5% of max|logit| is a near-tie: the
 # reference's own avx512 table leaves its scalar table exactly there on stories110M q4_0 (step 33).
 NEAR_TIE = 0.005
+# Free-running greedy steps (of 64) equal to the reference scalar engine's, as measured on the MI355X for
+# each golden configuration (the decode is deterministic: fixed reduction orders). The reference's own
+# avx512 table agrees with its scalar table for 64, 64, 33, 54 and 64 steps (simd_agree); SmolLM2 q8_0 parts
+# at step 49, past its first near-tie (47). The reference's `check` reports the same count (main.c:295-300).
+FREE_RUN_AGREE = {("stories15M", "bf16"): 64, ("stories42M", "q8_0"): 64, ("stories110M", "q4_0"): 64,
+                  ("smollm2", "q8_0"): 49, ("smollm2", "mxfp4"): 64}
+# The teacher-forced logits bar, as a multiple of the reference's own SIMD spread on the model (its avx512
+# table against its scalar table fed the same tokens, simd_spread): the GPU's worst deviation from the
+# scalar table over the 64 steps is 1.05, 1.02, 1.54, 1.08 and 0.96 times that spread (stories15M,
+# stories42M, stories110M, SmolLM2 q8_0, SmolLM2 mxfp4; with or without the batched prefill).
+TF_SPREAD_FACTOR = 1.6
 
 
 @pytest.mark.parametrize("i", range(5))
@@ -60,14 +71,15 @@ def test_greedy_tokens_match_reference(golden_cases, oracle, i):
     print(f"case {c['config']} {c['dtype']}", flush=True)
     m = A.Model(path)
     toks = m.generate(c["prompt"], len(c["scalar_tokens"]))
-    # Identical through the first near-tie: a step whose top-2 margin in the reference is inside the
-    # activation-quantization spread may legitimately go either way (the reference's own SIMD table
-    # leaves its scalar table at such steps, recorded as simd_agree).
+    # Identical through the first near-tie at least (a step whose top-2 margin in the reference is inside
+    # the activation-quantization spread may legitimately go either way: the reference's own SIMD table
+    # leaves its scalar table at such steps, recorded as simd_agree), and for as many steps as measured.
     ties = [i for i, mg in enumerate(c["scalar_margins"]) if mg < NEAR_TIE]
     must = ties[0] if ties else len(toks)
     agree = next((i for i, (a, b) in enumerate(zip(toks, c["scalar_tokens"])) if a != b), len(toks))
     print(f"greedy agreement {agree} of {len(toks)} (first near-tie at {must}, reference SIMD agrees {c['simd_agree']})", flush=True)
     assert agree >= must
+    assert agree >= FREE_RUN_AGREE[(c["config"], c["dtype"])]
     m.generate(c["prompt"], 0)
     lg = m.logits
     om = oracle.load(path)
@@ -109,11 +121,11 @@ def test_teacher_forced_golden_steps(golden_cases, oracle, monkeypatch, i, prefi
     m, om = A.Model(path), oracle.load(path)
     assert m.attention_mode == GOLDEN_ATTENTION[c["config"]], m.attention_mode
     prompt, ref, tie = c["prompt"], c["scalar_tokens"], c["simd_spread"]
-    # the logits bar at every step: the engine bar, or twice the reference's own SIMD spread, whichever is
-    # looser. The spread is the largest of 64 steps' max over the vocabulary of |avx512 - scalar|; the GPU
-    # adds in a third order, so its largest deviation from the scalar table is of the same kind and may be
-    # up to twice that (bf16 activations round too: the avx512 table is 2.4e-3 from scalar on stories15M)
-    bar = max(SPREAD[c["dtype"]], 2 * tie)
+    # the logits bar at every step: TF_SPREAD_FACTOR times the reference's own SIMD spread (the largest of
+    # 64 steps' max over the vocabulary of |avx512 - scalar|). The GPU adds in a third order, so its largest
+    # deviation from the scalar table is of the same kind (bf16 activations round too: the avx512 table is
+    # 2.4e-3 from scalar on stories15M, above the 1e-3 of the bf16 engine bar)
+    bar = TF_SPREAD_FACTOR * tie
     got, bad, worst, prefilled = [], [], (0.0, 0.0), 0
     for pos in range(len(prompt) - 1):
         om.forward(prompt[pos], pos, logits=False)

@@ -9,7 +9,9 @@ through exactly the device code the step runs it with, the int8 prep of the inpu
 compared here with the oracle's gemv of the file's own rows (kernels_scalar.c:19-75, the reference's
 per-block formula): within 1e-3 of max|y| for bf16 and q8_0 and 5e-3 for q4_0 and mxfp4 (the north star's
 bars, tests/test_kernels.c:114 measures against double the same way). With the same prepared input the two
-differ only in the order of the fp32 additions of block sums, so the error is also held to 1e-5.
+differ only in the order of the fp32 additions of block sums: the largest error measured over every group,
+chunk and head of the first and last layers of all six cases is 4.4e-7 of max|y| (stories15M's head), so
+the error is also held to 1e-6.
 """
 import numpy as np
 import pytest
@@ -19,7 +21,7 @@ from weights import read_tensors, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = {"f32": 1e-3, "bf16": 1e-3, "q8_0": 1e-3, "q4_0": 5e-3, "mxfp4": 5e-3}
-ORDER_ONLY = 1e-5
+ORDER_ONLY = 1e-6
 CASES = [("stories15M", "bf16", None), ("stories42M", "q8_0", None), ("stories110M", "q4_0", None),
          ("smollm2", "q8_0", None), ("smollm2", "mxfp4", None), ("smollm2", "mxfp4", "0")]
 
