@@ -344,6 +344,20 @@ def sampled_rate(A, m, prompt, n_tokens, temperature=1.0):
     return {"temperature": temperature, "value": round(1e9 / ns, 1) if ns > 0 else None, "unit": "tok/s"}
 
 
+def streamed_rate(A, m, prompt, n_tokens):
+    """Tokens/s of greedy generate calls with an on_token callback (tokens handed over as they come: runs of
+    8 positions, two in flight), restarting at a full context; a side figure beside the headline's runs of
+    up to 128 positions. The Python callback's own cost per token is included."""
+    m.generate(prompt, 16, on_token=lambda t: True)
+    t0, done = time.perf_counter(), 0
+    while done < n_tokens:
+        got = m.generate(prompt, min(n_tokens - done, m.ctx - len(prompt)), on_token=lambda t: True)
+        if not got:
+            break
+        done += len(got)
+    return {"value": round(done / (time.perf_counter() - t0), 1), "unit": "tok/s", "tokens": done}
+
+
 def cold_rate(A, path, prompt, n_tokens):
     """Tokens/s with the caches emptied of the weights before every forward pass (--cold, engine.c:330-338),
     the eviction not counted: a side figure (README.md:46-47 reports 6-8x slower on the CPU)."""
@@ -509,6 +523,9 @@ def main():
             sampled = sampled_rate(A, m, prompt, a.steps, a.sample_temp) if a.sample_temp > 0 and not a.only_decode else None
             if sampled:
                 log(f"bench: sampled at T={sampled['temperature']}: {sampled['value']} tok/s")
+            streamed = streamed_rate(A, m, prompt, max(a.steps, N_TOKENS)) if not a.only_decode else None
+            if streamed:
+                log(f"bench: streamed to on_token: {streamed['value']} tok/s")
         cold = cold_rate(A, path, prompt, min(a.steps, 64)) if a.cold and not a.only_decode else None
         if cold:
             log(f"bench: --cold {cold['value']} tok/s")
@@ -552,6 +569,7 @@ def main():
         "decode": decode,
         "matvec": matvec,
         "sampled_decode": sampled,
+        "streamed_decode": streamed,
         "cold_decode": cold,
         "cpu_baseline": cpu,
     }

@@ -18,6 +18,14 @@
 #define BODY_CUS 32            // the CUs of one MI355X XCD (256 in 8), where the persistent kernel keeps the body
 #define EVICT_BYTES (512u << 20)   // --cold: read before each forward pass, twice the 256 MiB Infinity Cache
 #define SPIN_LIMIT 100000000ull    // a wait of the persistent kernel gives up after 1 s (100 MHz ticks)
+#define LIVE_STEPS 8               // positions per run of steps when each token is handed over as it comes
+
+// What the host reads back after a run of steps: the persistent launch's abort word, and the tokens the run
+// produced (in order from its first position with a token).
+typedef struct {
+    unsigned abort;
+    int32_t  tok[NSLOTS];
+} l3m_chunk_out;
 
 struct l3m_model {
     l3m_mapped   f;
@@ -30,16 +38,20 @@ struct l3m_model {
     l3m_graphs  *graphs;
     l3m_dlayer  *layers_dev;   // the layer descriptors in device memory (persistent kernel)
     l3m_dmodel  *dm_dev;       // dm in device memory
-    l3m_run     *run_dev;      // the persistent kernel's launch parameters
-    l3m_run     *run_host;     // their pinned host copy (queued to run_dev without a wait)
+    l3m_run     *run_dev;      // [2] the persistent kernel's launch parameters, one per run of steps in flight
+    l3m_run     *run_host;     // [2] their pinned host copies (queued to run_dev without a wait)
+    l3m_chunk_out *out_host;   // [2] pinned: what each run of steps in flight hands back
+    void        *ev[2];        // the end of each run of steps in flight (its copies back included)
+    int32_t     *stage_tok;    // pinned [ctx + 1]: the call's prompt ids, queued to the device without a wait
+    l3m_dsample *stage_smp;    // pinned: the call's sampler state
+    int         *stage_pos;    // pinned: the call's first decoded position
     int          persist;      // decode with the persistent kernel (else one graph per step)
     int          grid, head_tpw, n_head, body_xcc;
     unsigned     lds_decode;
-    unsigned    *sync;         // L3M_SYNC_WORDS flag and key words of the persistent kernel
+    unsigned    *sync;         // 2 areas of L3M_SYNC_WORDS flag and key words of the persistent kernel (per run in flight)
     double       work[3];      // persistent launches so far: steps, steps with the head, K/V rows read
     int          chunk_rows;   // FFN rows per chunk (the last chunk takes the rest)
     unsigned long long spin_limit;   // the persistent kernel's longest wait, 100 MHz ticks (1 s)
-    int32_t     *tok_host;     // [ctx + 1]
     float       *logits;       // [vocab], host copy of the last fed position's logits
     int          logits_pos;   // position whose logits l3m_logits returns, -1 before any generate
     float        temp;         // the running generate call's temperature (0: greedy)
@@ -556,9 +568,15 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     int parts = d->head_grid > m->grid ? d->head_grid : m->grid;
     d->part_val = dalloc(m, (size_t)parts * 4);
     d->part_idx = dalloc(m, (size_t)parts * 4);
-    m->sync = dalloc(m, (size_t)L3M_SYNC_WORDS * 4);
-    m->run_dev = dalloc(m, sizeof(l3m_run));
-    m->run_host = l3m_dev_host_alloc(sizeof(l3m_run));
+    m->sync = dalloc(m, 2 * (size_t)L3M_SYNC_WORDS * 4);
+    m->run_dev = dalloc(m, 2 * sizeof(l3m_run));
+    m->run_host = l3m_dev_host_alloc(2 * sizeof(l3m_run));
+    m->out_host = l3m_dev_host_alloc(2 * sizeof(l3m_chunk_out));
+    m->stage_tok = l3m_dev_host_alloc(((size_t)d->ctx + 1) * 4);
+    m->stage_smp = l3m_dev_host_alloc(sizeof(l3m_dsample));
+    m->stage_pos = l3m_dev_host_alloc(sizeof(int));
+    m->ev[0] = l3m_dev_event_new();
+    m->ev[1] = l3m_dev_event_new();
     m->dm_dev = dalloc(m, sizeof(l3m_dmodel));
     m->layers_dev = dupload(m, m->layers, (size_t)d->n_layers * sizeof *m->layers);
     d->done = dalloc(m, 4);
@@ -568,10 +586,10 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     if (rope) l3m_rope_table(rope, d->ctx, d->hd, h->rope_theta);
     d->rope = rope ? dupload(m, rope, (size_t)d->ctx * d->hd * sizeof(float)) : NULL;
     free(rope);
-    m->tok_host = calloc((size_t)d->ctx + 1, sizeof *m->tok_host);
     m->logits = calloc((size_t)d->vocab, sizeof *m->logits);
     if (!d->pos || !d->tokens || !d->xa || !d->xb || !d->po || !d->pd || !d->samp || !d->logits || !d->part_val || !d->part_idx || !d->done ||
-        !d->kc || !d->vc || !d->rope || !d->norm || !m->tok_host || !m->logits || !m->sync || !m->layers_dev || !m->run_dev || !m->run_host ||
+        !d->kc || !d->vc || !d->rope || !d->norm || !m->logits || !m->sync || !m->layers_dev || !m->run_dev || !m->run_host ||
+        !m->out_host || !m->stage_tok || !m->stage_smp || !m->stage_pos || !m->ev[0] || !m->ev[1] ||
         !m->dm_dev || l3m_dev_upload(m->dm_dev, d, sizeof *d))
         return fail(m, "device allocation failed");
     m->cold = o.cold != 0;
@@ -602,39 +620,63 @@ void l3m_free(l3m_model *m) {
     l3m_graphs_free(m->graphs);
     l3m_pfgraphs_free(m->pfg);
     l3m_dev_host_free(m->run_host);
+    l3m_dev_host_free(m->out_host);
+    l3m_dev_host_free(m->stage_tok);
+    l3m_dev_host_free(m->stage_smp);
+    l3m_dev_host_free(m->stage_pos);
+    l3m_dev_event_free(m->ev[0]);
+    l3m_dev_event_free(m->ev[1]);
     for (int i = 0; i < m->n_allocs; i++) l3m_dev_free(m->allocs[i]);
-    free(m->allocs); free(m->layers); free(m->tok_host); free(m->logits); free(m->pf);
+    free(m->allocs); free(m->layers); free(m->logits); free(m->pf);
     if (m->f.map) l3m_map_close(&m->f);
     free(m);
 }
 
-// Positions first..last in one launch of the persistent kernel; -1 on a device error or a timed-out wait.
-static int decode_launch(l3m_model *m, int first, int last, int head_from) {
+static int step(l3m_model *m, int with_head) {
+    return m->graphs ? l3m_graphs_launch(m->graphs, with_head, NULL) : l3m_step_enqueue(&m->dm, m->layers, with_head, NULL);
+}
+
+// Positions first..last queued as one run of steps (one persistent launch, or one graph per step; logits
+// and a token from head_from on), then the copies of what the host reads back (the launch's abort word, the
+// run's tokens) into slot's pinned area, then slot's event. Nothing waits: two runs can be in flight, each
+// with its own sync area, launch parameters and pinned area. The sync words are zeroed and the parameters
+// copied on the stream, behind the run that used slot before (which the host has waited for).
+static int chunk_enqueue(l3m_model *m, int first, int last, int head_from, int slot) {
     const l3m_dmodel *d = &m->dm;
-    unsigned abort_flag = 0;
-    // the sync words zeroed and the launch parameters copied on the stream, behind the previous launch
-    // (whose results the host has read, so run_host is free), without a wait of their own
-    if (l3m_dev_zero_async(m->sync, (size_t)L3M_SYNC_WORDS * 4)) return -1;
-    const l3m_run r = {first, last - first + 1, head_from, m->head_tpw, m->n_head, m->body_xcc, m->sync, m->spin_limit, m->temp, 0};
-    *m->run_host = r;
-    if (l3m_dev_upload_async(m->run_dev, m->run_host, sizeof r)) return -1;
-    if (l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, m->dm_dev, m->layers_dev, m->run_dev, m->grid, m->lds_decode, NULL)) return -1;
-    if (l3m_dev_download(&abort_flag, m->sync + L3M_SYNC_ABORT, 4)) return -1;
-    if (l3m_decode_timer(2, NULL, NULL)) return -1;
-    for (int p = first; p <= last; p++) {
-        m->work[0] += 1;
-        m->work[1] += p >= head_from;
-        m->work[2] += p + 1;                           // attention reads K, V rows 0..p of every kv head
+    l3m_chunk_out *out = &m->out_host[slot];
+    if (m->persist) {
+        unsigned *sync = m->sync + (size_t)slot * L3M_SYNC_WORDS;
+        if (l3m_dev_zero_async(sync, (size_t)L3M_SYNC_WORDS * 4)) return -1;
+        const l3m_run r = {first, last - first + 1, head_from, m->head_tpw, m->n_head, m->body_xcc, sync, m->spin_limit, m->temp, 0};
+        m->run_host[slot] = r;
+        if (l3m_dev_upload_async(m->run_dev + slot, m->run_host + slot, sizeof r) ||
+            l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, m->dm_dev, m->layers_dev, m->run_dev + slot, m->grid, m->lds_decode, NULL,
+                              slot) ||
+            l3m_dev_download_async(&out->abort, sync + L3M_SYNC_ABORT, 4))
+            return -1;
+        for (int p = first; p <= last; p++) {
+            m->work[0] += 1;
+            m->work[1] += p >= head_from;
+            m->work[2] += p + 1;                       // attention reads K, V rows 0..p of every kv head
+        }
+    } else {
+        out->abort = 0;
+        for (int p = first; p <= last; p++)
+            if (step(m, p >= head_from)) return -1;
     }
-    if (abort_flag) {
+    const int f = first > head_from ? first : head_from;
+    if (last >= f && l3m_dev_download_async(out->tok, d->tokens + f + 1, (size_t)(last - f + 1) * 4)) return -1;
+    return l3m_dev_event_record(m->ev[slot]);
+}
+
+// Waits for slot's run of steps; -1 on a device error or a timed-out wait of the persistent kernel.
+static int chunk_finish(l3m_model *m, int slot) {
+    if (l3m_dev_event_wait(m->ev[slot]) || (m->persist && l3m_decode_timer_collect(slot))) return -1;
+    if (m->out_host[slot].abort) {
         fprintf(stderr, "l3m: decode kernel: a wait between phases timed out\n");
         return -1;
     }
     return 0;
-}
-
-static int step(l3m_model *m, int with_head) {
-    return m->graphs ? l3m_graphs_launch(m->graphs, with_head, NULL) : l3m_step_enqueue(&m->dm, m->layers, with_head, NULL);
 }
 
 // --cold (engine.c:330-338): the caches are emptied of the weights before a forward pass; the eviction is
@@ -650,19 +692,29 @@ static int evict(l3m_model *m) {
 }
 
 // Run forward passes for positions 0..last (prompt, then greedy or sampled tokens); calls back per the
-// reference's rules. temperature > 0 samples on the device from the generator seeded as engine.c:555
-// does. Returns the number generated, or -1 on a device error.
+// reference's rules (engine.c:322-327, 342-362). temperature > 0 samples on the device from the generator
+// seeded as engine.c:555 does. Returns the number generated, or -1 on a device error.
+//
+// The passes run in runs of steps queued on the stream, and the host reads each run's tokens back once it
+// has finished. When something can stop the generation early (an on_token callback, or an EOS or BOS id
+// the model has), the tokens are handed over as they come: the prompt's run ends at the first generated
+// token, the later runs are LIVE_STEPS positions long, and two are kept in flight, so the next run computes
+// while the host calls on_token for the last one's tokens; a stop leaves at most the rest of its run and the
+// run behind it (under 2 LIVE_STEPS passes) computed in vain. Otherwise runs are NSLOTS positions long.
 static int run(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, float temperature, uint64_t seed,
                int (*on_token)(int32_t, void *), void *user) {
     l3m_dmodel *d = &m->dm;
-    int bos = m->f.tok.bos, eos = m->f.tok.eos;
-    int last = n_prompt - 1 + max_new < d->ctx - 1 ? n_prompt - 1 + max_new : d->ctx - 1;   // exhausted() at engine.c:322
-    int n_gen = 0, stop = -1;
-    l3m_dsample smp = {0};
-    smp.temp = temperature > 0 ? temperature : 0.0f;
-    for (int h = 0; h < L3M_MAX_HEAD_WGS; h++) smp.rng[h] = seed * 0x9E3779B97F4A7C15ull + 1;   // engine.c:555
-    m->temp = smp.temp;
-    if (l3m_dev_upload(d->tokens, prompt, (size_t)n_prompt * 4) || l3m_dev_upload(d->samp, &smp, sizeof smp)) return -1;
+    const int bos = m->f.tok.bos, eos = m->f.tok.eos;
+    const int last = n_prompt - 1 + max_new < d->ctx - 1 ? n_prompt - 1 + max_new : d->ctx - 1;   // exhausted() at engine.c:322
+    int n_gen = 0, stop = -1, rc = 0;
+    l3m_dsample *smp = m->stage_smp;
+    memset(smp, 0, sizeof *smp);
+    smp->temp = temperature > 0 ? temperature : 0.0f;
+    for (int h = 0; h < L3M_MAX_HEAD_WGS; h++) smp->rng[h] = seed * 0x9E3779B97F4A7C15ull + 1;   // engine.c:555
+    m->temp = smp->temp;
+    memcpy(m->stage_tok, prompt, (size_t)n_prompt * 4);
+    // the pinned stage was last read by the previous call's copies, which its final wait covered
+    if (l3m_dev_upload_async(d->tokens, m->stage_tok, (size_t)n_prompt * 4) || l3m_dev_upload_async(d->samp, smp, sizeof *smp)) return -1;
     // a long prompt: positions 0..n_prompt-2 in one batched pass, then decode from the last prompt token
     int next = 0;
     m->prefilled = 0;
@@ -672,31 +724,39 @@ static int run(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, f
             return -1;
         next = m->prefilled = n_prompt - 1;
     }
-    if (l3m_dev_upload(d->pos, &next, 4)) return -1;
-    for (; next <= last && stop < 0;) {
-        int end = next + NSLOTS - 1 < last ? next + NSLOTS - 1 : last;
-        if (m->cold) {                                 // one forward pass per launch, each after an eviction
-            for (int p = next; p <= end; p++)
-                if (evict(m) || (m->persist ? decode_launch(m, p, p, n_prompt - 1) : step(m, p >= n_prompt - 1))) return -1;
-        } else if (m->persist) {
-            if (decode_launch(m, next, end, n_prompt - 1)) return -1;
-        } else {
-            for (int p = next; p <= end; p++)
-                if (step(m, p >= n_prompt - 1)) return -1;
+    *m->stage_pos = next;
+    if (l3m_dev_upload_async(d->pos, m->stage_pos, 4)) return -1;
+    const int live = on_token != NULL || bos >= 0 || eos >= 0, depth = live && !m->cold ? 2 : 1;
+    int q_first[2], q_end[2], q_slot[2], nq = 0, slot = 0;
+    for (;;) {
+        while (!rc && stop < 0 && next <= last && nq < depth) {
+            // --cold: one forward pass per run, each after an eviction
+            int len = m->cold ? 1 : !live ? NSLOTS : next <= n_prompt - 1 ? n_prompt - next : LIVE_STEPS;
+            if (len > NSLOTS) len = NSLOTS;
+            const int end = next + len - 1 < last ? next + len - 1 : last;
+            if ((m->cold && evict(m)) || chunk_enqueue(m, next, end, n_prompt - 1, slot)) {
+                rc = -1;
+                break;
+            }
+            q_first[nq] = next; q_end[nq] = end; q_slot[nq] = slot; nq++;
+            slot ^= 1;
+            next = end + 1;
         }
-        int first = next > n_prompt - 1 ? next : n_prompt - 1;
-        if (end >= first) {
-            if (l3m_dev_download(m->tok_host + first + 1, d->tokens + first + 1, (size_t)(end - first + 1) * 4)) return -1;
-        } else if (l3m_dev_sync()) return -1;
-        for (int p = first; p <= end && p < last; p++) {
-            int32_t tok = m->tok_host[p + 1];
+        if (!nq) break;
+        const int first = q_first[0], end = q_end[0], s = q_slot[0];
+        q_first[0] = q_first[1]; q_end[0] = q_end[1]; q_slot[0] = q_slot[1];
+        nq--;
+        if (chunk_finish(m, s)) rc = -1;               // the runs still in flight are waited for all the same
+        if (rc || stop >= 0) continue;
+        const int f = first > n_prompt - 1 ? first : n_prompt - 1;
+        for (int p = f; p <= end && p < last; p++) {
+            const int32_t tok = m->out_host[s].tok[p - f];
             if (tok == eos || tok == bos) { stop = p; break; }                 // accepted(), engine.c:323-327
             n_gen++;
             if (on_token && !on_token(tok, user)) { stop = p; break; }
         }
-        next = end + 1;
     }
-    if (l3m_dev_sync()) return -1;
+    if (l3m_dev_sync() || rc) return -1;
     m->logits_pos = stop >= 0 ? stop : last;
     m->logits_fresh = 0;
     m->tokens += m->logits_pos + 1;

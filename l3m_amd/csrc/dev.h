@@ -178,8 +178,18 @@ int l3m_decode_placement(int grid, unsigned lds, int *xcc);
 int l3m_decode_pair(int dtype, int head_dtype, int gpt2);    // 1 if the kernel is built for this (body, head, variant)
 int l3m_decode_fits(int dtype, int head_dtype, int gpt2, int grid, unsigned lds);   // 1 if grid workgroups with lds bytes can all be resident
 // m_dev, layers_dev, r_dev: device-memory copies (the kernel reads its parameters from there)
+// slot (0 or 1): which of the two launches that may be in flight at once this is (its timing events).
 int l3m_decode_launch(int dtype, int head_dtype, int gpt2, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev, int grid,
-                      unsigned lds, void *stream);
+                      unsigned lds, void *stream, int slot);
+// Adds slot's finished launch to l3m_decode_timer's total (after its stream work has been waited for).
+int l3m_decode_timer_collect(int slot);
+// Stream-ordered transfers and events on the library stream, for work kept in flight: a copy into pinned
+// host memory without a wait; events (no timing) to wait for a point of the stream.
+int   l3m_dev_download_async(void *dst_pinned, const void *src, size_t bytes);
+void *l3m_dev_event_new(void);
+void  l3m_dev_event_free(void *e);
+int   l3m_dev_event_record(void *e);
+int   l3m_dev_event_wait(void *e);
 
 // Timing (microseconds per launch, hipEvents on the library stream, after one untimed launch).
 double l3m_time_gemv(const l3m_dmat *mats, int n_mats, const void *act, int k, float *y, int iters);

@@ -3170,17 +3170,24 @@ template <int DT> void launch_head(const l3m_dmodel &M, int advance, hipStream_t
 int g_coop = 1;
 // Optional timing of the decode launches: hipEvents around each launch on its stream, collected after
 // the host has waited for it (l3m_decode_timer).
-hipEvent_t g_dec_ev[2];
-int g_dec_timing, g_dec_launches, g_dec_pending;
+// Each of the (at most two) launches in flight has its own pair of events (slot).
+hipEvent_t g_dec_ev[2][2];
+int g_dec_timing, g_dec_launches, g_dec_pending[2];
 double g_dec_us;
 template <int DT, int HDT, bool G2> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *layers, const l3m_run *R_dev, int grid,
-                                                      unsigned lds, hipStream_t st) {
+                                                      unsigned lds, hipStream_t st, int slot) {
     lds_opt_in(k_decode<DT, HDT, G2>, lds);
     const l3m_dmodel *m = M_dev;
     const l3m_dlayer *ly = layers;
     const l3m_run *r = R_dev;
     void *args[] = {&m, &ly, &r};
-    if (g_dec_timing) CK(hipEventRecord(g_dec_ev[0], st));
+    if (g_dec_timing) {
+        if (!g_dec_ev[slot][0]) {
+            CK(hipEventCreate(&g_dec_ev[slot][0]));
+            CK(hipEventCreate(&g_dec_ev[slot][1]));
+        }
+        CK(hipEventRecord(g_dec_ev[slot][0], st));
+    }
     hipError_t e;
     if (g_coop) {
         e = hipLaunchCooperativeKernel((const void *)k_decode<DT, HDT, G2>, dim3(grid), dim3(NTE), args, lds, st);
@@ -3190,8 +3197,8 @@ template <int DT, int HDT, bool G2> int launch_decode(const l3m_dmodel *M_dev, c
     }
     if (e != hipSuccess) return fail("decode launch", e);
     if (g_dec_timing) {
-        CK(hipEventRecord(g_dec_ev[1], st));
-        g_dec_pending = 1;
+        CK(hipEventRecord(g_dec_ev[slot][1], st));
+        g_dec_pending[slot] = 1;
     }
     return 0;
 }
@@ -3243,7 +3250,8 @@ void l3m_dev_shutdown(void) {
     if (g_ready != 1) return;
     (void)hipStreamSynchronize(g_stream);
     for (int i = 0; i < 2; i++)
-        if (g_dec_ev[i]) { (void)hipEventDestroy(g_dec_ev[i]); g_dec_ev[i] = nullptr; }
+        for (int j = 0; j < 2; j++)
+            if (g_dec_ev[i][j]) { (void)hipEventDestroy(g_dec_ev[i][j]); g_dec_ev[i][j] = nullptr; }
     (void)hipStreamDestroy(g_stream);
     g_stream = nullptr;
     g_ready = 0;
@@ -3332,6 +3340,28 @@ int l3m_dev_download(void *dst, const void *src, size_t bytes) {
 int l3m_dev_sync(void) {
     if (l3m_dev_init()) return -1;
     CK(hipStreamSynchronize(g_stream));
+    return 0;
+}
+int l3m_dev_download_async(void *dst_pinned, const void *src, size_t bytes) {
+    if (l3m_dev_init()) return -1;
+    CK(hipMemcpyAsync(dst_pinned, src, bytes, hipMemcpyDeviceToHost, g_stream));
+    return 0;
+}
+void *l3m_dev_event_new(void) {
+    hipEvent_t e = nullptr;
+    if (l3m_dev_init()) return nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) { fail_msg("hipEventCreate failed"); return nullptr; }
+    return (void *)e;
+}
+void l3m_dev_event_free(void *e) { if (e) (void)hipEventDestroy((hipEvent_t)e); }
+int l3m_dev_event_record(void *e) {
+    if (l3m_dev_init()) return -1;
+    CK(hipEventRecord((hipEvent_t)e, g_stream));
+    return 0;
+}
+int l3m_dev_event_wait(void *e) {
+    if (l3m_dev_init()) return -1;
+    CK(hipEventSynchronize((hipEvent_t)e));
     return 0;
 }
 
@@ -3622,23 +3652,26 @@ int l3m_decode_fits(int dtype, int head_dtype, int gpt2, int grid, unsigned lds)
     return 0;
 }
 
+// Adds the launch of slot `slot` to the running total once it has finished (its end event waited for).
+static int timer_collect(int slot) {
+    if (!g_dec_pending[slot]) return 0;
+    float ms = 0.f;
+    CK(hipEventSynchronize(g_dec_ev[slot][1]));
+    CK(hipEventElapsedTime(&ms, g_dec_ev[slot][0], g_dec_ev[slot][1]));
+    g_dec_us += 1000.0 * ms;
+    g_dec_launches++;
+    g_dec_pending[slot] = 0;
+    return 0;
+}
+
+int l3m_decode_timer_collect(int slot) { return slot < 0 || slot > 1 ? -1 : timer_collect(slot); }
+
 int l3m_decode_timer(int mode, double *us, int *launches) {
     if (l3m_dev_init()) return -1;
-    if (!g_dec_ev[0]) {
-        CK(hipEventCreate(&g_dec_ev[0]));
-        CK(hipEventCreate(&g_dec_ev[1]));
-    }
     if (mode == 1) {                                   // start: clear and time from now on
-        g_dec_timing = 1; g_dec_us = 0; g_dec_launches = 0; g_dec_pending = 0;
-    } else if (mode == 2) {                            // collect the last launch (its stream has been waited for)
-        if (g_dec_pending) {
-            float ms = 0.f;
-            CK(hipEventSynchronize(g_dec_ev[1]));
-            CK(hipEventElapsedTime(&ms, g_dec_ev[0], g_dec_ev[1]));
-            g_dec_us += 1000.0 * ms;
-            g_dec_launches++;
-            g_dec_pending = 0;
-        }
+        g_dec_timing = 1; g_dec_us = 0; g_dec_launches = 0; g_dec_pending[0] = g_dec_pending[1] = 0;
+    } else if (mode == 2) {                            // collect the finished launches (their stream has been waited for)
+        if (timer_collect(0) || timer_collect(1)) return -1;
     } else {                                           // stop
         g_dec_timing = 0;
     }
@@ -3668,10 +3701,11 @@ int l3m_decode_placement(int grid, unsigned lds, int *xcc) {
 }
 
 int l3m_decode_launch(int dtype, int head_dtype, int gpt2, const l3m_dmodel *M_dev, const l3m_dlayer *layers_dev, const l3m_run *R_dev,
-                      int grid, unsigned lds, void *stream) {
+                      int grid, unsigned lds, void *stream, int slot) {
     hipStream_t st = as_stream(stream);
+    if (slot < 0 || slot > 1) return fail_msg("decode: slot out of range");
 #define PAIR_LAUNCH(a, b, g) \
-    if (dtype == a && head_dtype == b && !gpt2 == !g) return launch_decode<a, b, g>(M_dev, layers_dev, R_dev, grid, lds, st);
+    if (dtype == a && head_dtype == b && !gpt2 == !g) return launch_decode<a, b, g>(M_dev, layers_dev, R_dev, grid, lds, st, slot);
     DECODE_PAIRS(PAIR_LAUNCH)
 #undef PAIR_LAUNCH
     return fail_msg("decode: no persistent kernel for this pair of dtypes");

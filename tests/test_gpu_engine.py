@@ -7,6 +7,7 @@
   main.c:291), and a max-abs bound relative to max|logit| (SPREAD below says why it is not 1e-3).
 - The stop rules, callbacks, perf counters and run-to-run determinism of engine.c:322-362, 549-602.
 """
+import ctypes as C
 import dataclasses
 import hashlib
 import os
@@ -469,4 +470,47 @@ def test_timed_out_wait_fails_cleanly_then_recovers(models, oracle, capfd):
     got = m.generate(prompt, 16)
     assert got == oracle.load(path).generate(prompt, 16)
     assert m.generate(prompt, 16) == got
+    m.close()
+
+
+def test_tokens_reach_on_token_as_they_come(models):
+    """on_token is called for each token as the decode produces it (engine.c:323-326, 352-357): the first call
+    comes once the prompt's run of steps is done, with at most 8 forward passes queued past the prompt (the
+    passes the library has launched, l3m_decode_work); a stop from on_token leaves fewer than 2 x 8 passes
+    computed in vain; the tokens, the perf count and the logits after the stop are those of an uninterrupted
+    run."""
+    path = models.get(SMALL, seed=5)
+    m = A.Model(path)
+    if not m.persistent:
+        pytest.skip("the pass count is the persistent kernel's")
+    lib = A.lib()
+
+    def passes():
+        w = (C.c_double * 3)()
+        lib.l3m_decode_work(m._handle(), w)
+        return w[0]
+
+    prompt = A.prompt(4, SMALL.vocab, 6)
+    full = m.generate(prompt, 40)
+    assert len(full) == 40
+    stop_pos = len(prompt) - 1 + 4                  # the position whose prediction is the 5th token
+    lg_full = m.logits_at(stop_pos)
+    seen, p0 = [], passes()
+    assert m.generate(prompt, 40, on_token=lambda t: seen.append(passes() - p0)) == full
+    print(f"streaming: passes launched at each callback {seen[:12]}...", flush=True)
+    assert seen[0] <= len(prompt) + 8
+    assert all(b - a <= 8 for a, b in zip(seen, seen[1:]))
+    m.perf()
+    count, p0 = [0], passes()
+
+    def stop5(_t):
+        count[0] += 1
+        return count[0] < 5
+
+    assert m.generate(prompt, 40, on_token=stop5) == full[:5]
+    spent = passes() - p0
+    print(f"streaming: stop after 5 tokens, {spent} passes launched", flush=True)
+    assert spent < len(prompt) + 5 + 16
+    assert m.perf()["tokens"] == stop_pos + 1
+    assert np.array_equal(m.logits, lg_full)
     m.close()
