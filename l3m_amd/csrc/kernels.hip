@@ -320,19 +320,24 @@ __device__ __forceinline__ float block_fma_at(float acc, const uint4 *w, uint32_
         } else if constexpr (DT == L3M_Q4_0) {
             // sum (n - 8) q over the block with q = 16 h + l: 16 * sum (n - 8) h (signed 4-bit dots, the
             // codes' top bits flipped make n - 8) + sum n l (unsigned 4-bit dots) - 8 * sum l
+            // the unsigned dots start from -8 sum l (two's complement: the sums wrap exactly), so the block's
+            // integer is one shift-and-add of the two chains; the block scale multiplies the f16 scale in
+            // one mixed-precision fma (the same single rounding as the product of its f32 value)
             const uint4 *xv = (const uint4 *)xq;
             const uint4 h = xv[0], l = xv[1];
             const int lsum = *xsum;
-            int dh = 0, dl = 0;
+            int dh = 0;
+            unsigned dl = (unsigned)(-8 * lsum);
             dh = __builtin_amdgcn_sdot8((int)(w[0].x ^ 0x88888888u), (int)h.x, dh, false);
             dh = __builtin_amdgcn_sdot8((int)(w[0].y ^ 0x88888888u), (int)h.y, dh, false);
             dh = __builtin_amdgcn_sdot8((int)(w[0].z ^ 0x88888888u), (int)h.z, dh, false);
             dh = __builtin_amdgcn_sdot8((int)(w[0].w ^ 0x88888888u), (int)h.w, dh, false);
-            dl = (int)__builtin_amdgcn_udot8(w[0].x, l.x, (unsigned)dl, false);
-            dl = (int)__builtin_amdgcn_udot8(w[0].y, l.y, (unsigned)dl, false);
-            dl = (int)__builtin_amdgcn_udot8(w[0].z, l.z, (unsigned)dl, false);
-            dl = (int)__builtin_amdgcn_udot8(w[0].w, l.w, (unsigned)dl, false);
-            return fmaf(xs * f16_f32(sc), (float)(16 * dh + dl - 8 * lsum), acc);
+            dl = __builtin_amdgcn_udot8(w[0].x, l.x, dl, false);
+            dl = __builtin_amdgcn_udot8(w[0].y, l.y, dl, false);
+            dl = __builtin_amdgcn_udot8(w[0].z, l.z, dl, false);
+            dl = __builtin_amdgcn_udot8(w[0].w, l.w, dl, false);
+            const float sd = __builtin_fmaf(f16_f32(sc), xs, 0.0f);
+            return fmaf(sd, (float)(int)(((unsigned)dh << 4) + dl), acc);
         } else {
             // each code byte's two e2m1 values, doubled, as f16 (exact), dotted with the (q[j], q[j + 16])
             // pairs in f32: every partial sum is an integer below 2^24, so the dot is exact
@@ -353,15 +358,16 @@ __device__ __forceinline__ float block_fma_at(float acc, const uint4 *w, uint32_
 }
 
 // One batch of a lane's blocks: U blocks of its row, 4 blocks apart (the quarter-wavefronts interleave).
-template <int DT> struct LaneBatch {
+template <int DT> constexpr int lane_batch() { return DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 4 : 8; }
+template <int DT, int UB = lane_batch<DT>()> struct LaneBatch {
     static constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
-    static constexpr int U = DT == L3M_F32 ? 1 : DT == L3M_BF16 ? 2 : DT == L3M_Q8_0 ? 4 : 8;
+    static constexpr int U = UB;
     uint4 w[U][NV];
     uint32_t sc[U];
 };
-template <int DT>
-__device__ __forceinline__ void lane_load(const l3m_dmat &m, int tile, int b, int b1, int lane, LaneBatch<DT> &x) {
-    using L = LaneBatch<DT>;
+template <int DT, int UB>
+__device__ __forceinline__ void lane_load(const l3m_dmat &m, int tile, int b, int b1, int lane, LaneBatch<DT, UB> &x) {
+    using L = LaneBatch<DT, UB>;
     const size_t base = (size_t)tile * m.nb * RT + (lane & 15);
     const uint8_t *__restrict__ qp = m.q + base * L::QBY;
     const uint8_t *__restrict__ sp = L::SBY ? m.s + base * L::SBY : nullptr;
@@ -380,10 +386,10 @@ __device__ __forceinline__ void lane_load(const l3m_dmat &m, int tile, int b, in
 }
 // This lane's partial dot for row (lane & 15) of `tile`, over blocks b0 + sub, b0 + sub + 4, ... < b1.
 // x: its first batch, already requested by the caller.
-template <int DT>
+template <int DT, int UB>
 __device__ __forceinline__ float lane_dot(const l3m_dmat &m, int tile, int b0, int b1, const uint8_t *act, int kp, int lane,
-                                          LaneBatch<DT> x) {
-    constexpr int U = LaneBatch<DT>::U;
+                                          LaneBatch<DT, UB> x) {
+    constexpr int U = UB;
     float acc = 0.f;
     int b = b0 + (lane >> 4);
     for (;;) {
@@ -514,6 +520,44 @@ __global__ void __launch_bounds__(NT) k_gemv(l3m_dmat m, const uint8_t *__restri
         float v = s.red[(tt * S) * 16 + r];
         for (int sp = 1; sp < S; sp++) v += s.red[(tt * S + sp) * 16 + r];
         if (row < m.rows) y[row] = v;
+    }
+}
+
+// The matvec of a matrix of many tiles and long rows: one tile per workgroup of S wavefronts, wavefront s
+// taking the s-th of S equal ranges of blocks (UB blocks per lane, one batch), so each wavefront has few
+// loads to wait for and a CU holds many wavefronts to hide their latency. The S partial sums of a row are
+// added in order through LDS.
+template <int DT, int S, int UB>
+__global__ void __launch_bounds__(64 * S) k_gemv_deep(l3m_dmat m, const uint8_t *__restrict__ act_g, int k, float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NTD = 64 * S;
+    const int kp = kpad(k), tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, tile = blockIdx.x;
+    const int b0 = wave * m.nb / S, b1 = (wave + 1) * m.nb / S;
+    float *red = (float *)(smem + align16(act_size(DT, k)));
+    const size_t bytes = act_size(DT, k);
+    const int n16 = (int)(bytes / 16), ntail = (int)(bytes % 16) / 4;
+    LaneBatch<DT, UB> x;
+    constexpr int AR = (16 * 64 + NTD - 1) / NTD;     // up to 16 KiB of activation in registers
+    u32x4 a[AR];
+#pragma unroll
+    for (int r = 0; r < AR; r++) a[r] = ((const u32x4 *)act_g)[min(tid + r * NTD, n16 - 1)];
+    const uint32_t at = ((const uint32_t *)act_g)[4 * n16 - 1 + min(tid + 1, ntail)];
+    lane_load<DT, UB>(m, tile, b0 + (lane >> 4), b1, lane, x);
+#pragma unroll
+    for (int r = 0; r < AR; r++) ((u32x4 *)smem)[min(tid + r * NTD, n16 - 1)] = a[r];
+    ((uint32_t *)smem)[4 * n16 - 1 + min(tid + 1, ntail)] = at;
+    __syncthreads();
+    float acc = lane_dot<DT, UB>(m, tile, b0, b1, smem, kp, lane, x);
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (lane < 16) red[wave * 16 + lane] = acc;
+    __syncthreads();
+    if (tid < 16) {
+        float v = red[tid];
+#pragma unroll
+        for (int w = 1; w < S; w++) v += red[w * 16 + tid];
+        const int r = tile * RT + tid;
+        if (r < m.rows) y[r] = v;
     }
 }
 
@@ -3135,7 +3179,26 @@ hipStream_t as_stream(void *s) { return s ? (hipStream_t)s : g_stream; }
 template <int DT> void launch_prep(const float *x, int k, void *act, hipStream_t st) {
     hipLaunchKernelGGL(k_prep<DT>, dim3(1), dim3(NT), smem_bytes(DT, k), st, x, k, (uint8_t *)act);
 }
+// Nibble-block matrices (q4_0, mxfp4) of at least 128 tiles whose rows are 64, 128 or 256 blocks take
+// k_gemv_deep: 8 wavefronts per tile, nb / 32 blocks per lane (measured at 14336 x 4096, warm / cold against
+// the 4-wavefront k_gemv: q4_0 +10% / +7%, mxfp4 +6% / +4%; 16 wavefronts per tile was slower).
+int g_gemv_deep = -1;   // L3M_GEMV_DEEP=0 keeps every matrix on k_gemv (for comparison)
+template <int DT> bool gemv_deep(const l3m_dmat &m, const void *act, int k, hipStream_t st, float *y) {
+    if (g_gemv_deep < 0) {
+        const char *e = getenv("L3M_GEMV_DEEP");
+        g_gemv_deep = !(e && !strcmp(e, "0"));
+    }
+    if (!g_gemv_deep || m.tiles < 128 || (m.nb != 64 && m.nb != 128 && m.nb != 256) || act_size(DT, k) / 16 > 16 * 64 || ((uintptr_t)act & 15)) return false;
+    const size_t lds = align16(act_size(DT, k)) + 8 * 16 * 4;
+    const uint8_t *a = (const uint8_t *)act;
+    if (m.nb == 64) hipLaunchKernelGGL((k_gemv_deep<DT, 8, 2>), dim3(m.tiles), dim3(512), lds, st, m, a, k, y);
+    else if (m.nb == 128) hipLaunchKernelGGL((k_gemv_deep<DT, 8, 4>), dim3(m.tiles), dim3(512), lds, st, m, a, k, y);
+    else hipLaunchKernelGGL((k_gemv_deep<DT, 8, 8>), dim3(m.tiles), dim3(512), lds, st, m, a, k, y);
+    return true;
+}
 template <int DT> void launch_gemv(const l3m_dmat &m, const void *act, int k, float *y, int S, hipStream_t st) {
+    if constexpr (DT != L3M_F32)
+        if (gemv_deep<DT>(m, act, k, st, y)) return;
     const int grid = (m.tiles + 4 / S - 1) / (4 / S);
     const size_t n16 = act_size(DT, k) / 16;
     const bool staged = n16 > 0 && n16 <= (size_t)GEMV_ACT_REGS * NT && ((uintptr_t)act & 15) == 0;
