@@ -232,6 +232,10 @@ int    l3m_probe_stream(size_t bytes_per_wg, int xcds, int per_xcd, int passes, 
 int    l3m_probe_exchange(int n, int same_xcd, int dim, int rounds, double *us_per_round);
 int    l3m_probe_graph_node(int nodes, int reps, double *us_per_node);
 
+// l3m_encode (src/l3m.h:48, tokenizer.c:156-170) on the tokenizer of the file at path, on the host alone (no
+// device needed): the count, or -1 when the file is refused or the ids do not fit max.
+int    l3m_tokenize(const char *path, const char *text, int add_bos, int32_t *out, int max);
+
 // Synthetic .l3m models (seeded, host-independent bytes).
 typedef struct {
     const char *arch;

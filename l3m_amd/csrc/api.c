@@ -944,3 +944,13 @@ int l3m_step_matvec(const l3m_model *m, int which, int layer, int index, const f
 // The persistent kernel's longest wait, in ticks of the 100 MHz clock (ticks < 0: the default, 1 s). A test
 // hook: with 0 every wait that has to spin gives up at once, so a launch ends through the abort path.
 void l3m_decode_spin_limit(l3m_model *m, long long ticks) { m->spin_limit = ticks < 0 ? SPIN_LIMIT : (unsigned long long)ticks; }
+
+// l3m_encode on the tokenizer of the file at path, without a device (the host's part of l3m_load): the
+// count, or -1 when the file is refused or the ids do not fit max.
+int l3m_tokenize(const char *path, const char *text, int add_bos, int32_t *out, int max) {
+    l3m_mapped f;
+    if (l3m_map_open(&f, path)) return -1;
+    const int n = l3m_vocab_encode(&f.tok, text, add_bos, out, max);
+    l3m_map_close(&f);
+    return n;
+}

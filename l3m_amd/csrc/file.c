@@ -166,7 +166,7 @@ static int open_checked(l3m_mapped *f, const char *path, why *w) {
     for (uint32_t i = 0; i < h->n_tensors; i++)
         if (entry_ok(f, i, w)) return -1;
     if (model_ok(f, w)) return -1;
-    if (l3m_vocab_init(&f->tok, (const uint8_t *)p + h->tokenizer_offset, f->size - h->tokenizer_offset))
+    if (l3m_vocab_init(&f->tok, (const uint8_t *)p + h->tokenizer_offset, f->size - h->tokenizer_offset, h->flags))
         return because(w, "bad tokenizer section");
     if (f->tok.n > (int)h->vocab) return because(w, "tokenizer has %d tokens, vocab only %u", f->tok.n, h->vocab);
     if (h->chat_offset) {                  // [i32 im_start][system prompt, NUL-terminated]

@@ -12,9 +12,12 @@
 // ---------------------------------------------------------------- mapped file (reference file.h:17-22)
 typedef struct {
     int             n, bos, eos, max_len;
-    int             merges;       // some piece is longer than one byte: the byte-level encoder refuses
+    int             sp_prefix, sp_words, digits;   // SentencePiece prefix space, its words split at spaces, digits one by one
     const uint8_t **bytes;
     const uint16_t *len;
+    float          *score;
+    int            *slot;         // ids by their bytes (open addressing, mask + 1 entries, -1 empty)
+    unsigned        mask;
 } l3m_vocab_table;
 
 typedef struct {
@@ -65,7 +68,7 @@ L3M_EXPORT void     l3m_quantize_row(int dtype, void *dst, const float *x, int k
 L3M_EXPORT uint16_t l3m_f32_to_f16(float f);
 
 // ---------------------------------------------------------------- tokenizer (byte table)
-int            l3m_vocab_init(l3m_vocab_table *t, const void *section, size_t size);
+int            l3m_vocab_init(l3m_vocab_table *t, const void *section, size_t size, unsigned flags);
 void           l3m_vocab_free(l3m_vocab_table *t);
 int            l3m_vocab_encode(const l3m_vocab_table *t, const char *text, int add_bos, int32_t *out, int max);
 const uint8_t *l3m_vocab_decode(const l3m_vocab_table *t, int32_t tok, int *len);

@@ -204,6 +204,7 @@ class Reference:
         api = {name: l3m_amd._SIG[name] for name in ("l3m_load", "l3m_free", "l3m_generate", "l3m_logits", "l3m_vocab",
                                                       "l3m_describe", "l3m_perf_read")}
         api["l3m_kernels_usable"] = (C.c_int, [C.c_void_p])           # dispatch.c:23
+        api["l3m_encode"] = l3m_amd._SIG["l3m_encode"]
         api["l3m_kernels_pick"] = (C.c_void_p, [])                    # dispatch.c:28
         internal = {
             "l3m_tile_bytes": (C.c_size_t, [C.c_int, C.c_int]),
@@ -284,6 +285,13 @@ class RefModel:
 
     def describe(self):
         return self.r.lib.l3m_describe(self.h).decode()
+
+    def encode(self, text, add_bos=True, cap=None):
+        raw = text.encode()
+        cap = cap or len(raw) + 8
+        out = (C.c_int32 * cap)()
+        n = self.r.lib.l3m_encode(self.h, raw, int(add_bos), out, cap)
+        return None if n < 0 else list(out[:n])
 
     def generate(self, prompt, max_new, temperature=0.0, seed=0):
         out = []
