@@ -87,9 +87,11 @@ const char        *l3m_hip_last_error(void);                   // the table's st
 // No counterpart in the reference: l3m_kernels_hip.attend for callers that cannot allocate device memory
 // (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments
 // (host pointers), same kernel, same result; it stages q, the K and V rows and the output through one
-// fixed 4 MiB device array instead of buffers grown on demand, so it refuses (-1, the reason on stderr) a
-// call whose (pos * stride + head_dim) * 2 bytes of K, and of V, exceed 2 MiB less 1 KiB. Calls are
-// serialized by a lock (two overlapping on one GPU would race on the array). 0 on success.
+// fixed 4 MiB device array instead of buffers grown on demand: q and the output take 4 head_dim bytes
+// each and K and V (pos * stride + head_dim) * 2 bytes each, every part rounded up to 256 bytes, so it
+// refuses (-1, the reason and the bound on stderr) a call whose K (and V) part exceeds
+// (4 MiB - 2 up256(4 head_dim)) / 2 bytes (2 MiB less 1 KiB at head_dim 256). Calls are serialized by a
+// lock (two overlapping on one GPU would race on the array). 0 on success.
 int l3m_hip_attend_noalloc(float *out, const float *q, const uint16_t *k, const uint16_t *v, int pos, int head_dim, int stride);
 
 // ============================================================== 3. device-level (pointers are device memory)
@@ -222,6 +224,7 @@ int    l3m_decode_window(const l3m_model *m);
 // K and V rows [pos0, pos0 + n) of kv head kvh in layer `layer` of m's cache (bf16 as the step writes them,
 // engine.c:247-248), into k and v [n][hd]; -1 when out of range.
 int    l3m_kv_rows(const l3m_model *m, int layer, int kvh, int pos0, int n, uint16_t *k, uint16_t *v);
+int    l3m_head_dim(const l3m_model *m);   // hd of m: the row length of l3m_kv_rows
 
 // Probes, the GPU analogues of the reference's bench/residency.c:31-97 and bench/exchange.c:22-44 (no
 // counterpart in its library): bandwidth of workgroups streaming their own shards (per_xcd workgroups on

@@ -75,7 +75,7 @@ l3m_dev_evict i p z p           | l3m_decode_attention i p       | l3m_kv_rows i
 l3m_decode_window i p
 l3m_k_step_mv i i i M p i p i p  | l3m_step_matvec i p i i i *f *f | l3m_step_layout v p *i
 l3m_widen_rows i i i i ** p | l3m_decode_spin_limit v p l | l3m_time_launch_interval d i
-l3m_tokenize i s s i *I i
+l3m_tokenize i s s i *I i | l3m_head_dim i p
 l3m_time_read d ** i z i         | l3m_hip_attend_noalloc i p p p p i i i | l3m_phase_stamps i i i i p
 """
 _SIG = {}
@@ -205,8 +205,13 @@ class Model:
         """Positions the decode step's LDS K/V window holds (ctx when all fit); past it attention reads the cache."""
         return self._lib.l3m_decode_window(self._handle())
 
-    def kv_rows(self, layer, kvh, pos0, n, hd):
-        """bf16 K and V rows [pos0, pos0 + n) of one kv head of one layer's cache, as uint16 [n, hd] each."""
+    def kv_rows(self, layer, kvh, pos0, n, hd=None):
+        """bf16 K and V rows [pos0, pos0 + n) of one kv head of one layer's cache, as uint16 [n, hd] each (hd is
+        the model's; a different one is refused)."""
+        model_hd = self._lib.l3m_head_dim(self._handle())
+        if hd is not None and hd != model_hd:
+            raise ValueError(f"head_dim {hd} is not the model's {model_hd}")
+        hd = model_hd
         k, v = np.zeros((n, hd), np.uint16), np.zeros((n, hd), np.uint16)
         if self._lib.l3m_kv_rows(self._handle(), layer, kvh, pos0, n, _p(k), _p(v)) != 0:
             raise ValueError("K/V rows out of range")

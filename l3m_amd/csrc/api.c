@@ -878,6 +878,8 @@ int l3m_decode_attention(const l3m_model *m) {
 
 int l3m_decode_window(const l3m_model *m) { return m->dm.kv_win; }
 
+int l3m_head_dim(const l3m_model *m) { return m->dm.hd; }
+
 int l3m_kv_rows(const l3m_model *m, int layer, int kvh, int pos0, int n, uint16_t *k, uint16_t *v) {
     const l3m_dmodel *d = &m->dm;
     if (layer < 0 || layer >= d->n_layers || kvh < 0 || kvh >= d->n_kv || pos0 < 0 || n < 1 || pos0 + n > d->ctx) return -1;

@@ -3820,10 +3820,14 @@ int l3m_prefill_graph(l3m_pfgraphs *g, const l3m_dmodel *M, const l3m_pflayer *L
     if (k < 0) {                                       // capture this length into the least recently used entry
         k = lru;
         if (g->P[k]) { (void)hipGraphExecDestroy(g->e[k]); g->P[k] = 0; }
-        hipGraph_t graph;
+        hipGraph_t graph = nullptr;
         if (hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal) != hipSuccess) return fail_msg("prefill graph capture");
         const int rc = l3m_prefill(M, L, B, P, g_stream);
-        if (hipStreamEndCapture(g_stream, &graph) != hipSuccess || rc) return fail_msg("prefill graph capture");
+        const hipError_t ec = hipStreamEndCapture(g_stream, &graph);
+        if (ec != hipSuccess || rc) {
+            if (ec == hipSuccess && graph) (void)hipGraphDestroy(graph);   // a capture that ended holds a graph
+            return fail_msg("prefill graph capture");
+        }
         const hipError_t e = hipGraphInstantiate(&g->e[k], graph, NULL, NULL, 0);
         (void)hipGraphDestroy(graph);
         if (e != hipSuccess) return fail_msg("prefill graph instantiate");
@@ -3834,7 +3838,6 @@ int l3m_prefill_graph(l3m_pfgraphs *g, const l3m_dmodel *M, const l3m_pflayer *L
     return 0;
 }
 
-// Average microseconds per launch over `iters` launches, timed with events on the library stream.
 // Mean microseconds per launch of iters launches queued back to back, after one untimed launch: one pair
 // of events around them all (events around each launch would add their own markers' time to every
 // figure). For a kernel shorter than the launch interval (l3m_time_launch_interval) this is the launch rate.
