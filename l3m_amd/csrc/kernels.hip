@@ -523,44 +523,6 @@ __global__ void __launch_bounds__(NT) k_gemv(l3m_dmat m, const uint8_t *__restri
     }
 }
 
-// The matvec of a matrix of many tiles and long rows: one tile per workgroup of S wavefronts, wavefront s
-// taking the s-th of S equal ranges of blocks (UB blocks per lane, one batch), so each wavefront has few
-// loads to wait for and a CU holds many wavefronts to hide their latency. The S partial sums of a row are
-// added in order through LDS.
-template <int DT, int S, int UB>
-__global__ void __launch_bounds__(64 * S) k_gemv_deep(l3m_dmat m, const uint8_t *__restrict__ act_g, int k, float *__restrict__ y) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int NTD = 64 * S;
-    const int kp = kpad(k), tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, tile = blockIdx.x;
-    const int b0 = wave * m.nb / S, b1 = (wave + 1) * m.nb / S;
-    float *red = (float *)(smem + align16(act_size(DT, k)));
-    const size_t bytes = act_size(DT, k);
-    const int n16 = (int)(bytes / 16), ntail = (int)(bytes % 16) / 4;
-    LaneBatch<DT, UB> x;
-    constexpr int AR = (16 * 64 + NTD - 1) / NTD;     // up to 16 KiB of activation in registers
-    u32x4 a[AR];
-#pragma unroll
-    for (int r = 0; r < AR; r++) a[r] = ((const u32x4 *)act_g)[min(tid + r * NTD, n16 - 1)];
-    const uint32_t at = ((const uint32_t *)act_g)[4 * n16 - 1 + min(tid + 1, ntail)];
-    lane_load<DT, UB>(m, tile, b0 + (lane >> 4), b1, lane, x);
-#pragma unroll
-    for (int r = 0; r < AR; r++) ((u32x4 *)smem)[min(tid + r * NTD, n16 - 1)] = a[r];
-    ((uint32_t *)smem)[4 * n16 - 1 + min(tid + 1, ntail)] = at;
-    __syncthreads();
-    float acc = lane_dot<DT, UB>(m, tile, b0, b1, smem, kp, lane, x);
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
-    if (lane < 16) red[wave * 16 + lane] = acc;
-    __syncthreads();
-    if (tid < 16) {
-        float v = red[tid];
-#pragma unroll
-        for (int w = 1; w < S; w++) v += red[w * 16 + tid];
-        const int r = tile * RT + tid;
-        if (r < m.rows) y[r] = v;
-    }
-}
-
 // One workgroup per query head (ops.c:58-73): scores q.K[t] / sqrt(hd) over t = 0..pos, softmax, sum of
 // p[t] V[t]. K, V rows are `stride` elements apart; head h reads kv head h / hpk at k + kvh * kv_stride.
 // dpos, when set, holds pos (device-resident step position).
@@ -2117,6 +2079,50 @@ __device__ int sample_block(const float *lg, int V, float gmax, float temp, unsi
     return tok == 0x7FFFFFFF ? V - 1 : tok;
 }
 
+// The matvec of a matrix of many tiles and long rows: one tile per workgroup of S wavefronts, wavefront s
+// taking the s-th of S equal ranges of blocks (UB blocks per lane, one batch), so each wavefront has few
+// loads to wait for and a CU holds many wavefronts to hide their latency. The S partial sums of a row are
+// added in order through LDS.
+template <int DT, int S, int UB> constexpr int gemv_deep_words() { return DT == L3M_MXFP4 || UB == 8 ? 2 : 1; }
+template <int DT, int S, int UB>
+__global__ void __launch_bounds__(64 * S) k_gemv_deep(l3m_dmat m, const uint8_t *__restrict__ act_g, int k, float *__restrict__ y) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NTD = 64 * S;
+    const int kp = kpad(k), tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, tile = blockIdx.x;
+    const int b0 = wave * m.nb / S, b1 = (wave + 1) * m.nb / S;
+    float *red = (float *)(smem + align16(act_size(DT, k)));
+    const size_t bytes = act_size(DT, k);
+    const int n16 = (int)(bytes / 16), ntail = (int)(bytes % 16) / 4;
+    LaneBatch<DT, UB> x;
+    // 16-byte words of the activation per thread (the launcher checks the activation fits): a load per
+    // thread covers up to 8 KiB at 8 wavefronts, two the larger mxfp4 form and the 256-block rows
+    constexpr int AR = gemv_deep_words<DT, S, UB>();
+    u32x4 a[AR];
+#pragma unroll
+    for (int r = 0; r < AR; r++) a[r] = ((const u32x4 *)act_g)[min(tid + r * NTD, n16 - 1)];
+    const uint32_t at = ((const uint32_t *)act_g)[4 * n16 - 1 + min(tid + 1, ntail)];
+    lane_load<DT, UB>(m, tile, b0 + (lane >> 4), b1, lane, x);
+#pragma unroll
+    for (int r = 0; r < AR; r++) ((u32x4 *)smem)[min(tid + r * NTD, n16 - 1)] = a[r];
+    ((uint32_t *)smem)[4 * n16 - 1 + min(tid + 1, ntail)] = at;
+    __syncthreads();
+    float acc = lane_dot<DT, UB>(m, tile, b0, b1, smem, kp, lane, x);
+    float lo, hi;
+    swap16(acc, lo, hi);                              // q0 + q1, q2 + q3
+    acc = lo + hi;
+    swap32(acc, lo, hi);                              // (q0 + q1) + (q2 + q3)
+    acc = lo + hi;
+    if (lane < 16) red[wave * 16 + lane] = acc;
+    __syncthreads();
+    if (tid < 16) {
+        float v = red[tid];
+#pragma unroll
+        for (int w = 1; w < S; w++) v += red[w * 16 + tid];
+        const int r = tile * RT + tid;
+        if (r < m.rows) y[r] = v;
+    }
+}
+
 // ------------------------------------------------------------------ pieces of the decode step, alone
 // For parity tests: the decode step's own device code on inputs the caller gives.
 
@@ -3188,7 +3194,9 @@ template <int DT> bool gemv_deep(const l3m_dmat &m, const void *act, int k, hipS
         const char *e = getenv("L3M_GEMV_DEEP");
         g_gemv_deep = !(e && !strcmp(e, "0"));
     }
-    if (!g_gemv_deep || m.tiles < 128 || (m.nb != 64 && m.nb != 128 && m.nb != 256) || act_size(DT, k) / 16 > 16 * 64 || ((uintptr_t)act & 15)) return false;
+    if (!g_gemv_deep || m.tiles < 128 || (m.nb != 64 && m.nb != 128 && m.nb != 256) || ((uintptr_t)act & 15)) return false;
+    const int ub = m.nb / 32, words = ub == 2 ? gemv_deep_words<DT, 8, 2>() : ub == 4 ? gemv_deep_words<DT, 8, 4>() : gemv_deep_words<DT, 8, 8>();
+    if (act_size(DT, k) / 16 > (size_t)words * 512) return false;
     const size_t lds = align16(act_size(DT, k)) + 8 * 16 * 4;
     const uint8_t *a = (const uint8_t *)act;
     if (m.nb == 64) hipLaunchKernelGGL((k_gemv_deep<DT, 8, 2>), dim3(m.tiles), dim3(512), lds, st, m, a, k, y);
