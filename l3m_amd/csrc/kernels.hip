@@ -3995,7 +3995,11 @@ int l3m_probe_exchange(int n, int same_xcd, int dim, int rounds, double *us_per_
     unsigned long long limit = 100000000ull, host_out[2] = {0, 0};
     int grid = l3m_dev_cus();
     void *args[] = {&vec, &dim, &n, &same_xcd, &rounds, &flags, &tickets, &out, &limit};
-    if (e == hipSuccess) e = hipLaunchCooperativeKernel((const void *)k_probe_exchange, dim3(grid), dim3(NTE), args, 0, g_stream);
+    if (e == hipSuccess && g_coop) e = hipLaunchCooperativeKernel((const void *)k_probe_exchange, dim3(grid), dim3(NTE), args, 0, g_stream);
+    if (e == hipSuccess && !g_coop) {                  // L3M_COOP=0: the same grid as an ordinary dispatch
+        hipLaunchKernelGGL(k_probe_exchange, dim3(grid), dim3(NTE), 0, g_stream, vec, dim, n, same_xcd, rounds, flags, tickets, out, limit);
+        e = hipGetLastError();
+    }
     unsigned abort_word = 0;
     if (e == hipSuccess) e = hipMemcpyAsync(host_out, out, 16, hipMemcpyDeviceToHost, g_stream);
     if (e == hipSuccess) e = hipMemcpyAsync(&abort_word, flags + 64, 4, hipMemcpyDeviceToHost, g_stream);
