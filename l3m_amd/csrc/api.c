@@ -23,8 +23,10 @@
 // What the host reads back after a run of steps: the persistent launch's abort word, and the tokens the run
 // produced (in order from its first position with a token).
 typedef struct {
-    unsigned abort;
-    int32_t  tok[NSLOTS];
+    unsigned           abort;
+    unsigned           pad;
+    unsigned long long waited;   // 100 MHz ticks attention group 0 waited for its inputs (persistent launches)
+    int32_t            tok[NSLOTS];
 } l3m_chunk_out;
 
 struct l3m_model {
@@ -62,6 +64,7 @@ struct l3m_model {
     int          prefilled;    // positions the last generate call prefilled
     int          logits_fresh;
     double       tokens, ns;
+    double       wait_ns;      // the persistent kernel's attention group 0 waiting for its inputs, since the last perf read
     int          cold;         // evict the caches before each forward pass (engine.c:330-338)
     void        *evict;        // EVICT_BYTES of device memory read to evict them
     double       cold_ns;      // host time spent evicting since the last perf read (not token time)
@@ -652,7 +655,8 @@ static int chunk_enqueue(l3m_model *m, int first, int last, int head_from, int s
         if (l3m_dev_upload_async(m->run_dev + slot, m->run_host + slot, sizeof r) ||
             l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, m->dm_dev, m->layers_dev, m->run_dev + slot, m->grid, m->lds_decode, NULL,
                               slot) ||
-            l3m_dev_download_async(&out->abort, sync + L3M_SYNC_ABORT, 4))
+            l3m_dev_download_async(&out->abort, sync + L3M_SYNC_ABORT, 4) ||
+            l3m_dev_download_async(&out->waited, sync + L3M_SYNC_WAIT, 8))
             return -1;
         for (int p = first; p <= last; p++) {
             m->work[0] += 1;
@@ -661,6 +665,7 @@ static int chunk_enqueue(l3m_model *m, int first, int last, int head_from, int s
         }
     } else {
         out->abort = 0;
+        out->waited = 0;
         for (int p = first; p <= last; p++)
             if (step(m, p >= head_from)) return -1;
     }
@@ -672,6 +677,7 @@ static int chunk_enqueue(l3m_model *m, int first, int last, int head_from, int s
 // Waits for slot's run of steps; -1 on a device error or a timed-out wait of the persistent kernel.
 static int chunk_finish(l3m_model *m, int slot) {
     if (l3m_dev_event_wait(m->ev[slot]) || (m->persist && l3m_decode_timer_collect(slot))) return -1;
+    m->wait_ns += 10.0 * (double)m->out_host[slot].waited;
     if (m->out_host[slot].abort) {
         fprintf(stderr, "l3m: decode kernel: a wait between phases timed out\n");
         return -1;
@@ -797,15 +803,19 @@ const char *l3m_decode(const l3m_model *m, int32_t tok, int *len) { return (cons
 
 // Counters since the last read (src/l3m.h:21-29): time per forward pass from the host clock around each
 // generate call, less the --cold evictions (engine.c:584); weight bytes streamed per token; the CPU-side
-// counters (L2 bytes, L3 misses, DRAM bytes, energy, LLC occupancy) have no GPU meaning here (NAN); the host
-// never waits on ranks, so ns_wait is 0 and ns_compute is the whole token.
+// counters (L2 bytes, L3 misses, DRAM bytes, energy, LLC occupancy) have no GPU meaning here (NAN).
+// ns_wait is the analogue of the ranks' barrier wait (engine.c:578-602): on the persistent kernel, the time
+// its attention group 0 (on the step's critical chain) waited for the FFN flags and the head's token, per
+// token; ns_compute is the rest. The one-graph-per-step path has no such waits (ns_wait NAN).
 int l3m_perf_read(l3m_model *m, l3m_perf *out) {
-    const double n = m->tokens, spent = m->ns - m->cold_ns;
-    m->tokens = m->ns = m->cold_ns = 0;
+    const double n = m->tokens, spent = m->ns - m->cold_ns, waited = m->wait_ns;
+    m->tokens = m->ns = m->cold_ns = m->wait_ns = 0;
     *out = (l3m_perf){.l2_bytes = NAN, .l3_miss = NAN, .dram_bytes = NAN, .energy_j = NAN, .llc_occupancy = NAN};
     if (!(n > 0)) return -1;
     out->tokens = n;
-    out->ns_token = out->ns_compute = spent / n;
+    out->ns_token = spent / n;
+    out->ns_wait = m->persist ? waited / n : NAN;
+    out->ns_compute = m->persist ? out->ns_token - out->ns_wait : out->ns_token;
     out->bytes_token = m->reference ? 0 : m->weight_bytes;
     return 0;
 }

@@ -95,6 +95,7 @@ typedef struct l3m_dsample {
     unsigned long long rng[L3M_MAX_HEAD_WGS];
 } l3m_dsample;
 #define L3M_SYNC_ABORT 192                           // the word a timed-out wait sets
+#define L3M_SYNC_WAIT 248                            // 64-bit: 100 MHz ticks attention group 0 waited for its inputs this launch
 
 // ------------------------------------------------------------------ runtime
 int         l3m_dev_init(void);                 // 0 when a gfx9 HIP device is usable

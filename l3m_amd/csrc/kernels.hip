@@ -2539,7 +2539,11 @@ template <int DT, bool G2>
 __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *layers, const l3m_run *Rp, int g, int s) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int ok_lds;
+    // group 0's time waiting for its inputs (the FFN flags, the head's token) since the launch began, in
+    // ticks of the 100 MHz clock: the decode's analogue of the reference's barrier wait (l3m_perf ns_wait)
+    __shared__ unsigned long long waited;
     g = uniform(g); s = uniform(s);
+    if (s == 0 && tidx() == 0) waited = 0;
     const int nl = fixed(Mp).n_layers;
     for (int l = 0; l < nl; l++) {
         const l3m_dmodel M = fixed(per_iteration(Mp));
@@ -2556,6 +2560,7 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
         attn_kv_window<DT>(M, G, l, pos, smem);
         const unsigned epoch = (unsigned)(s * nl + l);
         int tok = 0;
+        const unsigned long long w0 = __builtin_amdgcn_s_memrealtime();
         if (l == 0 && s > 0 && pos - 1 >= R.head_from) {
             // this step's token is the previous step's argmax (which also orders this step after every
             // read of the previous step's FFN partials)
@@ -2567,14 +2572,18 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
             if (epoch > 0 && !wait_flags<0, true>(sync + SY_FFN, M.n_chunks, epoch, abort_flag, R.spin_limit, &ok_lds)) return false;
             if (l == 0) tok = __hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        // read now, added after the block: the clock read's latency overlaps the prologue's loads
+        const unsigned long long w1 = __builtin_amdgcn_s_memrealtime();
         phase(g, 1, pos, l);
         attn_block<DT, true, G2>(M, Lw, G, l, pos, tok, g, wt, smem);
         set_flag<false>(sync + SY_ATTN + g, epoch + 1);
+        if (g == 0 && tidx() == 0) waited += w1 - w0;
         // the K/V rows while the FFN runs: off the block's path (the next read of them is the window copy
         // of the next position's step, behind this workgroup's later flag waits)
         kv_rows_store(M, G, l, pos, (const uint16_t *)(smem + lds_of(G).cur), tidx(), NTE);
         phase(g, 10, pos, l);
     }
+    if (g == 0 && tidx() == 0) gw((unsigned long long *)(fixed(Rp).sync + L3M_SYNC_WAIT))[0] = waited;
     return true;
 }
 

@@ -355,6 +355,13 @@ def test_callback_stop_logits_and_perf(oracle, models):
     counters = m.perf()
     assert counters["tokens"] == len(ids) - 1 + stop_after     # forward passes, the prompt included
     assert counters["ns_token"] > 0 < counters["bytes_token"]
+    # the wait/compute split (engine.c:578-602): on the persistent kernel, the time its attention group 0
+    # waited for the FFN flags and the head's token, per token; the rest is compute
+    if m.persistent:
+        print(f"perf: ns_token {counters['ns_token']:.0f}, ns_wait {counters['ns_wait']:.0f}, ns_compute {counters['ns_compute']:.0f}",
+              flush=True)
+        assert 0 < counters["ns_wait"] < counters["ns_token"]
+        assert counters["ns_compute"] == pytest.approx(counters["ns_token"] - counters["ns_wait"])
     assert np.isnan(list(m.perf().values())).all()             # nothing ran since the last read
     # logits are the prediction after the last token fed: position len(ids) + 3
     om = oracle.load(path)
