@@ -28,6 +28,7 @@ resident in HBM before the timed region. One JSON line on stdout:
 import argparse
 import ctypes as C
 import json
+import math
 import os
 import statistics
 import sys
@@ -508,6 +509,7 @@ def main():
         with A.Model(path) as m:
             log(f"bench: {m.describe()} on {lib.l3m_dev_name().decode()}")
             m.bench_decode(prompt, max(a.warmup, 1))
+            m.perf()                                  # l3m_perf counts from here: the timed tokens only
             with DecodeTimer(A, m) as t:
                 t0 = time.perf_counter()
                 m.bench_decode(prompt, a.steps)
@@ -515,7 +517,11 @@ def main():
                 elapsed = time.perf_counter() - t0
             dom = t.roofline(cfg)
             value = a.steps / elapsed
+            perf = m.perf()
+            split = {k: (None if math.isnan(perf[k]) else round(perf[k], 1)) for k in ("ns_token", "ns_wait", "ns_compute")}
             log(f"bench: {a.steps} tokens in {elapsed * 1e3:.2f} ms = {value:.0f} tok/s")
+            log(f"bench: l3m_perf per token: {split['ns_token']} ns, waits of attention group 0 {split['ns_wait']} ns, "
+                f"compute {split['ns_compute']} ns")
             if dom:
                 log(f"bench: k_decode {dom['launches']} launches, {dom['steps']:.0f} passes, {dom['us']:.1f} us per launch, "
                     f"{dom['us_per_step']:.1f} us per pass, {dom['GBs']:.1f} GB/s algorithmic")
@@ -570,6 +576,7 @@ def main():
         "matvec": matvec,
         "sampled_decode": sampled,
         "streamed_decode": streamed,
+        "perf_split": split,
         "cold_decode": cold,
         "cpu_baseline": cpu,
     }
