@@ -12,7 +12,7 @@
 
 #define MiB (1024.0 * 1024.0)
 #define DEFAULT_CTX 512        // engine.c:22
-#define NSLOTS 128             // logits slots = the most steps enqueued between two host reads
+#define NSLOTS 128             // logits slots = the most steps of one run (the last NSLOTS positions' logits stay readable)
 #define HEAD_WGS 256           // workgroups of the head kernel
 #define MAX_PARTS 64           // partial residual vectors a step kernel adds (head groups, FFN chunks)
 #define BODY_CUS 32            // the CUs of one MI355X XCD (256 in 8), where the persistent kernel keeps the body
@@ -706,9 +706,11 @@ static int evict(l3m_model *m) {
 // the model has), the tokens are handed over as they come: the prompt's run ends at the first generated
 // token, the later runs are LIVE_STEPS positions long, and two are kept in flight, so the next run computes
 // while the host calls on_token for the last one's tokens; a stop leaves at most the rest of its run and the
-// run behind it (under 2 LIVE_STEPS passes) computed in vain. Otherwise runs are NSLOTS positions long.
-static int run(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, float temperature, uint64_t seed,
-               int (*on_token)(int32_t, void *), void *user) {
+// run behind it (under 2 LIVE_STEPS passes) computed in vain. Otherwise runs are NSLOTS positions long, also
+// two in flight, so the next launch follows the last on the stream without waiting for the host. --cold
+// runs one pass at a time (each after an eviction the host times).
+static int run_steps(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, float temperature, uint64_t seed,
+                     int (*on_token)(int32_t, void *), void *user) {
     l3m_dmodel *d = &m->dm;
     const int bos = m->f.tok.bos, eos = m->f.tok.eos;
     const int last = n_prompt - 1 + max_new < d->ctx - 1 ? n_prompt - 1 + max_new : d->ctx - 1;   // exhausted() at engine.c:322
@@ -732,7 +734,7 @@ static int run(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, f
     }
     *m->stage_pos = next;
     if (l3m_dev_upload_async(d->pos, m->stage_pos, 4)) return -1;
-    const int live = on_token != NULL || bos >= 0 || eos >= 0, depth = live && !m->cold ? 2 : 1;
+    const int live = on_token != NULL || bos >= 0 || eos >= 0, depth = m->cold ? 1 : 2;
     int q_first[2], q_end[2], q_slot[2], nq = 0, slot = 0;
     for (;;) {
         while (!rc && stop < 0 && next <= last && nq < depth) {
@@ -769,14 +771,21 @@ static int run(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, f
     return n_gen;
 }
 
+// run_steps, its time counted for l3m_perf (the generate calls and the bench loop alike).
+static int run(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, float temperature, uint64_t seed,
+               int (*on_token)(int32_t, void *), void *user) {
+    const double t0 = now_ns();
+    const int n = run_steps(m, prompt, n_prompt, max_new, temperature, seed, on_token, user);
+    m->ns += now_ns() - t0;
+    return n;
+}
+
 int l3m_generate(l3m_model *m, const int32_t *prompt, int n_prompt, int max_new, float temperature, uint64_t seed,
                  int (*on_token)(int32_t, void *), void *user) {
     if (n_prompt < 1 || n_prompt >= m->dm.ctx) return 0;
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= m->dm.vocab) { fprintf(stderr, "l3m: token %d out of range\n", prompt[i]); return -1; }
-    double t0 = now_ns();
-    int n = run(m, prompt, n_prompt, max_new < 0 ? 0 : max_new, temperature, seed, on_token, user);
-    m->ns += now_ns() - t0;
+    const int n = run(m, prompt, n_prompt, max_new < 0 ? 0 : max_new, temperature, seed, on_token, user);
     if (n < 0) fprintf(stderr, "l3m: generate failed on the device: %s\n", l3m_dev_error() ? l3m_dev_error() : "?");
     return n;
 }

@@ -14,6 +14,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <type_traits>
 #include "dev.h"
 #include "format.h"
 
@@ -645,9 +646,9 @@ template <int DT> constexpr int nslot_b() { return DT == L3M_F32 ? 1 : DT == L3M
 // The attention block keeps its Wo slots live through the attention; q8_0 gives one up to stay in registers.
 template <int DT> constexpr int nslot_wo() { return DT == L3M_Q8_0 || DT == L3M_Q4_0 ? 2 : nslot_b<DT>(); }
 // The wide matrices (q/k/v rows, gate/up rows, the head) take the tile form (tile_rows) in the quantized
-// dtypes, whose slot batch holds a whole row of the benchmark shapes (up to 24 blocks); bf16 and f32 take
-// mv and rows_sum4 (bf16 in the tile form, with a third slot, measured 3% slower on stories15M). The
-// head's slots: one row's in the tile form.
+// dtypes, whose slot batch holds a whole row of the benchmark shapes (up to 24 blocks); bf16 takes the
+// matrix cores (tile_rows_mfma: the v_dot2 tile form, with a third slot, measured 3% slower on stories15M
+// than mv and rows_sum4), f32 mv and rows_sum4. The head's slots: one row's in the tile form.
 template <int DT> constexpr bool tiled() { return quantized(DT); }
 template <int DT> constexpr int nslot_h() { return tiled<DT>() ? nslot_a<DT>() : nslot_a<DT>() + nslot_b<DT>(); }
 
@@ -1548,6 +1549,79 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+// The bf16 wide matrices (q/k/v rows, gate/up rows, the head) on the matrix cores: wavefront w takes tiles
+// w, w + NWE, ... in turn, and a tile's blocks go through v_mfma_f32_16x16x32_bf16 one after the other, the
+// block's 16 x 32 weights as A, the activation's 32 values in every column of B, each product accumulating
+// onto the last (C). Every column of the result then holds the tile's 16 row sums, already in lanes: no
+// cross-lane sum, no LDS round trip, no barrier, and a quarter of the instructions of the v_dot2 form (one
+// per block where each lane of that form spends 16 v_dot2 on its block). Lane l holds A's row l % 16,
+// inputs 8 (l / 16) .. + 7 of each block: the 16-byte piece l / 16 of its row, so a block's 64 pieces are
+// its 1 KiB of the lane-tile plane, one load per lane, as the other forms read it. The products of bf16
+// values are exact in f32; the sums are f32 (the order differs from the v_dot2 form's, within its bounds).
+// PrefM holds MK blocks of one tile: the most that fit the bf16 roles' registers (36 VGPRs, where the
+// v_dot2 form's two slots take 32), which is every block of a 288-input row; longer rows take further
+// batches of MK, loaded in turn.
+constexpr int MK = 9;
+struct PrefM { uint4 a[MK]; };
+template <int DT, int NS> struct WideSel { using T = Pref<DT, NS>; };
+template <int NS> struct WideSel<L3M_BF16, NS> { using T = PrefM; };
+// The register batch of a wide matrix of dtype DT (NS slots in the v_dot2 and integer forms).
+template <int DT, int NS> using Wide = typename WideSel<DT, NS>::T;
+
+// Blocks b0 .. b0 + MK - 1 of tile t (past nb, and tiles past the end, the last valid one: loaded, not used).
+__device__ __forceinline__ void prefm_load(PrefM &pf, const l3m_dmat &m, int t, int b0) {
+    const int lane = tidx() & 63, nb = m.nb, tc = t < m.tiles ? t : m.tiles - 1;
+    const size_t piece = (size_t)(lane & 15) * 4 + (lane >> 4);   // uint4 of the block: row l % 16, piece l / 16
+#pragma unroll
+    for (int k = 0; k < MK; k++) {
+        const int b = b0 + k < nb ? b0 + k : nb - 1;
+        pf.a[k] = ldg16(m.q, ((size_t)tc * nb + b) * 64 + piece);
+    }
+}
+// The matvec of a bf16 matrix in this form (the wavefront's first batch loaded by prefm_load beforehand),
+// act the bf16 activation in LDS. f(i, y, partner, lead) runs for each of the tile's 16 rows in the lanes
+// l with 4 (l / 16) + l % 4 = the row's place in the tile (lead: (l / 4) % 4 == 0), partner being row
+// i ^ 1's value (the neighbouring lane), as the other forms call it.
+template <class F>
+__device__ __forceinline__ void tile_rows_mfma(PrefM &pf, const l3m_dmat &m, const uint8_t *act, int rows, F f) {
+    const int wave = wave_id(), lane = tidx() & 63, nb = m.nb, q = lane & 3;
+    const uint4 *xb = (const uint4 *)act + (lane >> 4);   // block b's piece: xb[4 b]
+    auto batch = [&](f32x4 c, int b0) {
+        // pin the loaded registers here, as pref_compute does
+#pragma unroll
+        for (int k = 0; k < MK; k++) asm volatile("" : "+v"(pf.a[k].x), "+v"(pf.a[k].y), "+v"(pf.a[k].z), "+v"(pf.a[k].w));
+#pragma unroll
+        for (int k = 0; k < MK; k++) {
+            if (b0 + k >= nb) break;
+            c = mfma_bf16(__builtin_bit_cast(bf16x8, pf.a[k]), __builtin_bit_cast(bf16x8, xb[4 * (b0 + k)]), c);
+        }
+        return c;
+    };
+    auto finish = [&](f32x4 c, int t) {
+        const float y = q == 0 ? c[0] : q == 1 ? c[1] : q == 2 ? c[2] : c[3];
+        const float partner = dppf<QP_X1>(y);        // row i ^ 1 is the neighbouring lane
+        const int i = t * 16 + 4 * (lane >> 4) + q;
+        if (i < rows) f(i, y, partner, ((lane >> 2) & 3) == 0);
+    };
+    if (wave < m.tiles) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+        c = batch(c, 0);
+        for (int b0 = MK; b0 < nb; b0 += MK) {
+            prefm_load(pf, m, wave, b0);
+            c = batch(c, b0);
+        }
+        finish(c, wave);
+        for (int t = wave + NWE; t < m.tiles; t += NWE) {
+            c = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int b0 = 0; b0 < nb; b0 += MK) {
+                prefm_load(pf, m, t, b0);
+                c = batch(c, b0);
+            }
+            finish(c, t);
+        }
+    }
+}
+
 // x as the sum of three bf16 (each rounded to nearest even from what is left): exact to 2^-24 of x, so
 // three bf16 products with an exact bf16 operand give x * y to f32 accuracy.
 __device__ __forceinline__ void split3(float x, __bf16 &h, __bf16 &m, __bf16 &l) {
@@ -1672,9 +1746,9 @@ template <int DT> constexpr int a_dtype() { return DT; }
 #else
 template <int DT> constexpr int a_dtype() { return DT == L3M_Q4_0 ? L3M_Q8_0 : DT; }
 #endif
-template <int DT> struct AttnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_wo<DT>()> b; ProStatic st; };
-template <int DT> struct FfnW { Pref<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_b<DT>()> b; ProStatic st; };
-template <int DT> struct HeadW { Pref<DT, nslot_h<DT>()> a; ProStatic st; };
+template <int DT> struct AttnW { Wide<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_wo<DT>()> b; ProStatic st; };
+template <int DT> struct FfnW { Wide<a_dtype<DT>(), nslot_a<DT>()> a; Pref<a_dtype<DT>(), nslot_b<DT>()> b; ProStatic st; };
+template <int DT> struct HeadW { Wide<DT, nslot_h<DT>()> a; ProStatic st; };
 
 // A block's static prologue inputs (ProStatic), issued ahead of its weights.
 __device__ __forceinline__ void attn_static(ProStatic &st, const l3m_dmodel &M, const l3m_dlayer &Lw, int pos) {
@@ -1688,6 +1762,7 @@ template <int DT, int NS> __device__ __forceinline__ void wide_issue(Pref<DT, NS
     if constexpr (tiled<DT>()) pref_load_tile<DT, NS>(pf, m, wave_id(), 0);
     else pref_load<DT, NS>(pf, m, 0);
 }
+__device__ __forceinline__ void wide_issue(PrefM &pf, const l3m_dmat &m) { prefm_load(pf, m, wave_id(), 0); }
 template <int DT, int NS, class F>
 __device__ __forceinline__ void wide_rows(Pref<DT, NS> &pf, const l3m_dmat &m, const uint8_t *act, int kp, float *res, int rows, F f) {
     if constexpr (tiled<DT>()) {
@@ -1698,16 +1773,20 @@ __device__ __forceinline__ void wide_rows(Pref<DT, NS> &pf, const l3m_dmat &m, c
         rows_sum4(m, res, rows, f);
     }
 }
+template <class F>
+__device__ __forceinline__ void wide_rows(PrefM &pf, const l3m_dmat &m, const uint8_t *act, int, float *, int rows, F f) {
+    tile_rows_mfma(pf, m, act, rows, f);
+}
 template <int DT> __device__ __forceinline__ void attn_issue(AttnW<DT> &w, const l3m_dgroup &G) {
-    wide_issue<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv);
+    wide_issue(w.a, G.qkv);
     pref_load<a_dtype<DT>(), nslot_wo<DT>()>(w.b, G.wo, 0);
 }
 template <int DT> __device__ __forceinline__ void ffn_issue(FfnW<DT> &w, const l3m_dchunk &C) {
-    wide_issue<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up);
+    wide_issue(w.a, C.gate_up);
     pref_load<a_dtype<DT>(), nslot_b<DT>()>(w.b, C.down, 0);
 }
 template <int DT> __device__ __forceinline__ void head_issue(HeadW<DT> &w, const l3m_dmat &V) {
-    wide_issue<DT, nslot_h<DT>()>(w.a, V);
+    wide_issue(w.a, V);
 }
 
 // The persistent path's K/V window copy for the attention block of group G at (layer, pos): rows
@@ -1799,7 +1878,7 @@ __device__ __forceinline__ void attn_block(const l3m_dmodel &M, const l3m_dlayer
             }
         }
     };
-    wide_rows<a_dtype<DT>(), nslot_a<DT>()>(w.a, G.qkv, act, kp, work, nqd + 2 * nkd, qkv_row);
+    wide_rows(w.a, G.qkv, act, kp, work, nqd + 2 * nkd, qkv_row);
     phase(gi, 4, pos, layer);
     // the window's copy (issued long before) is complete; this step's rows go to the cache after the
     // attention, so their store acknowledgements stay off the path to it
@@ -1873,7 +1952,7 @@ __device__ __forceinline__ void ffn_block(const l3m_dmodel &M, const l3m_dlayer 
             if (lead && !(i & 1)) gu[i >> 1] = silu_mul(partner, y);
         }
     };
-    wide_rows<a_dtype<DT>(), nslot_a<DT>()>(w.a, C.gate_up, act, kp, work, C.gate_up.rows, gu_row);
+    wide_rows(w.a, C.gate_up, act, kp, work, C.gate_up.rows, gu_row);
     phase(64 + ci, 4, pos, layer);
     __syncthreads();
     phase(64 + ci, 5, pos, layer);
@@ -1970,7 +2049,7 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
             better(v, idx, yy, t0 * 16 + i);
         }
     };
-    wide_rows<DT, nslot_h<DT>()>(w.a, V, act, kp, work, V.rows, logit_row);
+    wide_rows(w.a, V, act, kp, work, V.rows, logit_row);
     block_argmax(v, idx, scr, (int *)scr + 16);
 }
 
@@ -2217,8 +2296,8 @@ __global__ void __launch_bounds__(NTE) k_step_mv(l3m_dmat m, const float *x, int
         m.rows = nt * 16 < m.rows - t0 * 16 ? nt * 16 : m.rows - t0 * 16;
         m.tiles = nt;
     }
-    Pref<AT, NS> pf;
-    if constexpr (WIDE) wide_issue<AT, NS>(pf, m);
+    std::conditional_t<WIDE, Wide<AT, NS>, Pref<AT, NS>> pf;
+    if constexpr (WIDE) wide_issue(pf, m);
     else pref_load<AT, NS>(pf, m, 0);
     float e[4];
 #pragma unroll
@@ -2226,7 +2305,7 @@ __global__ void __launch_bounds__(NTE) k_step_mv(l3m_dmat m, const float *x, int
     prep_owned<AT>(make_float4(e[0], e[1], e[2], e[3]), act, kp);
     float *out = y + (size_t)t0 * 16;
     if constexpr (WIDE) {
-        wide_rows<AT, NS>(pf, m, act, kp, work, m.rows, [&](int i, float v, float, bool lead) {
+        wide_rows(pf, m, act, kp, work, m.rows, [&](int i, float v, float, bool lead) {
             if (lead) out[i] = v;
         });
     } else {
