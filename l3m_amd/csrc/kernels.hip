@@ -88,6 +88,22 @@ __device__ __forceinline__ void stcoh16(void *p, size_t i, float4 x) {
 __device__ __forceinline__ void stcoh4(void *p, size_t i, float x) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), buf(p), (uint32_t)(4 * i), 0, SC1);
 }
+// Element i of a weight plane p (a uniform base, under 2 GiB), or zeros with no memory access when ok is
+// false: the offset of a load that is not wanted lies past the buffer's range, which the hardware answers
+// with zeros and no request. A wavefront's loads for tiles or pairs past a matrix's end then cost no cache or
+// memory bandwidth, and no branch ties a load to its use (a branch around loads would make the compiler
+// merge the loaded registers where the branches join, and wait for the loads there).
+constexpr uint32_t OOB = 0x80000000u;
+__device__ __forceinline__ uint4 ldg16_if(const void *p, size_t i, bool ok) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(buf(p), ok ? (uint32_t)(16 * i) : OOB, 0, 0));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldg2_if(const void *p, size_t i, bool ok) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(buf(p), ok ? (uint32_t)(2 * i) : OOB, 0, 0);
+}
+__device__ __forceinline__ uint32_t ldg1_if(const void *p, size_t i, bool ok) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(buf(p), ok ? (uint32_t)i : OOB, 0, 0);
+}
 template <bool COH> __device__ __forceinline__ uint4 ld16(const void *p, size_t i) { return COH ? ldcoh16(p, i) : ldg16(p, i); }
 template <bool COH> __device__ __forceinline__ float4 ld16f(const void *p, size_t i) {
     if constexpr (COH) {
@@ -660,9 +676,8 @@ struct Pref {
 
 // Slot s of this lane holds pair p = (wave + (s0 + s) * NWE) * 4 + sub of m, a pair being (tile, block)
 // = (p / nb, p % nb) and the lane reading row (lane & 15) of it: 4 consecutive pairs = one contiguous
-// 64 * QBYTES run per wavefront. Loads are unconditional (past the end they repeat the last pair) so that
-// no branch ties a load to its use (a branch around them would make the compiler copy the loaded
-// registers at the join, which waits for the loads). m has at least one pair.
+// 64 * QBYTES run per wavefront. Loads are unconditional: past the end they return zeros with no memory
+// access (ldg16_if). m has at least one pair.
 // The wavefront index as a scalar (uniform) value, so index arithmetic on it runs on the scalar unit.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tidx() >> 6); }
 
@@ -672,13 +687,13 @@ __device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, i
     const int wave = wave_id(), sub = (tidx() >> 4) & 3, row = tidx() & 15, n = m.tiles * m.nb;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
-        int p = (wave + (s0 + s) * NWE) * 4 + sub;
-        p = p < n ? p : n - 1;
+        const int p = (wave + (s0 + s) * NWE) * 4 + sub;
+        const bool ok = p < n;                        // pairs past the end: zeros, no memory access
         const size_t slot = (size_t)p * 16 + row;
 #pragma unroll
-        for (int v = 0; v < NV; v++) pf.w[s][v] = ldg16(m.q, slot * NV + v);
-        if constexpr (SBY == 2) pf.sc[s] = gp<uint16_t>(m.s)[slot];
-        if constexpr (SBY == 1) pf.sc[s] = gp<uint8_t>(m.s)[slot];
+        for (int v = 0; v < NV; v++) pf.w[s][v] = ldg16_if(m.q, slot * NV + v, ok);
+        if constexpr (SBY == 2) pf.sc[s] = ldg2_if(m.s, slot, ok);
+        if constexpr (SBY == 1) pf.sc[s] = ldg1_if(m.s, slot, ok);
         if constexpr (SBY == 0) pf.sc[s] = 0;
     }
 }
@@ -686,19 +701,20 @@ __device__ __forceinline__ void pref_load(Pref<DT, NS> &pf, const l3m_dmat &m, i
 // The tile form of a matrix: wavefront w takes tiles w, w + NWE, ... in turn, each in slots of 4 blocks
 // of its 16 rows (lane quarter sub = lane / 16 takes blocks sub, sub + 4, ...), NS slots per batch.
 // pref_load_tile loads slots j0 .. j0 + NS - 1 of tile t: 4 consecutive pairs per slot, as pref_load;
-// blocks past nb and tiles past the end load the last valid pair (not used).
+// blocks past nb and tiles past the end are zeros, with no memory access (not used).
 template <int DT, int NS>
 __device__ __forceinline__ void pref_load_tile(Pref<DT, NS> &pf, const l3m_dmat &m, int t, int j0) {
     constexpr int QBY = qbytes(DT), SBY = sbytes(DT), NV = QBY / 16;
-    const int sub = (tidx() >> 4) & 3, row = tidx() & 15, nb = m.nb, tc = t < m.tiles ? t : m.tiles - 1;
+    const int sub = (tidx() >> 4) & 3, row = tidx() & 15, nb = m.nb;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         const int b = 4 * (j0 + s) + sub;
-        const size_t slot = ((size_t)tc * nb + (b < nb ? b : nb - 1)) * 16 + row;
+        const bool ok = t < m.tiles && b < nb;
+        const size_t slot = ((size_t)t * nb + b) * 16 + row;
 #pragma unroll
-        for (int v = 0; v < NV; v++) pf.w[s][v] = ldg16(m.q, slot * NV + v);
-        if constexpr (SBY == 2) pf.sc[s] = gp<uint16_t>(m.s)[slot];
-        if constexpr (SBY == 1) pf.sc[s] = gp<uint8_t>(m.s)[slot];
+        for (int v = 0; v < NV; v++) pf.w[s][v] = ldg16_if(m.q, slot * NV + v, ok);
+        if constexpr (SBY == 2) pf.sc[s] = ldg2_if(m.s, slot, ok);
+        if constexpr (SBY == 1) pf.sc[s] = ldg1_if(m.s, slot, ok);
         if constexpr (SBY == 0) pf.sc[s] = 0;
     }
 }
@@ -1568,14 +1584,18 @@ template <int NS> struct WideSel<L3M_BF16, NS> { using T = PrefM; };
 // The register batch of a wide matrix of dtype DT (NS slots in the v_dot2 and integer forms).
 template <int DT, int NS> using Wide = typename WideSel<DT, NS>::T;
 
-// Blocks b0 .. b0 + MK - 1 of tile t (past nb, and tiles past the end, the last valid one: loaded, not used).
+// Blocks b0 .. b0 + MK - 1 of tile t (past nb: zeros, no memory access, not used). A wavefront with no tile
+// issues nothing: the bf16 roles have the registers to spare for the branch (no spills), and the loads it
+// saves cost more than loads past the range (measured: stories15M 16,018 -> 16,380 tok/s). The integer
+// roles, at their register limit, spill with it and keep loads past the range (ldg16_if) instead.
 __device__ __forceinline__ void prefm_load(PrefM &pf, const l3m_dmat &m, int t, int b0) {
-    const int lane = tidx() & 63, nb = m.nb, tc = t < m.tiles ? t : m.tiles - 1;
+    const int lane = tidx() & 63, nb = m.nb;
     const size_t piece = (size_t)(lane & 15) * 4 + (lane >> 4);   // uint4 of the block: row l % 16, piece l / 16
+    if (t >= m.tiles) return;                         // no tile for this wavefront (uniform)
 #pragma unroll
     for (int k = 0; k < MK; k++) {
-        const int b = b0 + k < nb ? b0 + k : nb - 1;
-        pf.a[k] = ldg16(m.q, ((size_t)tc * nb + b) * 64 + piece);
+        const int b = b0 + k;
+        pf.a[k] = ldg16_if(m.q, ((size_t)t * nb + b) * 64 + piece, b < nb);
     }
 }
 // The matvec of a bf16 matrix in this form (the wavefront's first batch loaded by prefm_load beforehand),
