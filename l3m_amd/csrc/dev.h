@@ -115,7 +115,7 @@ int         l3m_dev_sync(void);
 void       *l3m_dev_stream(void);
 
 // ------------------------------------------------------------------ single kernels
-size_t l3m_act_bytes(int dtype, int k);         // prepared activation: per 32-block values (q8_0 32 B, q4_0 nibble planes 32 B, mxfp4 f16 pairs 64 B) + scale[nb] + sum[nb], bf16[kp] or f32[kp]
+size_t l3m_act_bytes(int dtype, int k);         // prepared activation: per 32-block values (q8_0 32 B, q4_0 nibble planes 32 B, mxfp4 f16 pairs 64 B) + scale[nb] + sum[nb] (mxfp4: + fp8 parts h, l 64 B per block), bf16[kp] or f32[kp]
 int    l3m_k_prep(int dtype, const float *x, int k, void *act, void *stream);
 int    l3m_k_gemv(const l3m_dmat *m, const void *act, int k, float *y, void *stream);
 int    l3m_k_attend(float *out, const float *q, const uint16_t *k, const uint16_t *v, int pos, int hd, int stride, void *stream);

@@ -43,6 +43,10 @@ __host__ __device__ inline size_t act_size(int dt, int k) {
     const int kp = kpad(k);
     return quantized(dt) ? (size_t)act_qbytes(dt) * (kp / 32) + 8 * (size_t)(kp / 32) : dt == L3M_BF16 ? 2 * (size_t)kp : 4 * (size_t)kp;
 }
+// The standalone prepared activation (l3m_k_prep, l3m_k_gemv): the same, and for mxfp4 then per 32-block the
+// values' exact fp8 (e4m3) parts h = floor(q / 16) and l = q - 16 h, 32 bytes each in the f16 pairs' element
+// order (the form the matrix-core matvec reads, k_gemv_mx).
+__host__ __device__ inline size_t act_bytes(int dt, int k) { return act_size(dt, k) + (dt == L3M_MXFP4 ? (size_t)64 * (kpad(k) / 32) : 0); }
 __host__ __device__ inline size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
 
 // Reads through explicit global (address space 1) pointers: pointers taken from descriptors in device
@@ -223,6 +227,28 @@ __device__ void stage_x(float *xs, Src src, int k, int kp, const float *nw, floa
     __syncthreads();
 }
 
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+// Two fp8 (e4m3) bytes of a and b in the low (HI false) or high half of old.
+template <bool HI> __device__ __forceinline__ uint32_t pk_fp8(float a, float b, uint32_t old) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, HI);
+}
+// The integer activation q = 16 h + l of four f16 pairs (one 16-byte word of the mxfp4 form): h = floor(q / 16)
+// in [-8, 7] and l in [0, 15] as fp8 bytes, both exact (e4m3 holds every integer up to 16), in the word's
+// element order.
+__device__ __forceinline__ void split_hl(uint4 w, u32x2 &h, u32x2 &l) {
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+    float hv[8], lv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float q = f16_f32(d[i >> 1] >> (16 * (i & 1)));
+        hv[i] = floorf(q * 0.0625f);
+        lv[i] = fmaf(-16.f, hv[i], q);
+    }
+    h.x = pk_fp8<true>(hv[2], hv[3], pk_fp8<false>(hv[0], hv[1], 0));
+    h.y = pk_fp8<true>(hv[6], hv[7], pk_fp8<false>(hv[4], hv[5], 0));
+    l.x = pk_fp8<true>(lv[2], lv[3], pk_fp8<false>(lv[0], lv[1], 0));
+    l.y = pk_fp8<true>(lv[6], lv[7], pk_fp8<false>(lv[4], lv[5], 0));
+}
 // The lane holding values 4m..4m+3 of a 32-block (m = lane & 7) writes its share of the block's prepared
 // form at blk (the block's bytes): P = its four int8 values packed, Pp = those of lane m + 4 (values
 // 4m + 16 ..), used by lanes m < 4 only. Returns the lane's part of the block sum.
@@ -490,6 +516,15 @@ __global__ void __launch_bounds__(NT) k_prep(const float *__restrict__ x, int k,
     prep_act<DT>(s.act, s.xs, kp);
     const size_t n = act_size(DT, k);
     for (size_t i = threadIdx.x; i < n; i += NT) out[i] = s.act[i];
+    if constexpr (DT == L3M_MXFP4) {
+        for (int w = threadIdx.x; w < kp / 8; w += NT) {            // one 16-byte word of f16 pairs: 8 values
+            u32x2 h, l;
+            split_hl(((const uint4 *)s.act)[w], h, l);
+            uint8_t *o = out + n + 64 * (w >> 2) + 8 * (w & 3);
+            *(u32x2 *)o = h;
+            *(u32x2 *)(o + 32) = l;
+        }
+    }
 }
 
 // STAGED: the activation is 16-byte aligned and at most GEMV_ACT_REGS * NT 16-byte words (gemv_staged).
@@ -2178,6 +2213,35 @@ __device__ int sample_block(const float *lg, int V, float gmax, float temp, unsi
     return tok == 0x7FFFFFFF ? V - 1 : tok;
 }
 
+// The first batch of a deep-kernel lane (k_gemv_deep, k_gemv_mx): blocks b0 + sub + 4u (u < UB) of row
+// lane & 15 of a tile, all inside the matrix. Buffer loads over a wavefront-uniform base (the tile's block b0)
+// at the lane's offset plus a constant per u: no per-load address arithmetic.
+template <int DT, int UB>
+__device__ __forceinline__ void lane_load_deep(const l3m_dmat &m, int tile, int b0, int lane, LaneBatch<DT, UB> &x) {
+    using L = LaneBatch<DT, UB>;
+    const size_t first = ((size_t)tile * m.nb + b0) * RT;          // (tile, block b0, row 0)
+    const __amdgpu_buffer_rsrc_t rq = buf(m.q + first * L::QBY);
+    const uint32_t oq = (uint32_t)lane * L::QBY;
+#pragma unroll
+    for (int u = 0; u < L::U; u++) {
+#pragma unroll
+        for (int v = 0; v < L::NV; v++) {
+            const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq + 16 * v, 64 * u * L::QBY, 0));
+            x.w[u][v] = make_uint4(w.x, w.y, w.z, w.w);
+        }
+        x.sc[u] = 0;
+    }
+    if constexpr (L::SBY) {
+        const __amdgpu_buffer_rsrc_t rs = buf(m.s + first * L::SBY);
+        const uint32_t os = (uint32_t)lane * L::SBY;
+#pragma unroll
+        for (int u = 0; u < L::U; u++) {
+            if constexpr (L::SBY == 2) x.sc[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, os, 64 * u * 2, 0);
+            else x.sc[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, os, 64 * u, 0);
+        }
+    }
+}
+
 // The matvec of a matrix of many tiles and long rows: one tile per workgroup of S wavefronts, wavefront s
 // taking the s-th of S equal ranges of blocks (UB blocks per lane, one batch), so each wavefront has few
 // loads to wait for and a CU holds many wavefronts to hide their latency. The S partial sums of a row are
@@ -2187,7 +2251,7 @@ template <int DT, int S, int UB>
 __global__ void __launch_bounds__(64 * S) k_gemv_deep(l3m_dmat m, const uint8_t *__restrict__ act_g, int k, float *__restrict__ y) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NTD = 64 * S;
-    const int kp = kpad(k), tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, tile = blockIdx.x;
+    const int kp = kpad(k), tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, tile = blockIdx.x;
     const int b0 = wave * m.nb / S, b1 = (wave + 1) * m.nb / S;
     float *red = (float *)(smem + align16(act_size(DT, k)));
     const size_t bytes = act_size(DT, k);
@@ -2200,16 +2264,100 @@ __global__ void __launch_bounds__(64 * S) k_gemv_deep(l3m_dmat m, const uint8_t 
 #pragma unroll
     for (int r = 0; r < AR; r++) a[r] = ((const u32x4 *)act_g)[min(tid + r * NTD, n16 - 1)];
     const uint32_t at = ((const uint32_t *)act_g)[4 * n16 - 1 + min(tid + 1, ntail)];
-    lane_load<DT, UB>(m, tile, b0 + (lane >> 4), b1, lane, x);
+    lane_load_deep<DT, UB>(m, tile, b0, lane, x);
 #pragma unroll
     for (int r = 0; r < AR; r++) ((u32x4 *)smem)[min(tid + r * NTD, n16 - 1)] = a[r];
     ((uint32_t *)smem)[4 * n16 - 1 + min(tid + 1, ntail)] = at;
     __syncthreads();
-    float acc = lane_dot<DT, UB>(m, tile, b0, b1, smem, kp, lane, x);
+    // the wavefront's range is exactly UB batches of 4 blocks: one straight run of block dots
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < UB; u++) acc = block_fma<DT>(acc, x.w[u], x.sc[u], smem, kp, b0 + 4 * u + (lane >> 4));
+    (void)b1;
     float lo, hi;
     swap16(acc, lo, hi);                              // q0 + q1, q2 + q3
     acc = lo + hi;
     swap32(acc, lo, hi);                              // (q0 + q1) + (q2 + q3)
+    acc = lo + hi;
+    if (lane < 16) red[wave * 16 + lane] = acc;
+    __syncthreads();
+    if (tid < 16) {
+        float v = red[tid];
+#pragma unroll
+        for (int w = 1; w < S; w++) v += red[w * 16 + tid];
+        const int r = tile * RT + tid;
+        if (r < m.rows) y[r] = v;
+    }
+}
+
+// The mxfp4 matvec of k_gemv_deep's shapes on the matrix cores. One v_mfma_scale_f32_16x16x128_f8f6f4
+// takes 4 blocks of a tile's 16 rows: B is the e2m1 codes as they lie in the lane-tile plane (lane l: row
+// l % 16, block l / 16 of the 4, its 16 bytes; the code bytes need no decode), A is the activation's exact
+// fp8 parts h and l (q = 16 h + l, the prepared activation's last part), row 4g + p of A holding part p of
+// block g and zeros outside block g's 32 inputs, so that row 4g of the result is block g's dot with h and
+// row 4g + 1 its dot with l, per weight row. Both block scales of the product are 1 (e8m0 127); the products
+// of e2m1 values (half the doubled codes the reference dots) with these integers, and their sums, are
+// multiples of 1/2 below 2^13, exact in f32. Lane l then holds block g = l / 16 of row l % 16: the
+// reference's integer dot 2 (16 D[4g] + D[4g + 1]), scaled by the reference's formula
+// (kernels_scalar.c:62-75). A wavefront's lanes add their blocks in order, the 4 block lanes of a row meet by
+// permlane swaps, the wavefronts through LDS.
+// Memory instructions are what bounds this kernel warm (each one of 64 lanes costs the load unit its cycles
+// whatever share of its lanes carry data), so every load is full width: a wavefront's 4 batches of weights,
+// each 16 blocks' fp8 parts (1 KiB) in one load that it stores to its own LDS span and reads back in the
+// product's layout (its own bytes only: no workgroup barrier), the block scales as 4 byte loads and the
+// activation scales as 4 word loads.
+template <int S, int R>
+__global__ void __launch_bounds__(64 * S) k_gemv_mx(l3m_dmat m, const uint8_t *__restrict__ act_g, int k, float *__restrict__ y) {
+    constexpr int UB = 4 * R;                             // R rounds of 16 blocks per wavefront
+    __shared__ float red[S * 16];
+    __shared__ __align__(16) uint8_t stage[S][1024 * R + 16];
+    const int nb = m.nb, tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, tile = blockIdx.x;
+    const int b0 = wave * nb / S;
+    const uint8_t *hl = act_g + act_size(L3M_MXFP4, k);   // [nb][h, l][32] fp8
+    const float *xs = (const float *)(act_g + 64 * (size_t)nb);
+    // the fp8 parts first (cache hits, stored to LDS while the weights are in flight), then the weights
+    const __amdgpu_buffer_rsrc_t ra = buf(hl + 64 * (size_t)b0);
+    u32x4 aw[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) aw[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, 16 * lane, 1024 * r, 0));
+    LaneBatch<L3M_MXFP4, UB> x;
+    lane_load_deep<L3M_MXFP4, UB>(m, tile, b0, lane, x);
+    const __amdgpu_buffer_rsrc_t rx = buf(xs + b0);
+    const int g = lane >> 4, row = lane & 15, bb = row >> 2, part = row & 3;
+    float sx[UB];
+#pragma unroll
+    for (int u = 0; u < UB; u++) sx[u] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rx, 4 * g, 16 * u, 0));
+    uint8_t *my = stage[wave];
+#pragma unroll
+    for (int r = 0; r < R; r++) *(u32x4 *)(my + 1024 * r + 16 * lane) = aw[r];
+    if (lane == 0) *(u32x4 *)(my + 1024 * R) = u32x4{0u, 0u, 0u, 0u};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Inputs of the product: lane group g of B holds block g's 32 codes (inputs 32 g .. 32 g + 31 of the 128),
+    // lane group g of A holds inputs 16 g .. 16 g + 15 in its first 16 bytes and 64 + 16 g .. + 15 in its last
+    // 16. So block bb's part p (row 4 bb + p of A) lies in the first 16 bytes of lane groups 2 bb and 2 bb + 1
+    // for bb < 2, in the last 16 of lane groups 2 (bb - 2) and 2 (bb - 2) + 1 for bb >= 2; lane group g holds
+    // its inputs 16 (g & 1) .. + 15 there. Every other half reads the span's 16 zero bytes.
+    const bool has = part < 2 && (bb & 1) == (g >> 1), second = bb >= 2;
+    const int oa = 64 * bb + 32 * part + 16 * (g & 1);
+    const uint8_t *plo = has && !second ? my + oa : my + 1024 * R, *phi = has && second ? my + oa : my + 1024 * R;
+    const int step = has ? 256 : 0;                       // the next 4 blocks, or the zero bytes again
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < UB; u++) {
+        const u32x4 lo = *(const u32x4 *)(plo + (!second ? u * step : 0)), hi = *(const u32x4 *)(phi + (second ? u * step : 0));
+        const i32x8 A = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        const i32x8 B = {(int)x.w[u][0].x, (int)x.w[u][0].y, (int)x.w[u][0].z, (int)x.w[u][0].w, 0, 0, 0, 0};
+        const f32x4 d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 4, 0, 127, 0, 127);
+        const float dot = 2.f * fmaf(16.f, d[0], d[1]);
+        // xs 2^(e - 128) as one exact scaling (the product the reference forms, rounded once either way)
+        acc = fmaf(__builtin_amdgcn_ldexpf(sx[u], (int)x.sc[u] - 128), dot, acc);
+    }
+    float lo, hi;
+    swap16(acc, lo, hi);                              // blocks g = 0 + 1, 2 + 3
+    acc = lo + hi;
+    swap32(acc, lo, hi);
     acc = lo + hi;
     if (lane < 16) red[wave * 16 + lane] = acc;
     __syncthreads();
@@ -3297,16 +3445,29 @@ template <int DT> void launch_prep(const float *x, int k, void *act, hipStream_t
 // k_gemv_deep: 8 wavefronts per tile, nb / 32 blocks per lane (measured at 14336 x 4096, warm / cold against
 // the 4-wavefront k_gemv: q4_0 +10% / +7%, mxfp4 +6% / +4%; 16 wavefronts per tile was slower).
 int g_gemv_deep = -1;   // L3M_GEMV_DEEP=0 keeps every matrix on k_gemv (for comparison)
+int g_gemv_mx = -1;     // L3M_GEMV_MX=0 keeps mxfp4 on k_gemv_deep's VALU dots (for comparison)
 template <int DT> bool gemv_deep(const l3m_dmat &m, const void *act, int k, hipStream_t st, float *y) {
     if (g_gemv_deep < 0) {
         const char *e = getenv("L3M_GEMV_DEEP");
         g_gemv_deep = !(e && !strcmp(e, "0"));
     }
     if (!g_gemv_deep || m.tiles < 128 || (m.nb != 64 && m.nb != 128 && m.nb != 256) || ((uintptr_t)act & 15)) return false;
+    const uint8_t *a = (const uint8_t *)act;
+    if constexpr (DT == L3M_MXFP4) {
+        if (g_gemv_mx < 0) {
+            const char *e = getenv("L3M_GEMV_MX");
+            g_gemv_mx = !(e && !strcmp(e, "0"));
+        }
+        if (g_gemv_mx) {
+            if (m.nb == 64) hipLaunchKernelGGL((k_gemv_mx<4, 1>), dim3(m.tiles), dim3(256), 0, st, m, a, k, y);
+            else if (m.nb == 128) hipLaunchKernelGGL((k_gemv_mx<8, 1>), dim3(m.tiles), dim3(512), 0, st, m, a, k, y);
+            else hipLaunchKernelGGL((k_gemv_mx<8, 2>), dim3(m.tiles), dim3(512), 0, st, m, a, k, y);
+            return true;
+        }
+    }
     const int ub = m.nb / 32, words = ub == 2 ? gemv_deep_words<DT, 8, 2>() : ub == 4 ? gemv_deep_words<DT, 8, 4>() : gemv_deep_words<DT, 8, 8>();
     if (act_size(DT, k) / 16 > (size_t)words * 512) return false;
     const size_t lds = align16(act_size(DT, k)) + 8 * 16 * 4;
-    const uint8_t *a = (const uint8_t *)act;
     if (m.nb == 64) hipLaunchKernelGGL((k_gemv_deep<DT, 8, 2>), dim3(m.tiles), dim3(512), lds, st, m, a, k, y);
     else if (m.nb == 128) hipLaunchKernelGGL((k_gemv_deep<DT, 8, 4>), dim3(m.tiles), dim3(512), lds, st, m, a, k, y);
     else hipLaunchKernelGGL((k_gemv_deep<DT, 8, 8>), dim3(m.tiles), dim3(512), lds, st, m, a, k, y);
@@ -3544,7 +3705,7 @@ int l3m_dev_event_wait(void *e) {
     return 0;
 }
 
-size_t l3m_act_bytes(int dtype, int k) { return act_size(dtype, k); }
+size_t l3m_act_bytes(int dtype, int k) { return act_bytes(dtype, k); }
 
 int l3m_k_prep(int dtype, const float *x, int k, void *act, void *stream) {
     if (k < 1 || dtype < 0 || dtype >= L3M_NDTYPES || smem_bytes(dtype, k) > LDS_MAX) return fail_msg("prep: k out of range for this dtype");

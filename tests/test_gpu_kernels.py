@@ -35,6 +35,40 @@ def test_prep_quantized_bit_exact(dev, oracle, k):
     assert np.array_equal(s, want["sum"])
 
 
+def fp8_e4m3(b):
+    """Values of fp8 e4m3 bytes (no NaN among the bytes checked here)."""
+    b = np.asarray(b, np.int64)
+    e, m = (b >> 3) & 15, b & 7
+    v = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7))
+    return np.where(b & 0x80, -v, v)
+
+
+@pytest.mark.parametrize("k", [32, 288, 1376, 4096])
+def test_prep_mxfp4_parts(dev, oracle, k):
+    """The mxfp4 form: f16 pairs (q[j], q[j + 16]) per block, the scales and sums, then per block the fp8
+    parts h = floor(q / 16) and l = q - 16 h of the pairs' elements (the matrix-core matvec's operand)."""
+    rng = np.random.default_rng(k + 9)
+    x = rng.standard_normal(k).astype(np.float32) * 3
+    x[:32] = 0
+    if k > 64:
+        x[40] = -12.0                                 # the block's largest: q = -127
+    raw = dev.prep(MXFP4, x)
+    nb = (k + 31) // 32
+    want = oracle.prepare(Q8_0, x)
+    q = np.zeros(nb * 32, np.int64)
+    q[:k] = want["q8"]
+    q = q.reshape(nb, 32)
+    pairs = raw[:64 * nb].view(np.float16).reshape(nb, 16, 2)
+    elem = np.stack([q[:, :16], q[:, 16:]], axis=2)  # element e = 2j + i: q[j + 16 i]
+    assert np.array_equal(pairs.astype(np.int64), elem)
+    assert np.array_equal(raw[64 * nb:68 * nb].view(np.float32).view(np.uint32), want["scale"].view(np.uint32))
+    hl = raw[72 * nb:136 * nb].reshape(nb, 2, 32)
+    assert len(raw) == 136 * nb
+    e = elem.reshape(nb, 32)
+    assert np.array_equal(fp8_e4m3(hl[:, 0]), np.floor(e / 16))
+    assert np.array_equal(fp8_e4m3(hl[:, 1]), e - 16 * np.floor(e / 16))
+
+
 @pytest.mark.parametrize("k", [2, 18, 288, 4096])
 def test_prep_bf16_bit_exact(dev, oracle, k):
     x = np.random.default_rng(k).standard_normal(k).astype(np.float32)
@@ -81,6 +115,25 @@ def test_gemv_edges(dev, oracle, dtype, k):
     want = oracle.gemv(dtype, w0, n, k, x)
     want[n - 5:] = 0
     assert np.all(y[n - 5:] == 0)
+    assert rel_err(y, want) < TOL[dtype], rel_err(y, want)
+    dev.free_all()
+
+
+@pytest.mark.parametrize("dtype", [Q8_0, Q4_0, MXFP4], ids=NAMES.get)
+@pytest.mark.parametrize("k", [2048, 4096, 8192])
+def test_gemv_deep_edges(dev, oracle, dtype, k):
+    """The same extremes on the shapes of the 8-wavefront matvecs (at least 128 tiles, rows of 64, 128 or 256
+    blocks; mxfp4 on the matrix cores): a q8 weight of -128 and subnormal mxfp4 scales in every block, a zero
+    activation block, an activation of one large value in a block (q = +-127 there), and a ragged last tile."""
+    n = 2048 + 5
+    w = extremes(dtype, rows(dtype, n, k, seed=k + 1), k)
+    x = np.random.default_rng(5).standard_normal(k).astype(np.float32)
+    x[:32] = 0
+    x[64:96] = -1e-3
+    x[70] = -50.0
+    x[100] = 50.0
+    y = dev.gemv(dev.matrix(dtype, w, k), x)
+    want = oracle.gemv(dtype, w, n, k, x)
     assert rel_err(y, want) < TOL[dtype], rel_err(y, want)
     dev.free_all()
 
