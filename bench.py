@@ -431,6 +431,9 @@ def phase_report(A, d, name, dtype, pos, layer):
             "head_workgroups_see_every_flag": med([t[0, h, 1] for h in heads]),
             "head_blocks_end": med([t[0, h, 2] for h in heads]),
             "head_keys_stored": med([t[0, h, 3] for h in heads]),
+            "head_final_sum_done": med([t[0, h, 4] for h in heads if t[0, h, 4] > 0]),
+            "head_norm_prep_done": med([t[0, h, 5] for h in heads if t[0, h, 5] > 0]),
+            "head_matvec_done": med([t[0, h, 6] for h in heads if t[0, h, 6] > 0]),
             "next_position_attention_wakes": med([t[1, g, 1] for g in groups]),
             "next_position_prologue_done": med([t[1, g, 2] for g in groups]),
         }

@@ -990,6 +990,29 @@ template <int N> __device__ __forceinline__ int lanes_mini(int v) {
 // a NaN never wins) into every thread: a wavefront's largest value (fmaxf passes NaN over), then the
 // lowest index that holds it; then the same over the wavefronts' results, which every wavefront reads
 // after one barrier. sv, si: NWE words each, not read again before a later barrier.
+// The same into wavefront 0 only (the head's key comes from thread 0): the wavefronts at and past
+// `busy` hold no rows, and store their empty result without reducing it; only wavefront 0 takes the
+// second stage, so the others leave at the barrier.
+__device__ void block_argmax0(float &v, int &i, float *sv, int *si, int busy) {
+    const int w = wave_id();
+    float m = -INFINITY;
+    int ci = 0x7FFFFFFF;
+    if (w < busy) {
+        m = lanes_max<64>(v);
+        ci = lanes_mini<64>(v == m ? i : 0x7FFFFFFF);
+    }
+    if ((tidx() & 63) == 0) { sv[w] = m; si[w] = ci; }
+    __syncthreads();
+    if (w == 0) {
+        const int k = tidx() & (NWE - 1);
+        const float vk = sv[k];
+        const int ik = si[k];
+        m = lanes_max<NWE>(vk);
+        ci = lanes_mini<NWE>(vk == m ? ik : 0x7FFFFFFF);
+    }
+    v = m;
+    i = ci;
+}
 __device__ void block_argmax(float &v, int &i, float *sv, int *si) {
     float m = lanes_max<64>(v);
     int ci = lanes_mini<64>(v == m ? i : 0x7FFFFFFF);
@@ -2068,7 +2091,7 @@ __device__ __forceinline__ l3m_dmat head_slice(const l3m_dmodel &M, int t0, int 
 // into slot pos % nslots, and this slice's (max, lowest index) in v, idx for every thread.
 template <int DT, bool PRE, bool G2 = false>
 __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &V, int t0, int tpw, int pos, HeadW<DT> &w,
-                                           uint8_t *smem, float &v, int &idx, float *keep = nullptr) {
+                                           uint8_t *smem, float &v, int &idx, float *keep = nullptr, int role = -1) {
     const int dim = M.dim, kp = kwide(dim);
     const LdsH L = lds_h(DT, dim, M.head.nb, tpw);
     float *work = (float *)(smem + L.work), *scr = (float *)(smem + L.scr);
@@ -2091,8 +2114,10 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
         head_issue<DT>(w, V);
         x = pro_finish<false>(P, M.pd, PG, false, (float4 *)work, nullptr, nullptr, w.st.cs, 0);
     }
+    if (role >= 0) phase(role, 4, pos, 0);
     if constexpr (G2) ln_prep<DT>(x, M.norm, M.norm_b, dim, kp, M.eps, act, red);
     else norm_prep<DT>(x, w.st.nw, dim, kp, M.eps, act, red);
+    if (role >= 0) phase(role, 5, pos, 0);
     // each row's logit from the lane that sums it: stored, and kept if it beats the lane's earlier rows
     float *lg = M.logits + (size_t)(pos % M.nslots) * M.vocab + (size_t)t0 * 16;
     v = -INFINITY;
@@ -2105,7 +2130,11 @@ __device__ __forceinline__ void head_block(const l3m_dmodel &M, const l3m_dmat &
         }
     };
     wide_rows(w.a, V, act, kp, work, V.rows, logit_row);
-    block_argmax(v, idx, scr, (int *)scr + 16);
+    if (role >= 0) phase(role, 6, pos, 0);
+    // the tile forms (quantized and bf16 heads) leave tile t's rows in wavefront t; f32 heads sum rows in
+    // every wavefront
+    constexpr bool by_tile = tiled<DT>() || DT == L3M_BF16;
+    block_argmax0(v, idx, scr, (int *)scr + 16, by_tile && V.tiles < NWE ? V.tiles : NWE);
 }
 
 // The argmax over n (value, index) partials, in index order (engine.c:294-300), into every thread.
@@ -2988,7 +3017,7 @@ __device__ __noinline__ bool head_role(const l3m_dmodel *Mp, const l3m_run *Rp, 
     phase(128 + h, 1, pos, M.n_layers - 1);
     const float temp = R.temp;
     float *keep = temp > 0 ? (float *)(smem + lds_h(DT, M.dim, M.head.nb, R.head_tpw).lgv) : nullptr;
-    if (has_tiles) head_block<DT, true, G2>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx, keep);
+    if (has_tiles) head_block<DT, true, G2>(M, V, t0, R.head_tpw, pos, wt, smem, v, idx, keep, 128 + h);
     phase(128 + h, 2, pos, M.n_layers - 1);
     if (tidx() == 0)
         __hip_atomic_store(gw((uint64_t *)(R.sync + SY_SLOTS) + h), argmax_key(v, idx, step_tag(s)), __ATOMIC_RELAXED,
