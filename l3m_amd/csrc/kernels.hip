@@ -5,7 +5,8 @@
 // consecutive 32-input blocks, so each step of a wavefront is one contiguous 1-4 KiB run of 128-bit
 // loads. The activation vector is prepared once per workgroup into LDS (l3m's per-32-block int8
 // quantization, or bf16, or f32) and broadcast from there. Per-block integer dots use v_dot4_i32_i8;
-// q4_0 nibbles are masked in registers, mxfp4 e2m1 codes go through two v_perm_b32 byte tables.
+// q4_0 nibbles go to v_dot8 as they are stored; mxfp4 e2m1 codes convert to f16 for v_dot2 in the decode
+// step, and go as they are stored to the matrix cores (fp4 operand) in the large standalone matvecs.
 // Reductions are fixed-order (wavefront shuffles, then LDS), so results are run-to-run identical.
 #include <hip/hip_runtime.h>
 #include <math.h>
