@@ -4,6 +4,7 @@
 // chunks, applies the stop rules and calls on_token.
 #include <math.h>
 #include <stdio.h>
+#include <stddef.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
@@ -40,17 +41,23 @@ struct l3m_model {
     l3m_graphs  *graphs;
     l3m_dlayer  *layers_dev;   // the layer descriptors in device memory (persistent kernel)
     l3m_dmodel  *dm_dev;       // dm in device memory
-    l3m_run     *run_dev;      // [2] the persistent kernel's launch parameters, one per run of steps in flight
-    l3m_run     *run_host;     // [2] their pinned host copies (queued to run_dev without a wait)
+    // The call area, one device allocation and its pinned host image (call_host), in this order: the first
+    // decoded position, the sampler state, the token ids [ctx + 1], then per run of steps in flight (slot)
+    // its launch parameters and its sync words (zero in the image). A generate call's inputs and its first
+    // run's parameters and zeroed sync words are one contiguous copy; each later run's, another.
+    uint8_t     *call_dev, *call_host;
+    size_t       call_samp, call_tok, call_slot[2];   // byte offsets in the call area
+    l3m_run     *run_dev[2];   // the persistent kernel's launch parameters, one per run of steps in flight
+    l3m_run     *run_host[2];  // their images
+    unsigned    *sync[2];      // L3M_SYNC_WORDS flag, key and output words of the persistent kernel, per run in flight
     l3m_chunk_out *out_host;   // [2] pinned: what each run of steps in flight hands back
     void        *ev[2];        // the end of each run of steps in flight (its copies back included)
-    int32_t     *stage_tok;    // pinned [ctx + 1]: the call's prompt ids, queued to the device without a wait
-    l3m_dsample *stage_smp;    // pinned: the call's sampler state
-    int         *stage_pos;    // pinned: the call's first decoded position
+    int32_t     *stage_tok;    // the call's prompt ids in the image
+    l3m_dsample *stage_smp;    // the call's sampler state in the image
+    int         *stage_pos;    // the call's first decoded position in the image
     int          persist;      // decode with the persistent kernel (else one graph per step)
     int          grid, head_tpw, n_head, body_xcc;
     unsigned     lds_decode;
-    unsigned    *sync;         // 2 areas of L3M_SYNC_WORDS flag and key words of the persistent kernel (per run in flight)
     double       work[3];      // persistent launches so far: steps, steps with the head, K/V rows read
     int          chunk_rows;   // FFN rows per chunk (the last chunk takes the rest)
     unsigned long long spin_limit;   // the persistent kernel's longest wait, 100 MHz ticks (1 s)
@@ -514,8 +521,28 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
 
     // activations and state
     size_t kv = (size_t)d->n_layers * d->n_kv * d->ctx * d->hd * 2;
-    d->pos = dalloc(m, 4);
-    d->tokens = dalloc(m, ((size_t)d->ctx + 1) * 4);
+    // the call area (struct l3m_model): 256-byte aligned pieces
+    m->call_samp = 256;
+    m->call_tok = m->call_samp + (sizeof(l3m_dsample) + 255) / 256 * 256;
+    m->call_slot[0] = m->call_tok + (((size_t)d->ctx + 1) * 4 + 255) / 256 * 256;
+    m->call_slot[1] = m->call_slot[0] + 256 + (size_t)L3M_SYNC_WORDS * 4;
+    const size_t call_bytes = m->call_slot[1] + 256 + (size_t)L3M_SYNC_WORDS * 4;
+    _Static_assert(sizeof(l3m_run) <= 256, "launch parameters fit their 256 bytes");
+    m->call_dev = dalloc(m, call_bytes);
+    m->call_host = l3m_dev_host_alloc(call_bytes);
+    if (!m->call_dev || !m->call_host) return fail(m, "device allocation failed");
+    memset(m->call_host, 0, call_bytes);
+    d->pos = (int *)m->call_dev;
+    d->samp = (l3m_dsample *)(m->call_dev + m->call_samp);
+    d->tokens = (int32_t *)(m->call_dev + m->call_tok);
+    m->stage_pos = (int *)m->call_host;
+    m->stage_smp = (l3m_dsample *)(m->call_host + m->call_samp);
+    m->stage_tok = (int32_t *)(m->call_host + m->call_tok);
+    for (int sl = 0; sl < 2; sl++) {
+        m->run_dev[sl] = (l3m_run *)(m->call_dev + m->call_slot[sl]);
+        m->run_host[sl] = (l3m_run *)(m->call_host + m->call_slot[sl]);
+        m->sync[sl] = (unsigned *)(m->call_dev + m->call_slot[sl] + 256);
+    }
     d->xa = dalloc(m, (size_t)d->dim * 4);
     d->xb = dalloc(m, (size_t)d->dim * 4);
     d->po = dalloc(m, (size_t)d->n_groups * d->dim * 4);
@@ -534,7 +561,6 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
         const char *pg = getenv("L3M_PREFILL_GRAPH");  // 0: loose launches (for comparison)
         if ((!pg || strcmp(pg, "0")) && !(m->pfg = l3m_pfgraphs_new())) return fail(m, "out of host memory");
     }
-    d->samp = dalloc(m, sizeof(l3m_dsample));
     d->logits = dalloc(m, (size_t)NSLOTS * d->vocab * 4);
     // persistent kernel: one workgroup per CU (the LDS request keeps a second one off each CU); the body
     // (head groups, then FFN chunks) on the workgroups of one XCD, every other workgroup on head tiles.
@@ -571,13 +597,7 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     int parts = d->head_grid > m->grid ? d->head_grid : m->grid;
     d->part_val = dalloc(m, (size_t)parts * 4);
     d->part_idx = dalloc(m, (size_t)parts * 4);
-    m->sync = dalloc(m, 2 * (size_t)L3M_SYNC_WORDS * 4);
-    m->run_dev = dalloc(m, 2 * sizeof(l3m_run));
-    m->run_host = l3m_dev_host_alloc(2 * sizeof(l3m_run));
     m->out_host = l3m_dev_host_alloc(2 * sizeof(l3m_chunk_out));
-    m->stage_tok = l3m_dev_host_alloc(((size_t)d->ctx + 1) * 4);
-    m->stage_smp = l3m_dev_host_alloc(sizeof(l3m_dsample));
-    m->stage_pos = l3m_dev_host_alloc(sizeof(int));
     m->ev[0] = l3m_dev_event_new();
     m->ev[1] = l3m_dev_event_new();
     m->dm_dev = dalloc(m, sizeof(l3m_dmodel));
@@ -591,8 +611,8 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
     free(rope);
     m->logits = calloc((size_t)d->vocab, sizeof *m->logits);
     if (!d->pos || !d->tokens || !d->xa || !d->xb || !d->po || !d->pd || !d->samp || !d->logits || !d->part_val || !d->part_idx || !d->done ||
-        !d->kc || !d->vc || !d->rope || !d->norm || !m->logits || !m->sync || !m->layers_dev || !m->run_dev || !m->run_host ||
-        !m->out_host || !m->stage_tok || !m->stage_smp || !m->stage_pos || !m->ev[0] || !m->ev[1] ||
+        !d->kc || !d->vc || !d->rope || !d->norm || !m->logits || !m->layers_dev ||
+        !m->out_host || !m->ev[0] || !m->ev[1] ||
         !m->dm_dev || l3m_dev_upload(m->dm_dev, d, sizeof *d))
         return fail(m, "device allocation failed");
     m->cold = o.cold != 0;
@@ -622,11 +642,8 @@ void l3m_free(l3m_model *m) {
     l3m_dev_sync();
     l3m_graphs_free(m->graphs);
     l3m_pfgraphs_free(m->pfg);
-    l3m_dev_host_free(m->run_host);
+    l3m_dev_host_free(m->call_host);
     l3m_dev_host_free(m->out_host);
-    l3m_dev_host_free(m->stage_tok);
-    l3m_dev_host_free(m->stage_smp);
-    l3m_dev_host_free(m->stage_pos);
     l3m_dev_event_free(m->ev[0]);
     l3m_dev_event_free(m->ev[1]);
     for (int i = 0; i < m->n_allocs; i++) l3m_dev_free(m->allocs[i]);
@@ -644,19 +661,23 @@ static int step(l3m_model *m, int with_head) {
 // run's tokens) into slot's pinned area, then slot's event. Nothing waits: two runs can be in flight, each
 // with its own sync area, launch parameters and pinned area. The sync words are zeroed and the parameters
 // copied on the stream, behind the run that used slot before (which the host has waited for).
-static int chunk_enqueue(l3m_model *m, int first, int last, int head_from, int slot) {
+// from: the call-area byte offset the run's upload starts at (the slot's own parameters, or the start of
+// the call area for a call's first run, whose inputs go with them); -1: nothing to upload.
+static int chunk_enqueue(l3m_model *m, int first, int last, int head_from, int slot, long from) {
     const l3m_dmodel *d = &m->dm;
     l3m_chunk_out *out = &m->out_host[slot];
+    const int f = first > head_from ? first : head_from, ntok = last >= f ? last - f + 1 : 0;
     if (m->persist) {
-        unsigned *sync = m->sync + (size_t)slot * L3M_SYNC_WORDS;
-        if (l3m_dev_zero_async(sync, (size_t)L3M_SYNC_WORDS * 4)) return -1;
+        // the parameters and the zeroed sync words in one copy from the image; the output span (abort word,
+        // wait ticks, tokens) back in one copy
+        unsigned *sync = m->sync[slot];
         const l3m_run r = {first, last - first + 1, head_from, m->head_tpw, m->n_head, m->body_xcc, sync, m->spin_limit, m->temp, 0};
-        m->run_host[slot] = r;
-        if (l3m_dev_upload_async(m->run_dev + slot, m->run_host + slot, sizeof r) ||
-            l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, m->dm_dev, m->layers_dev, m->run_dev + slot, m->grid, m->lds_decode, NULL,
+        *m->run_host[slot] = r;
+        const size_t end = m->call_slot[slot] + 256 + (size_t)L3M_SYNC_WORDS * 4;
+        if (l3m_dev_upload_async(m->call_dev + from, m->call_host + from, end - (size_t)from) ||
+            l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, m->dm_dev, m->layers_dev, m->run_dev[slot], m->grid, m->lds_decode, NULL,
                               slot) ||
-            l3m_dev_download_async(&out->abort, sync + L3M_SYNC_ABORT, 4) ||
-            l3m_dev_download_async(&out->waited, sync + L3M_SYNC_WAIT, 8))
+            l3m_dev_download_async(out, sync + L3M_SYNC_OUT, offsetof(l3m_chunk_out, tok) + (size_t)ntok * 4))
             return -1;
         for (int p = first; p <= last; p++) {
             m->work[0] += 1;
@@ -666,11 +687,13 @@ static int chunk_enqueue(l3m_model *m, int first, int last, int head_from, int s
     } else {
         out->abort = 0;
         out->waited = 0;
+        // a call's inputs: the position, the sampler state and the prompt's ids (head_from + 1 of them)
+        if (from >= 0 && l3m_dev_upload_async(m->call_dev + from, m->call_host + from, m->call_tok - (size_t)from + (size_t)(head_from + 1) * 4))
+            return -1;
         for (int p = first; p <= last; p++)
             if (step(m, p >= head_from)) return -1;
+        if (ntok && l3m_dev_download_async(out->tok, d->tokens + f + 1, (size_t)ntok * 4)) return -1;
     }
-    const int f = first > head_from ? first : head_from;
-    if (last >= f && l3m_dev_download_async(out->tok, d->tokens + f + 1, (size_t)(last - f + 1) * 4)) return -1;
     return l3m_dev_event_record(m->ev[slot]);
 }
 
@@ -721,19 +744,21 @@ static int run_steps(l3m_model *m, const int32_t *prompt, int n_prompt, int max_
     for (int h = 0; h < L3M_MAX_HEAD_WGS; h++) smp->rng[h] = seed * 0x9E3779B97F4A7C15ull + 1;   // engine.c:555
     m->temp = smp->temp;
     memcpy(m->stage_tok, prompt, (size_t)n_prompt * 4);
-    // the pinned stage was last read by the previous call's copies, which its final wait covered
-    if (l3m_dev_upload_async(d->tokens, m->stage_tok, (size_t)n_prompt * 4) || l3m_dev_upload_async(d->samp, smp, sizeof *smp)) return -1;
+    // the image was last read by the previous call's copies, which its final wait covered
     // a long prompt: positions 0..n_prompt-2 in one batched pass, then decode from the last prompt token
-    int next = 0;
+    const int prefill = m->pf && n_prompt - 1 >= m->prefill_min && n_prompt - 1 >= 1;
+    int next = prefill ? n_prompt - 1 : 0;
+    *m->stage_pos = next;
+    long from = 0;                                     // the first run takes the call's inputs with it
     m->prefilled = 0;
-    if (m->pf && n_prompt - 1 >= m->prefill_min && n_prompt - 1 >= 1) {
+    if (prefill) {                                     // the prefill reads the prompt ids first
+        if (l3m_dev_upload_async(m->call_dev, m->call_host, m->call_tok + (size_t)n_prompt * 4)) return -1;
+        from = -1;
         if (m->cold && evict(m)) return -1;
         if (m->pfg ? l3m_prefill_graph(m->pfg, d, m->pf, &m->pfb, n_prompt - 1) : l3m_prefill(d, m->pf, &m->pfb, n_prompt - 1, NULL))
             return -1;
-        next = m->prefilled = n_prompt - 1;
+        m->prefilled = n_prompt - 1;
     }
-    *m->stage_pos = next;
-    if (l3m_dev_upload_async(d->pos, m->stage_pos, 4)) return -1;
     const int live = on_token != NULL || bos >= 0 || eos >= 0, depth = m->cold ? 1 : 2;
     int q_first[2], q_end[2], q_slot[2], nq = 0, slot = 0;
     for (;;) {
@@ -742,7 +767,9 @@ static int run_steps(l3m_model *m, const int32_t *prompt, int n_prompt, int max_
             int len = m->cold ? 1 : !live ? NSLOTS : next <= n_prompt - 1 ? n_prompt - next : LIVE_STEPS;
             if (len > NSLOTS) len = NSLOTS;
             const int end = next + len - 1 < last ? next + len - 1 : last;
-            if ((m->cold && evict(m)) || chunk_enqueue(m, next, end, n_prompt - 1, slot)) {
+            const long up = from >= 0 ? from : m->persist ? (long)m->call_slot[slot] : -1;
+            from = -1;
+            if ((m->cold && evict(m)) || chunk_enqueue(m, next, end, n_prompt - 1, slot, up)) {
                 rc = -1;
                 break;
             }

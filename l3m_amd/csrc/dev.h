@@ -83,8 +83,11 @@ typedef struct {
     unsigned           pad;
 } l3m_run;
 #define L3M_MAX_HEAD_WGS 256                         // the key area holds this many keys, whatever n_head is
-#define L3M_SYNC_WORDS (256 + 4 * L3M_MAX_HEAD_WGS)  // flag words, one 64-bit key per head workgroup, then
-                                                     // one 64-bit slice total per head workgroup (sampling)
+// Flag words, one 64-bit key per head workgroup, one 64-bit slice total per head workgroup (sampling),
+// then the run's output span: the abort word, the wait ticks and the run's tokens, laid out as the host's
+// l3m_chunk_out so that one copy brings all of it back.
+#define L3M_SYNC_OUT (256 + 4 * L3M_MAX_HEAD_WGS)
+#define L3M_SYNC_WORDS (L3M_SYNC_OUT + 256)
 // Device-resident sampling state, set by the host at the start of each generate call. Every workgroup
 // that takes part in sampling keeps its own copy of the xorshift64* state (engine.c:98-101) and advances
 // it once per sampled token, so all copies stay equal: rng[h] for head workgroup h of the persistent
@@ -94,8 +97,9 @@ typedef struct l3m_dsample {
     unsigned           pad;
     unsigned long long rng[L3M_MAX_HEAD_WGS];
 } l3m_dsample;
-#define L3M_SYNC_ABORT 192                           // the word a timed-out wait sets
-#define L3M_SYNC_WAIT 248                            // 64-bit: 100 MHz ticks attention group 0 waited for its inputs this launch
+#define L3M_SYNC_ABORT L3M_SYNC_OUT                  // the word a timed-out wait sets
+#define L3M_SYNC_WAIT (L3M_SYNC_OUT + 2)             // 64-bit: 100 MHz ticks attention group 0 waited for its inputs this launch
+#define L3M_SYNC_TOK (L3M_SYNC_OUT + 4)              // the run's tokens, from its first position with a token (at most 128)
 
 // ------------------------------------------------------------------ runtime
 int         l3m_dev_init(void);                 // 0 when a gfx9 HIP device is usable

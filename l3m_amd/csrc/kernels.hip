@@ -2606,7 +2606,13 @@ __global__ void __launch_bounds__(NTE) k_head_block(l3m_dmodel M, int advance) {
 enum { SY_ATTN = 0, SY_FFN = 64, SY_ABORT = L3M_SYNC_ABORT, SY_TOKEN = 208, SY_TICKET = 224, SY_HEAD_TICKET = 240,
        SY_SLOTS = 256 };
 constexpr int SY_SUMS = SY_SLOTS + 2 * L3M_MAX_HEAD_WGS;   // slice totals (sampling) follow the keys
-static_assert(L3M_SYNC_WORDS == SY_SUMS + 2 * L3M_MAX_HEAD_WGS && L3M_MAX_HEAD_WGS == 256, "keys and totals follow the flag words");
+static_assert(L3M_SYNC_OUT == SY_SUMS + 2 * L3M_MAX_HEAD_WGS && L3M_MAX_HEAD_WGS == 256, "keys and totals follow the flag words");
+static_assert(L3M_SYNC_TOK + 128 <= L3M_SYNC_WORDS, "a run's tokens fit its output span");
+// The run's token at position p + 1 (p >= head_from), into the output span the host copies back.
+__device__ __forceinline__ void out_token(const l3m_run &R, int p, int tok) {
+    const int f = R.pos0 > R.head_from ? R.pos0 : R.head_from;
+    gw((int *)(R.sync + L3M_SYNC_TOK))[p - f] = tok;
+}
 
 __device__ __forceinline__ unsigned xcc_id() {
     unsigned x;
@@ -2844,7 +2850,10 @@ __device__ __noinline__ bool attn_role(const l3m_dmodel *Mp, const l3m_dlayer *l
             tok = R.temp > 0 ? wait_token_word(sync + SY_TOKEN, s - 1, abort_flag, R.spin_limit, &ok_lds)
                                    : wait_token((const uint64_t *)(sync + SY_SLOTS), R.n_head, s - 1, abort_flag, R.spin_limit, &ok_lds);
             if (tok < 0) return false;
-            if (g == 0 && tidx() == 0) gw(M.tokens)[pos] = tok;
+            if (g == 0 && tidx() == 0) {
+                gw(M.tokens)[pos] = tok;
+                out_token(R, pos - 1, tok);
+            }
         } else {
             if (epoch > 0 && !wait_flags<0, true>(sync + SY_FFN, M.n_chunks, epoch, abort_flag, R.spin_limit, &ok_lds)) return false;
             if (l == 0) tok = __hip_atomic_load(gp<int32_t>(M.tokens + pos), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -3072,7 +3081,10 @@ __global__ void __launch_bounds__(NTE) k_decode(const l3m_dmodel *__restrict__ M
         const int tok = R.temp > 0
                             ? wait_token_word(R.sync + SY_TOKEN, R.nsteps - 1, R.sync + SY_ABORT, R.spin_limit, &role_lds)
                             : wait_token((const uint64_t *)(R.sync + SY_SLOTS), R.n_head, R.nsteps - 1, R.sync + SY_ABORT, R.spin_limit, &role_lds);
-        if (tok >= 0 && tidx() == 0) gw(Mp->tokens)[last + 1] = tok;
+        if (tok >= 0 && tidx() == 0) {
+            gw(Mp->tokens)[last + 1] = tok;
+            out_token(R, last, tok);
+        }
     }
 }
 
@@ -3546,18 +3558,16 @@ int g_dec_timing, g_dec_launches, g_dec_pending[2];
 double g_dec_us;
 template <int DT, int HDT, bool G2> int launch_decode(const l3m_dmodel *M_dev, const l3m_dlayer *layers, const l3m_run *R_dev, int grid,
                                                       unsigned lds, hipStream_t st, int slot) {
-    lds_opt_in(k_decode<DT, HDT, G2>, lds);
+    static unsigned opted;                            // per instantiation: set once, again only for more
+    if (lds > opted) {
+        lds_opt_in(k_decode<DT, HDT, G2>, lds);
+        opted = lds;
+    }
     const l3m_dmodel *m = M_dev;
     const l3m_dlayer *ly = layers;
     const l3m_run *r = R_dev;
     void *args[] = {&m, &ly, &r};
-    if (g_dec_timing) {
-        if (!g_dec_ev[slot][0]) {
-            CK(hipEventCreate(&g_dec_ev[slot][0]));
-            CK(hipEventCreate(&g_dec_ev[slot][1]));
-        }
-        CK(hipEventRecord(g_dec_ev[slot][0], st));
-    }
+    if (g_dec_timing) CK(hipEventRecord(g_dec_ev[slot][0], st));
     hipError_t e;
     if (g_coop) {
         e = hipLaunchCooperativeKernel((const void *)k_decode<DT, HDT, G2>, dim3(grid), dim3(NTE), args, lds, st);
@@ -4039,6 +4049,9 @@ int l3m_decode_timer_collect(int slot) { return slot < 0 || slot > 1 ? -1 : time
 int l3m_decode_timer(int mode, double *us, int *launches) {
     if (l3m_dev_init()) return -1;
     if (mode == 1) {                                   // start: clear and time from now on
+        for (int s = 0; s < 2; s++)                   // made here, outside the timed calls
+            for (int e = 0; e < 2; e++)
+                if (!g_dec_ev[s][e]) CK(hipEventCreate(&g_dec_ev[s][e]));
         g_dec_timing = 1; g_dec_us = 0; g_dec_launches = 0; g_dec_pending[0] = g_dec_pending[1] = 0;
     } else if (mode == 2) {                            // collect the finished launches (their stream has been waited for)
         if (timer_collect(0) || timer_collect(1)) return -1;
