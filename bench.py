@@ -272,7 +272,7 @@ def cpu_matvec_lib():
     return lib
 
 
-def matvec_bench(A, dtypes, iters=50, cpu_seconds=0.2):
+def matvec_bench(A, dtypes, iters=50, cpu_seconds=0.2, shapes=None):
     """Warm: one matrix re-read; cold: round robin over copies totalling > 512 MiB (beyond the 256 MB
     Infinity Cache). Launches run back to back and each figure is their mean interval; where the warm
     matvec or read is within 1.5x of an empty kernel's launch interval, warm_launch_bound marks it (those
@@ -291,7 +291,7 @@ def matvec_bench(A, dtypes, iters=50, cpu_seconds=0.2):
     for name in dtypes:
         dt = A.DTYPES[name]
         res = {}
-        for n, k in MICRO_SHAPES:
+        for n, k in shapes or MICRO_SHAPES:
             w = make_rows(dt, n, k, seed=n + k)
             x = np.random.default_rng(0).standard_normal(k).astype(np.float32)
             q, s = dev.pack_rows(dt, w, k)
@@ -479,6 +479,8 @@ def main():
     ap.add_argument("--phases", default="", help="only per-phase timing of CONFIG:DTYPE:POS:LAYER (e.g. stories110M:q4_0:64:5), "
                                                 "with l3m_amd/libl3m_hip_phases.so, one JSON line")
     ap.add_argument("--only-decode", action="store_true", help="the headline decode only (for profiling runs)")
+    ap.add_argument("--matvec-shapes", default="", help="rowsxk,... : only these shapes in the matvec microbench (counter passes)")
+    ap.add_argument("--matvec-iters", type=int, default=50, help="timed launches per matvec figure (at least 2 per copy when cold)")
     ap.add_argument("--matvec-only", action="store_true", help="only the matvec microbench, one JSON line (profiling runs "
                                                                "of the matvec kernels: no decode, no persistent launch)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -501,7 +503,9 @@ def main():
         print(json.dumps({"probes": probes(A)}), flush=True)
         return
     if a.matvec_only:
-        print(json.dumps({"matvec": matvec_bench(A, [s for s in a.matvec.split(",") if s], cpu_seconds=a.cpu_matvec_seconds)}), flush=True)
+        shapes = [tuple(int(v) for v in sh.split("x")) for sh in a.matvec_shapes.split(",") if sh]
+        print(json.dumps({"matvec": matvec_bench(A, [s for s in a.matvec.split(",") if s], iters=a.matvec_iters,
+                                                 cpu_seconds=a.cpu_matvec_seconds, shapes=shapes)}), flush=True)
         return
     cfg = A.CONFIGS[a.config]
     dtype = a.dtype or cfg.dtype
