@@ -206,14 +206,16 @@ def test_argmax_lowest_index_wins(dev):
 
 @pytest.mark.parametrize("dtype", [F32, BF16, Q8_0, Q4_0, MXFP4], ids=NAMES.get)
 def test_table_matches_reference_tables(reference, dtype):
-    """l3m_kernels_hip on the reference's own packed tiles and prepared vector, against its scalar table."""
+    """l3m_kernels_hip on the reference's own packed tiles and prepared vector, against its scalar table; the
+    128-tile case takes the 8-wavefront matvecs (mxfp4 on the matrix cores, from the table's own prepared
+    form)."""
     import ctypes as C
     import l3m_amd as A
     from oracle.oracle import _Table
     lib = A.lib()
     table = _Table.in_dll(lib, "l3m_kernels_hip")
     assert table.name == b"hip"
-    for k, ntiles in [(288, 3), (1376, 2), (3072, 5)]:
+    for k, ntiles in [(288, 3), (1376, 2), (3072, 5), (4096, 128)]:
         n = ntiles * 16
         w = rows(dtype, n, k, seed=k + dtype)
         tiles = reference.pack_tiles(dtype, [w[i] if i < n - 3 else None for i in range(n)], k)
