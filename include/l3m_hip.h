@@ -198,6 +198,12 @@ double l3m_weight_bytes(const l3m_model *m);                       // weight byt
 // l3m_generate returns -1 ("a wait between phases timed out"). A test hook for that path (no counterpart in
 // the reference, whose barrier waits without bound, pool.c:111-123).
 void   l3m_decode_spin_limit(l3m_model *m, long long ticks);
+// Whether the mxfp4 matvecs of at least 128 tiles of 64-256 blocks (l3m_k_gemv) take the matrix cores (1,
+// the default; L3M_GEMV_MX=0 in the environment starts at 0) or the VALU dots of the other dtypes' 8-wavefront
+// matvec (0); on < 0 only reads it. Returns the setting before the call. A test and measurement hook (no
+// counterpart in the reference): at 128 blocks per row both forms split a tile over 8 wavefronts and add
+// each lane's blocks in the same order, so their results are bit-identical.
+int    l3m_gemv_matrix_cores(int on);
 // 1 when decode runs as one persistent cooperative kernel per chunk of steps (L3M_PERSIST=0 at load
 // selects the one-graph-per-step path), 0 otherwise.
 int    l3m_decode_persistent(const l3m_model *m);

@@ -75,7 +75,7 @@ l3m_dev_evict i p z p           | l3m_decode_attention i p       | l3m_kv_rows i
 l3m_decode_window i p
 l3m_k_step_mv i i i M p i p i p  | l3m_step_matvec i p i i i *f *f | l3m_step_layout v p *i
 l3m_widen_rows i i i i ** p | l3m_decode_spin_limit v p l | l3m_time_launch_interval d i
-l3m_tokenize i s s i *I i | l3m_head_dim i p
+l3m_tokenize i s s i *I i | l3m_head_dim i p | l3m_gemv_matrix_cores i i
 l3m_time_read d ** i z i         | l3m_hip_attend_noalloc i p p p p i i i | l3m_phase_stamps i i i i p
 """
 _SIG = {}

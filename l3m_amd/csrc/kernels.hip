@@ -3747,6 +3747,16 @@ int l3m_dev_event_wait(void *e) {
 
 size_t l3m_act_bytes(int dtype, int k) { return act_bytes(dtype, k); }
 
+int l3m_gemv_matrix_cores(int on) {
+    if (g_gemv_mx < 0) {
+        const char *e = getenv("L3M_GEMV_MX");
+        g_gemv_mx = !(e && !strcmp(e, "0"));
+    }
+    const int was = g_gemv_mx;
+    if (on >= 0) g_gemv_mx = on != 0;
+    return was;
+}
+
 int l3m_k_prep(int dtype, const float *x, int k, void *act, void *stream) {
     if (k < 1 || dtype < 0 || dtype >= L3M_NDTYPES || smem_bytes(dtype, k) > LDS_MAX) return fail_msg("prep: k out of range for this dtype");
     hipStream_t st = as_stream(stream);

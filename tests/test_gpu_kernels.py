@@ -138,6 +138,31 @@ def test_gemv_deep_edges(dev, oracle, dtype, k):
     dev.free_all()
 
 
+@pytest.mark.parametrize("k", [4096])
+def test_gemv_mxfp4_matrix_cores_equal_valu_dots(dev, oracle, k):
+    """The matrix-core mxfp4 matvec gives the VALU form's results bit for bit at 128 blocks per row (the same
+    per-block values, the same split over 8 wavefronts and order of additions), extremes included, and
+    meets the oracle. (At 64 blocks per row the two forms split a tile differently; at 256 the VALU form's
+    activation does not fit the 8-wavefront kernel's staging and the 4-wavefront kernel runs.)"""
+    n = 2048 + 16 * 3
+    w = extremes(MXFP4, rows(MXFP4, n, k, seed=k + 3), k)
+    w[::7] = rows(MXFP4, n, k, seed=k + 4)[::7]          # ordinary scales on every 7th row
+    x = np.random.default_rng(6).standard_normal(k).astype(np.float32)
+    x[32:64] = 0
+    m = dev.matrix(MXFP4, w, k)
+    was = dev.lib.l3m_gemv_matrix_cores(1)
+    try:
+        y_mx = dev.gemv(m, x)
+        dev.lib.l3m_gemv_matrix_cores(0)
+        y_valu = dev.gemv(m, x)
+    finally:
+        dev.lib.l3m_gemv_matrix_cores(was)
+    assert np.array_equal(y_mx.view(np.uint32), y_valu.view(np.uint32))
+    want = oracle.gemv(MXFP4, w, n, k, x)
+    assert rel_err(y_mx, want) < TOL[MXFP4], rel_err(y_mx, want)
+    dev.free_all()
+
+
 @pytest.mark.parametrize("dtype,k", [(F32, 2), (F32, 18), (F32, 34), (BF16, 2), (BF16, 18), (BF16, 34)])
 def test_gemv_ragged_k(dev, oracle, dtype, k):
     n = 33
