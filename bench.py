@@ -440,8 +440,14 @@ def phase_report(A, d, name, dtype, pos, layer):
     return rep
 
 
+# the dependent steps of l3m_probe_latency, by index
+LATENCY_STEPS = ["LDS hand-over (write, barrier, read, barrier)", "dependent LDS read", "64-lane DPP/permlane sum",
+                 "bf16 matrix-core product 16x16x32", "barrier", "LDS write and read-back", "expf"]
+
+
 def probes(A):
-    """The residency and exchange probes (the GPU analogues of bench/residency.c and bench/exchange.c)."""
+    """The residency and exchange probes (the GPU analogues of bench/residency.c and bench/exchange.c), and the
+    latencies of the dependent steps inside one workgroup that the decode kernel's phases are built from."""
     lib, out = A.lib(), {"stream": [], "exchange": [], "graph_node_us": None}
     v = C.c_double()
     for xcds in (1, 8):
@@ -459,6 +465,11 @@ def probes(A):
                 out["exchange"].append({"workgroups": n, "same_xcd": bool(same), "dim": 768, "us_per_round": round(v.value, 3)})
     if lib.l3m_probe_graph_node(256, 20, C.byref(v)) == 0:
         out["graph_node_us"] = round(v.value, 3)
+    out["latency_clocks"] = []
+    for which, name in enumerate(LATENCY_STEPS):
+        for threads in (64, 1024):
+            if lib.l3m_probe_latency(which, threads, C.byref(v)) == 0:
+                out["latency_clocks"].append({"step": name, "threads": threads, "clocks": round(v.value, 1)})
     return out
 
 

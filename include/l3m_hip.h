@@ -236,10 +236,15 @@ int    l3m_head_dim(const l3m_model *m);   // hd of m: the row length of l3m_kv_
 // counterpart in its library): bandwidth of workgroups streaming their own shards (per_xcd workgroups on
 // each of the first xcds XCDs, bytes_per_wg each, warm, passes per launch), in GB/s; microseconds per
 // exchange round of n workgroups (each writes its slice of a dim-float vector, flags, waits for all flags,
-// reads the vector; on one XCD or across XCDs); microseconds per node of a hipGraph of empty kernels.
+// reads the vector; on one XCD or across XCDs); microseconds per node of a hipGraph of empty kernels;
+// shader clocks per dependent step inside one workgroup of `threads` threads (a power of two, 64-1024), for
+// which = 0 an LDS hand-over (write, barrier, another lane's word read, barrier), 1 a dependent LDS read,
+// 2 a 64-lane sum by DPP and permlane swaps, 3 a bf16 matrix-core product (16x16x32) into its own
+// accumulator, 4 a barrier, 5 an LDS write and read-back, 6 expf.
 int    l3m_probe_stream(size_t bytes_per_wg, int xcds, int per_xcd, int passes, double *gbs);
 int    l3m_probe_exchange(int n, int same_xcd, int dim, int rounds, double *us_per_round);
 int    l3m_probe_graph_node(int nodes, int reps, double *us_per_node);
+int    l3m_probe_latency(int which, int threads, double *clocks);
 
 // l3m_encode (src/l3m.h:48, tokenizer.c:156-170) on the tokenizer of the file at path, on the host alone (no
 // device needed): the count, or -1 when the file is refused or the ids do not fit max.

@@ -69,7 +69,7 @@ l3m_gen_u64 q q q               | l3m_gen_normal f q q           | l3m_quantize_
 l3m_f32_to_f16 w f               | l3m_decode_persistent i p      | l3m_decode_timer i i *d *i
 l3m_decode_work v p *d          | l3m_logits_at i p i *f         | l3m_bench_decode_t d p *I i i f q
 l3m_prefill_positions i p       | l3m_probe_stream i z i i i *d   | l3m_probe_exchange i i i i i *d
-l3m_probe_graph_node i i i *d
+l3m_probe_graph_node i i i *d   | l3m_probe_latency i i i *d
 l3m_k_dequant i M i i p p       | l3m_attention_mode i i i i i   | l3m_k_attend_decode i i p p p p i i i i i p
 l3m_dev_evict i p z p           | l3m_decode_attention i p       | l3m_kv_rows i p i i i i p p
 l3m_decode_window i p

@@ -3438,6 +3438,55 @@ __global__ void __launch_bounds__(NTE) k_probe_exchange(float *vec, int dim, int
 
 __global__ void k_probe_empty() {}
 
+// Latencies inside one workgroup, the steps every phase of the decode kernel is built from: thread 0
+// reads the shader clock (s_memtime) around `iters` repetitions of one dependent step, each taking the
+// previous one's result:
+//   0 every thread writes an LDS word, barrier, reads another wavefront's word, barrier (a hand-over
+//     through LDS); 1 a dependent LDS read; 2 a 64-lane sum (DPP and permlane swaps, lanes_sum);
+//   3 a bf16 matrix-core product into its own accumulator (16x16x32); 4 a barrier; 5 an LDS write, a wait,
+//   the same word read back; 6 expf.
+// The step's latency is the difference of two launches (iters and 2 iters) over iters. blockDim.x is a power
+// of two from 64 to NTE (with 64 threads, mode 0's word comes from the same wavefront).
+template <int MODE>
+__global__ void __launch_bounds__(NTE) k_probe_latency(unsigned long long *out, float *sink, int iters) {
+    __shared__ float buf[2 * NTE];
+    const int t = tidx(), n = blockDim.x;
+    buf[t] = (float)t;
+    buf[t + NTE] = 0.f;
+    __syncthreads();
+    float v = (float)(t & 7);
+    int idx = t;
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+    const bf16x8 a = {}, b = {};
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+#pragma unroll 8
+    for (int i = 0; i < iters; i++) {
+        if constexpr (MODE == 0) {
+            buf[t] = v;
+            __syncthreads();
+            v += buf[(t + 65) & (n - 1)];
+            __syncthreads();
+        } else if constexpr (MODE == 1) {
+            idx = ((int)buf[idx] + 1) & (n - 1);
+        } else if constexpr (MODE == 2) {
+            v = lanes_sum<64>(v) * 0.001f;
+        } else if constexpr (MODE == 3) {
+            c = mfma_bf16(a, b, c);
+        } else if constexpr (MODE == 4) {
+            __syncthreads();
+        } else if constexpr (MODE == 5) {
+            buf[t + NTE] = v;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            v = buf[t + NTE] + 1.0f;
+        } else {
+            v = expf(v * 0.5f - 1.0f);
+        }
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    if (t == 0) gw(out)[0] = t1 - t0;
+    if (v == 12345.f || idx < 0 || c[0] == 12345.f) gw(sink)[t] = v + (float)idx + c[0];   // keeps the work
+}
+
 // ----------------------------------------------------------------------------------------- runtime
 
 char g_err[512];
@@ -4363,6 +4412,32 @@ int l3m_probe_graph_node(int nodes, int reps, double *us_per_node) {
     if (cs) (void)hipStreamDestroy(cs);
     if (e != hipSuccess) return fail("probe_graph_node", e);
     *us_per_node = 1e3 * ms / ((double)reps * nodes);
+    return 0;
+}
+
+int l3m_probe_latency(int which, int threads, double *clocks) {
+    if (l3m_dev_init()) return -1;
+    if (which < 0 || which > 6 || threads < 64 || threads > NTE || (threads & (threads - 1)))
+        return fail_msg("probe_latency: bad arguments (which 0-6, threads a power of two from 64 to 1024)");
+    void (*const kernels[7])(unsigned long long *, float *, int) = {k_probe_latency<0>, k_probe_latency<1>, k_probe_latency<2>,
+                                                                    k_probe_latency<3>, k_probe_latency<4>, k_probe_latency<5>,
+                                                                    k_probe_latency<6>};
+    unsigned long long *out = nullptr;
+    float *sink = nullptr;
+    CK(hipMalloc(&out, 8));
+    if (hipMalloc(&sink, NTE * sizeof(float)) != hipSuccess) { (void)hipFree(out); return fail_msg("probe_latency: out of memory"); }
+    const int iters = 1000;
+    unsigned long long got[2] = {0, 0};
+    hipError_t e = hipSuccess;
+    for (int k = 0; k < 2 && e == hipSuccess; k++) {
+        hipLaunchKernelGGL(kernels[which], dim3(1), dim3(threads), 0, g_stream, out, sink, (k + 1) * iters);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipMemcpyAsync(got + k, out, 8, hipMemcpyDeviceToHost, g_stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    }
+    (void)hipFree(out); (void)hipFree(sink);
+    if (e != hipSuccess) return fail("probe_latency", e);
+    *clocks = ((double)got[1] - (double)got[0]) / iters;
     return 0;
 }
 

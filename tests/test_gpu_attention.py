@@ -32,7 +32,8 @@ def want(oracle, q, kc, vc, nq, nkv, hd, pos):
 
 # (mode, hd, nq, nkv, ctx): the window of modes 1 and 2 must fit in LDS beside the rest, so their ctx is
 # the largest that does for the shape; mode 0 takes the longest positions.
-CASES = [(2, 64, 1, 1, 512), (2, 64, 2, 1, 320), (2, 48, 1, 1, 512), (2, 48, 2, 2, 256), (2, 48, 2, 1, 512), (1, 64, 1, 1, 512), (1, 48, 2, 2, 256), (1, 48, 2, 1, 512),
+CASES = [(2, 64, 1, 1, 512), (2, 64, 2, 1, 320), (2, 48, 1, 1, 512), (2, 48, 2, 2, 256), (2, 48, 2, 1, 512), (2, 32, 1, 1, 512),
+         (2, 80, 1, 1, 256), (2, 80, 2, 1, 256), (1, 64, 1, 1, 512), (1, 48, 2, 2, 256), (1, 48, 2, 1, 512),
          (0, 64, 1, 1, 1024), (0, 48, 2, 2, 1024), (0, 64, 3, 1, 1024), (0, 32, 1, 1, 1024)]
 
 
