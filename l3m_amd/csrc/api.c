@@ -1,7 +1,8 @@
 // The l3m model API (src/l3m.h) on one MI355X: load a .l3m file into device memory in the lane-tile
 // layout, then run the reference's generate loop (engine.c:322-362, 549-561) with every forward pass on
-// the GPU, captured as one graph per step. The host only feeds prompt ids, reads back the argmax ids in
-// chunks, applies the stop rules and calls on_token.
+// the GPU: runs of consecutive positions, each one launch of the persistent decode kernel (one captured
+// graph per position where the persistent grid is not available). The host only feeds prompt ids, reads
+// back the chosen ids per run, applies the stop rules and calls on_token.
 #include <math.h>
 #include <stdio.h>
 #include <stddef.h>
