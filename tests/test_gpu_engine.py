@@ -248,6 +248,28 @@ def test_head_shapes_match_oracle(oracle, models, monkeypatch, cfg, dtype):
     np.testing.assert_array_equal(out["1"][1], out["0"][1])
 
 
+ONE = A.Config("one", dim=128, n_layers=1, n_heads=4, n_kv_heads=2, ffn_dim=256, vocab=512, ctx=160, dtype="q8_0")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "q8_0", "q4_0", "mxfp4"])
+def test_one_layer_model(oracle, models, monkeypatch, dtype):
+    """A one-layer model, whose only layer is both the first (the embedding row) and the last (partials
+    stored through for the head): 140 greedy tokens, across a launch boundary, equal the oracle's, and the
+    persistent kernel equals the one-graph-per-step path bit for bit."""
+    path = models.get(ONE, dtype, seed=3, std=0.08, norm_jitter=0.2)
+    ids = A.prompt(3, ONE.vocab, 5)
+    want = oracle.load(path).generate(ids, 140)
+    out = {}
+    for persist in ("1", "0"):
+        monkeypatch.setenv("L3M_PERSIST", persist)
+        with A.Model(path) as m:
+            assert m.persistent == (persist == "1")
+            out[persist] = (m.generate(ids, 140), m.logits)
+    assert out["1"][0] == want
+    assert out["0"][0] == want
+    np.testing.assert_array_equal(out["1"][1], out["0"][1])
+
+
 def test_mxfp4_native_blocks(oracle, models, monkeypatch):
     """An mxfp4 body run on its own e2m1 blocks (L3M_WIDEN=0; otherwise blocks that widen exactly run as
     q8_0): its tokens and last logits vs the oracle, and the same tokens as the widened run."""
