@@ -255,7 +255,9 @@ ONE = A.Config("one", dim=128, n_layers=1, n_heads=4, n_kv_heads=2, ffn_dim=256,
 def test_one_layer_model(oracle, models, monkeypatch, dtype):
     """A one-layer model, whose only layer is both the first (the embedding row) and the last (partials
     stored through for the head): 140 greedy tokens, across a launch boundary, equal the oracle's, and the
-    persistent kernel equals the one-graph-per-step path bit for bit."""
+    persistent kernel equals the one-graph-per-step path bit for bit; in the int8 dtypes a 30-token prompt
+    through the batched prefill (whose only layer is then its last, K/V rows alone) gives the oracle's 40
+    tokens too."""
     path = models.get(ONE, dtype, seed=3, std=0.08, norm_jitter=0.2)
     ids = A.prompt(3, ONE.vocab, 5)
     want = oracle.load(path).generate(ids, 140)
@@ -268,6 +270,13 @@ def test_one_layer_model(oracle, models, monkeypatch, dtype):
     assert out["1"][0] == want
     assert out["0"][0] == want
     np.testing.assert_array_equal(out["1"][1], out["0"][1])
+    if dtype in ("q8_0", "q4_0", "mxfp4"):                # a 30-token prompt through the batched prefill
+        monkeypatch.setenv("L3M_PERSIST", "1")
+        long_ids = A.prompt(4, ONE.vocab, 30)
+        want = oracle.load(path).generate(long_ids, 40)
+        with A.Model(path) as m:
+            assert m.generate(long_ids, 40) == want
+            assert m.prefilled == len(long_ids) - 1
 
 
 def test_mxfp4_native_blocks(oracle, models, monkeypatch):
