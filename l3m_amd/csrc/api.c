@@ -747,7 +747,7 @@ static int run_steps(l3m_model *m, const int32_t *prompt, int n_prompt, int max_
     memcpy(m->stage_tok, prompt, (size_t)n_prompt * 4);
     // the image was last read by the previous call's copies, which its final wait covered
     // a long prompt: positions 0..n_prompt-2 in one batched pass, then decode from the last prompt token
-    const int prefill = m->pf && n_prompt - 1 >= m->prefill_min && n_prompt - 1 >= 1;
+    const int prefill = m->pf && n_prompt >= m->prefill_min && n_prompt - 1 >= 1;
     int next = prefill ? n_prompt - 1 : 0;
     *m->stage_pos = next;
     long from = 0;                                     // the first run takes the call's inputs with it

@@ -4,9 +4,10 @@ A prompt of at least L3M_PREFILL_MIN (8) tokens runs its positions before the la
 that fills the K/V cache; decoding then starts at the last prompt token. The logits after the prompt
 must meet the engine bar of test_gpu_engine.py against the oracle (the reference's token-by-token order)
 and against the GPU's own token-by-token path (L3M_PREFILL=0): equal argmax, KL < 0.01 nats, max-abs
-within 2% of max|logit| (the int8 activation noise floor of the quantized paths). Prompts of 40 and 100
-tokens cover three and seven 16-token groups of the GEMM and one and two of the attention's 64-position
-chunks; head dims of 32 and 64 prepare the attention output inside the attention kernel, hd 48 in one of
+within 2% of max|logit| (the int8 activation noise floor of the quantized paths). Prompts of 8 (the
+threshold: 7 positions, less than one 16-token group of the GEMM), 9 and 17 (a group boundary), 40 and 100
+tokens cover one to seven 16-token groups of the GEMM, and 65 ends exactly at the attention's second
+64-position chunk; head dims of 32 and 64 prepare the attention output inside the attention kernel, hd 48 in one of
 its own. q4_0 and
 mxfp4 bodies run the same int8 GEMM on q8_0 copies of their matrices with the same values (an mxfp4 block's
 scale 2^(e-128) is an f16 and its doubled e2m1 codes are int8).
@@ -48,7 +49,7 @@ def close(a, b):
     return int(np.argmax(a)) == int(np.argmax(b)) and kl(b, a) < 0.01 and np.abs(a - b).max() <= 0.02 * np.abs(b).max()
 
 
-@pytest.mark.parametrize("n_prompt", [40, 100])
+@pytest.mark.parametrize("n_prompt", [8, 9, 17, 40, 65, 100])
 @pytest.mark.parametrize("cfg", [GQA, MHA, MX, HD48], ids=["q8_0-gqa", "q4_0-mha", "mxfp4-gqa", "q8_0-hd48"])
 def test_prefill_logits(models, oracle, monkeypatch, cfg, n_prompt):
     print(f"case {cfg.name} prompt {n_prompt}", flush=True)
