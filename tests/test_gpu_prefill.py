@@ -129,3 +129,39 @@ def test_prefill_graph_replays_equal_loose_launches(models, monkeypatch):
                 kg, vg = graph.kv_rows(layer, kvh, 0, n_prompt - 1, hd)
                 kl_, vl = loose.kv_rows(layer, kvh, 0, n_prompt - 1, hd)
                 assert np.array_equal(kg, kl_) and np.array_equal(vg, vl), (i, layer, kvh)
+
+
+LONG = A.Config("pf_long", dim=128, n_layers=2, n_heads=4, n_kv_heads=2, ffn_dim=256, vocab=512, ctx=256, dtype="q8_0")
+
+
+def test_prefill_past_128_positions(models, oracle, monkeypatch):
+    """A 200-token prompt at ctx 256: 199 prefilled positions, past the 128-slot logits ring and over four of
+    the attention's 64-position chunks. The logits after the prompt meet the engine bar against the oracle
+    and the GPU's token-by-token path, and each of the 30 greedy tokens that follow is the oracle's argmax
+    given the same prefix (its second at a near-tie)."""
+    path = models.get(LONG, "q8_0", seed=3, std=0.08, norm_jitter=0.2)
+    ids = A.prompt(7, LONG.vocab, 200)
+    om = oracle.load(path, ctx=256)
+    om.generate(ids, 0)
+    lo = om.logits()
+    with A.Model(path, ctx=256) as m:
+        m.generate(ids, 0)
+        assert m.prefilled == 199
+        lf = m.logits
+        got = m.generate(ids, 30)
+    om2, seq = oracle.load(path, ctx=256), list(ids) + got
+    for p in range(len(ids) - 1):
+        om2.forward(seq[p], p, logits=False)
+    for k in range(len(got)):
+        pos = len(ids) - 1 + k
+        lg = om2.forward(seq[pos], pos).astype(np.float64)
+        order, lv = np.argsort(-lg, kind="stable"), np.sort(lg)
+        tie = (lv[-1] - lv[-2]) / np.abs(lv).max() < 0.005
+        assert got[k] == order[0] or (tie and got[k] == order[1]), (k, got[k], order[:2])
+    monkeypatch.setenv("L3M_PREFILL", "0")
+    with A.Model(path, ctx=256) as m:
+        m.generate(ids, 0)
+        assert m.prefilled == 0
+        ls = m.logits
+    assert close(lf, lo), (kl(lo, lf), np.abs(lf - lo).max() / np.abs(lo).max())
+    assert close(lf, ls)
