@@ -93,3 +93,23 @@ def test_seed_repeats_and_greedy_is_unchanged(models):
     a = m.generate(ids, 40, temperature=0.9, seed=5)
     assert m.generate(ids, 40, temperature=0.9, seed=5) == a
     assert m.generate(ids, 40) == greedy              # the sampled calls leave no state behind
+
+
+@pytest.mark.parametrize("persist", ["1", "0"])
+def test_extreme_temperatures(models, oracle, monkeypatch, persist):
+    """Temperatures far from 1 follow the reference's rules too: 1e-30 leaves weight only on the maximum
+    (every other exponent is below -16), 1e-3 nearly so, 1e3 and 1e30 spread the weight over the whole
+    vocabulary, and infinity makes every weight 1. The picks equal the oracle's from the GPU's logits."""
+    monkeypatch.setenv("L3M_PERSIST", persist)
+    path = models.get(CFG, "q8_0", seed=6, std=0.05)
+    m = A.Model(path)
+    ids = A.prompt(6, CFG.vocab, 5)
+    greedy = m.generate(ids, 24)
+    for temp in (1e-30, 1e-3, 1e3, 1e30, float("inf")):
+        print(f"case temperature {temp} persist={persist}", flush=True)
+        toks = check_against_oracle(m, oracle, ids, temp, 11, 24)
+        if temp == 1e-30:
+            assert toks == greedy
+        if temp >= 1e3:
+            assert len(set(toks)) > 12                  # spread over the vocabulary
+    m.close()
