@@ -279,6 +279,28 @@ def test_one_layer_model(oracle, models, monkeypatch, dtype):
             assert m.prefilled == len(long_ids) - 1
 
 
+def test_two_models_interleaved(models):
+    """Two models of different shapes and dtypes loaded at once, their generate calls interleaved (each
+    model keeps its own device state, call area and sync words; the library's stream and kernels are
+    shared): every call gives the tokens and logits the same call gives on a model loaded alone."""
+    a_path = models.get(SMALL, "q8_0", seed=3, std=0.08, norm_jitter=0.2)
+    b_path = models.get(MQA, "bf16", seed=5, std=0.08, norm_jitter=0.2)
+    a_ids, b_ids = A.prompt(3, SMALL.vocab, 5), A.prompt(5, MQA.vocab, 3)
+    solo = {}
+    for key, path, ids, n in (("a", a_path, a_ids, 60), ("b", b_path, b_ids, 150)):
+        with A.Model(path) as m:
+            solo[key] = (m.generate(ids, n), m.logits)
+    a, b = A.Model(a_path), A.Model(b_path)
+    assert a.persistent and b.persistent
+    for _ in range(2):
+        ta = a.generate(a_ids, 60)
+        tb = b.generate(b_ids, 150)
+        assert ta == solo["a"][0] and tb == solo["b"][0]
+        np.testing.assert_array_equal(a.logits, solo["a"][1])
+        np.testing.assert_array_equal(b.logits, solo["b"][1])
+    a.close(); b.close()
+
+
 def test_mxfp4_native_blocks(oracle, models, monkeypatch):
     """An mxfp4 body run on its own e2m1 blocks (L3M_WIDEN=0; otherwise blocks that widen exactly run as
     q8_0): its tokens and last logits vs the oracle, and the same tokens as the widened run."""
