@@ -98,3 +98,37 @@ def test_persistent_kernel_equals_graph_path(models, monkeypatch, arch, dtype):
         ids = A.prompt(30 + i, CFG.vocab, n_prompt)
         assert fast.generate(ids, n_new) == step.generate(ids, n_new), i
         assert np.array_equal(fast.logits, step.logits), i
+
+
+LONG = A.Config("g2long", dim=128, n_layers=2, n_heads=4, n_kv_heads=4, ffn_dim=512, vocab=512, ctx=300, dtype="q8_0")
+TIE = {"f32": 1e-4, "bf16": 0.01, "q8_0": 0.02, "q4_0": 0.02}
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "q8_0"])
+def test_gpt2_to_the_end_of_a_long_context(models, oracle, monkeypatch, dtype):
+    """GPT-2 greedy decoding to the end of a 300-position context (three launches of the persistent kernel,
+    learned position rows up to the last): teacher-forcing the oracle along the GPU's tokens, each is the
+    oracle's argmax, or its second where the oracle's top-2 margin is inside the dtype's rounding spread;
+    the one-graph-per-step path gives the same tokens and logits bit for bit."""
+    path = models.get(LONG, dtype, seed=5, std=0.06, norm_jitter=0.1, arch="gpt2")
+    ids = A.prompt(5, LONG.vocab, 5)
+    out = {}
+    for persist in ("1", "0"):
+        monkeypatch.setenv("L3M_PERSIST", persist)
+        with A.Model(path) as m:
+            assert m.persistent == (persist == "1") and m.ctx == 300
+            out[persist] = (m.generate(ids, 1000), m.logits)
+    got = out["1"][0]
+    assert len(got) == 300 - len(ids)
+    om, seq, bad = oracle.load(path), list(ids) + got, []
+    for pos in range(len(seq) - 1):
+        lg = om.forward(seq[pos], pos, logits=pos >= len(ids) - 1)
+        if lg is None:
+            continue
+        k = pos - (len(ids) - 1)
+        order = np.argsort(-lg.astype(np.float64), kind="stable")
+        if not (got[k] == order[0] or (margin(lg) < TIE[dtype] and got[k] == order[1])):
+            bad.append(k)
+    assert not bad, bad
+    assert out["0"][0] == got
+    np.testing.assert_array_equal(out["0"][1], out["1"][1])
