@@ -165,3 +165,21 @@ def test_prefill_past_128_positions(models, oracle, monkeypatch):
         ls = m.logits
     assert close(lf, lo), (kl(lo, lf), np.abs(lf - lo).max() / np.abs(lo).max())
     assert close(lf, ls)
+
+
+def test_prefill_graph_cache_replaces_the_oldest(models, monkeypatch):
+    """More prompt lengths than the eight captured graphs a model keeps: eleven lengths in turn, then the
+    first three again (each replaced since and captured anew) and the last (still kept). Every call's tokens
+    and logits equal the loose launches' bit for bit."""
+    path = models.get(GQA, GQA.dtype, seed=9, std=0.05, norm_jitter=0.1)
+    graph = A.Model(path)
+    monkeypatch.setenv("L3M_PREFILL_GRAPH", "0")
+    loose = A.Model(path)
+    lengths = list(range(10, 32, 2))
+    for i, n_prompt in enumerate(lengths + lengths[:3] + lengths[-1:]):
+        ids = A.prompt(40 + n_prompt, GQA.vocab, n_prompt)
+        got, want = graph.generate(ids, 2), loose.generate(ids, 2)
+        assert graph.prefilled == loose.prefilled == n_prompt - 1
+        assert got == want, (i, n_prompt)
+        assert np.array_equal(graph.logits, loose.logits), (i, n_prompt)
+    graph.close(); loose.close()
