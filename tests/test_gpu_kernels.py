@@ -252,13 +252,16 @@ def test_table_matches_reference_tables(reference, dtype):
         assert rel_err(y, want) < TOL[dtype], (k, rel_err(y, want))
 
 
-def test_table_attend_matches_reference(reference):
+@pytest.mark.parametrize("hd,pos,stride", [(64, 100, 128), (48, 0, 48), (32, 1, 96), (128, 511, 128), (64, 4000, 64)])
+def test_table_attend_matches_reference(reference, hd, pos, stride):
+    """The table's attend (kernels.h: one query head over rows 0..pos of K and V with a row stride) against
+    the reference's scalar table, 1e-5 absolute (tests/test_kernels.c:145): head dims 32 to 128, the first
+    position, the second, and 4,001 positions."""
     import ctypes as C
     import l3m_amd as A
     from oracle.oracle import _Table
     table = _Table.in_dll(A.lib(), "l3m_kernels_hip")
-    rng = np.random.default_rng(9)
-    hd, pos, stride = 64, 100, 128
+    rng = np.random.default_rng(9 + hd + pos)
     q = rng.standard_normal(hd).astype(np.float32)
     k = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBFFF
     v = rng.integers(0, 1 << 16, (pos + 1) * stride, dtype=np.uint16) & 0xBFFF
