@@ -65,6 +65,27 @@ def test_reference_cli_generate_matches_cpu_engine(cli, models):
     assert gpu.stdout == cpu.stdout                 # the prompt and 24 greedy tokens, as raw bytes
 
 
+def test_reference_cli_bench_on_gpu(cli, models):
+    """The reference CLI's `bench` (main.c:233-263) on the GPU library: its perf line for one model (the
+    description ends in "(hip)", then tok/s, us/tok and the compute/wait split of l3m_perf), and its
+    markdown table for two models, one row each."""
+    import re
+    a, b = models.get("stories110M", "q4_0"), models.get("stories15M", "bf16")
+    r = run(cli, "bench", a, "-n", "64")
+    out = r.stdout.decode(errors="replace")
+    assert r.returncode == 0, out
+    assert "(hip)" in out, out
+    m = re.search(r"([0-9]+) tok/s\s+([0-9.]+) us/tok\s+\(compute ([0-9.]+), wait ([0-9.]+)\)", out)
+    assert m, out
+    tok_s, us, compute, wait = (float(g) for g in m.groups())
+    assert tok_s > 1000 and abs(compute + wait - us) < 0.2 * us, out
+    r = run(cli, "bench", "--md", a, b, "-n", "32")
+    out = r.stdout.decode(errors="replace")
+    assert r.returncode == 0, out
+    rows = [line for line in out.splitlines() if line.startswith("| ") and "(hip)" in line]
+    assert len(rows) == 2, out
+
+
 TOL = {F32: 1e-3, BF16: 1e-3, Q8_0: 1e-3, Q4_0: 5e-3, MXFP4: 5e-3}
 
 
