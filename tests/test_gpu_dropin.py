@@ -65,6 +65,24 @@ def test_reference_cli_generate_matches_cpu_engine(cli, models):
     assert gpu.stdout == cpu.stdout                 # the prompt and 24 greedy tokens, as raw bytes
 
 
+def test_reference_cli_chat_matches_cpu_engine(cli, models):
+    """The reference CLI's `chat` (main.c:200-230: the conversation re-fed as text each turn) with two turns
+    piped in: the GPU library prints the same greedy replies as the same CLI on the reference's CPU engine."""
+    if not ON_CPU.exists():
+        pytest.skip("oracle/_ref/l3m missing")
+    path = models.get("stories15M", "bf16")
+    env = {k: v for k, v in os.environ.items() if k != "L3M_ISA"}
+    outs = []
+    for binary in (cli, ON_CPU):
+        r = subprocess.run([str(binary), "chat", str(path), "-n", "16", "-t", "0"], input=b"Once upon a time\nThe cat sat\n",
+                           capture_output=True, timeout=300, env=env)
+        print(r.stderr.decode(errors="replace")[-300:], flush=True)
+        assert r.returncode == 0
+        outs.append(r.stdout)
+    assert outs[0] == outs[1]
+    assert outs[0].count(b"> ") == 3                  # two turns answered, then the prompt for a third
+
+
 def test_reference_cli_bench_on_gpu(cli, models):
     """The reference CLI's `bench` (main.c:233-263) on the GPU library: its perf line for one model (the
     description ends in "(hip)", then tok/s, us/tok and the compute/wait split of l3m_perf), and its
