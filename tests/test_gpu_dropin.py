@@ -65,6 +65,20 @@ def test_reference_cli_generate_matches_cpu_engine(cli, models):
     assert gpu.stdout == cpu.stdout                 # the prompt and 24 greedy tokens, as raw bytes
 
 
+@pytest.mark.parametrize("extra", [("-t", "0.8", "-s", "7"), ("--ref",), ("--cold",)], ids=["sampled", "ref", "cold"])
+def test_reference_cli_generate_options(cli, models, extra):
+    """The CLI's `generate` with its other options (main.c:59-75) prints the same text on the GPU library as
+    on the reference's CPU engine: temperature sampling with a seed (the same draws from the same logits),
+    the fp32 reference path (--ref), and caches emptied before every forward pass (--cold)."""
+    if not ON_CPU.exists():
+        pytest.skip("oracle/_ref/l3m missing")
+    path = models.get("stories15M", "bf16")
+    args = ("generate", path, "-p", "Once upon a time", "-n", "24", *extra)
+    gpu, cpu = run(cli, *args), run(ON_CPU, *args)
+    assert gpu.returncode == 0 and cpu.returncode == 0
+    assert gpu.stdout == cpu.stdout
+
+
 def test_reference_cli_chat_matches_cpu_engine(cli, models):
     """The reference CLI's `chat` (main.c:200-230: the conversation re-fed as text each turn) with two turns
     piped in: the GPU library prints the same greedy replies as the same CLI on the reference's CPU engine."""
