@@ -113,3 +113,24 @@ def test_extreme_temperatures(models, oracle, monkeypatch, persist):
         if temp >= 1e3:
             assert len(set(toks)) > 12                  # spread over the vocabulary
     m.close()
+
+
+def test_sampled_streamed_after_a_prefilled_prompt(models, oracle):
+    """The three features together: a 40-token prompt through the batched prefill, temperature sampling on
+    the device, and tokens handed to on_token as they come, with a stop after 20. Every pick equals the
+    oracle's from the GPU's logits, and the stopped call's tokens are the first 20 of the same call without a
+    callback."""
+    path = models.get(CFG, "q8_0", seed=6, std=0.05)
+    m = A.Model(path)
+    ids = A.prompt(8, CFG.vocab, 40)
+    full = check_against_oracle(m, oracle, ids, 0.9, 3, 60)
+    assert m.prefilled == len(ids) - 1
+    seen = []
+    got = m.generate(ids, 60, temperature=0.9, seed=3, on_token=lambda t: seen.append(t) or len(seen) < 20)
+    assert m.prefilled == len(ids) - 1
+    assert got == seen == full[:20]
+    st = oracle.seed_state(3)
+    for k, tok in enumerate(got):
+        want, st = oracle.sample(m.logits_at(len(ids) - 1 + k), 0.9, st)
+        assert tok == want
+    m.close()
