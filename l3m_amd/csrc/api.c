@@ -580,7 +580,7 @@ l3m_model *l3m_load(const char *path, const l3m_opts *opts) {
         const char *pe = getenv("L3M_PERSIST");
         m->persist = (!pe || strcmp(pe, "0")) && l3m_decode_pair(d->body_dtype, d->head.dtype, gpt2) && d->n_groups <= 64 &&
                      d->n_chunks <= 64 && d->vocab <= 0x20000 && m->head_tpw <= 64 && m->lds_decode <= lds_max &&
-                     l3m_decode_fits(d->body_dtype, d->head.dtype, gpt2, m->grid, m->lds_decode);
+                     l3m_decode_fits(d->body_dtype, d->head.dtype, gpt2, d->hd, m->grid, m->lds_decode);
         int *xcc = m->persist ? calloc((size_t)m->grid, sizeof *xcc) : NULL;
         if (xcc && !l3m_decode_placement(m->grid, m->lds_decode, xcc)) {
             int count[16] = {0};
@@ -676,7 +676,7 @@ static int chunk_enqueue(l3m_model *m, int first, int last, int head_from, int s
         *m->run_host[slot] = r;
         const size_t end = m->call_slot[slot] + 256 + (size_t)L3M_SYNC_WORDS * 4;
         if (l3m_dev_upload_async(m->call_dev + from, m->call_host + from, end - (size_t)from) ||
-            l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, m->dm_dev, m->layers_dev, m->run_dev[slot], m->grid, m->lds_decode, NULL,
+            l3m_decode_launch(d->body_dtype, d->head.dtype, d->gpt2, d->hd, m->dm_dev, m->layers_dev, m->run_dev[slot], m->grid, m->lds_decode, NULL,
                               slot) ||
             l3m_dev_download_async(out, sync + L3M_SYNC_OUT, offsetof(l3m_chunk_out, tok) + (size_t)ntok * 4))
             return -1;

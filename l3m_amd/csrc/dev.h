@@ -181,11 +181,12 @@ int l3m_dev_cus(void);
 // (xcc[grid]); 0, or -1 on a device error.
 int l3m_decode_placement(int grid, unsigned lds, int *xcc);
 int l3m_decode_pair(int dtype, int head_dtype, int gpt2);    // 1 if the kernel is built for this (body, head, variant)
-int l3m_decode_fits(int dtype, int head_dtype, int gpt2, int grid, unsigned lds);   // 1 if grid workgroups with lds bytes can all be resident
+// hd: the model's head dimension (the kernel built for it as a constant when there is one, else the general one)
+int l3m_decode_fits(int dtype, int head_dtype, int gpt2, int hd, int grid, unsigned lds);   // 1 if grid workgroups with lds bytes can all be resident
 // m_dev, layers_dev, r_dev: device-memory copies (the kernel reads its parameters from there)
 // slot (0 or 1): which of the two launches that may be in flight at once this is (its timing events).
-int l3m_decode_launch(int dtype, int head_dtype, int gpt2, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev, int grid,
-                      unsigned lds, void *stream, int slot);
+int l3m_decode_launch(int dtype, int head_dtype, int gpt2, int hd, const l3m_dmodel *m_dev, const l3m_dlayer *layers_dev, const l3m_run *r_dev,
+                      int grid, unsigned lds, void *stream, int slot);
 // Adds slot's finished launch to l3m_decode_timer's total (after its stream work has been waited for).
 int l3m_decode_timer_collect(int slot);
 // Stream-ordered transfers and events on the library stream, for work kept in flight: a copy into pinned
