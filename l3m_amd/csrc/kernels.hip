@@ -110,6 +110,12 @@ __device__ __forceinline__ uint32_t ldg1_if(const void *p, size_t i, bool ok) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(buf(p), ok ? (uint32_t)i : OOB, 0, 0);
 }
 template <bool COH> __device__ __forceinline__ uint4 ld16(const void *p, size_t i) { return COH ? ldcoh16(p, i) : ldg16(p, i); }
+// Element i of a uniform base p, or zeros with no memory access when ok is false (the offset past the
+// buffer's range): a load that needs no branch around it.
+template <bool COH> __device__ __forceinline__ float4 ld16f_if(const void *p, size_t i, bool ok) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(buf(p), ok ? (uint32_t)(16 * i) : OOB, 0, COH ? SC1 : 0));
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
 template <bool COH> __device__ __forceinline__ float4 ld16f(const void *p, size_t i) {
     if constexpr (COH) {
         const uint4 u = ldcoh16(p, i);
@@ -1192,12 +1198,8 @@ __device__ __forceinline__ void pro_load(Pro &P, const float *base, const float 
     if (wave * 64 < G.n4) P.base = ld16f<COH>(base, f);
     if (wave * 64 < G.groups * G.n4) {
 #pragma unroll
-        for (int j = 0; j < FILL_PER; j++) {
-            if (j < G.per) {
-                const int pj = j0 + j < nparts ? j0 + j : nparts - 1;
-                P.p[j] = ld16f<COH>(parts, (size_t)pj * (dim >> 2) + f);
-            }
-        }
+        for (int j = 0; j < FILL_PER; j++)
+            P.p[j] = ld16f_if<COH>(parts, (size_t)(j0 + j) * (dim >> 2) + f, j < G.per && j0 + j < nparts);
     }
     if (use_embed) P.emb = lt_elem4(embed, tok, 4 * own);   // layer 0: x = dequant(embed[tok]) (engine.c:236)
     asm volatile("" ::: "memory");                            // these loads are issued before the weights
@@ -1219,10 +1221,7 @@ __device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, const P
         if (grp < G.groups) {
             float4 v = grp == 0 ? P.base : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int j = 0; j < FILL_PER; j++) {
-                const bool use = j < G.per && j0 + j < nparts;
-                v.x += use ? P.p[j].x : 0.f; v.y += use ? P.p[j].y : 0.f; v.z += use ? P.p[j].z : 0.f; v.w += use ? P.p[j].w : 0.f;
-            }
+            for (int j = 0; j < FILL_PER; j++) { v.x += P.p[j].x; v.y += P.p[j].y; v.z += P.p[j].z; v.w += P.p[j].w; }
             for (int j = FILL_PER; j < G.per && j0 + j < nparts; j++) {   // beyond one batch: in order
                 const float4 p = ld16f<COH>(parts, (size_t)(j0 + j) * (dim >> 2) + f);
                 v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
@@ -1239,8 +1238,10 @@ __device__ __forceinline__ float4 pro_finish(Pro &P, const float *parts, const P
 #pragma unroll
                     for (int u = 0; u < 4; u++) p[u] = pbuf[(g0 + u < G.groups ? g0 + u : G.groups - 1) * G.n4 + tid];
 #pragma unroll
-                    for (int u = 0; u < 4; u++)
-                        if (g0 + u < G.groups) { x.x += p[u].x; x.y += p[u].y; x.z += p[u].z; x.w += p[u].w; }
+                    for (int u = 0; u < 4; u++) {
+                        const bool in = g0 + u < G.groups;
+                        x.x += in ? p[u].x : 0.f; x.y += in ? p[u].y : 0.f; x.z += in ? p[u].z : 0.f; x.w += in ? p[u].w : 0.f;
+                    }
                 }
             }
         }
